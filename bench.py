@@ -1,0 +1,320 @@
+#!/usr/bin/env python3
+"""Benchmark of Flash Deformable 3D Attention forward+backward on one MI355X.
+
+Default workload: c4, the headline configuration -- bf16 self-attention over a 256x512x2048
+volume at strides 16/32 (levels (16,32,128) and (8,16,64), S = Q = 73728), B=1, G=8, D=32,
+L=2, K=4, synthetic seeded inputs (value N(0,1), locations U(0,1), logits N(0,1), upstream
+grad N(0,1)), all resident in HBM before timing.
+
+A step is one forward + backward through FlashDeformAttnFunction (autograd), over one batch.
+W untimed warmup steps, then K timed steps bracketed by torch.cuda.synchronize(); HIP events
+on the launch stream give per-step times (median / p10 / p90) and, in separate loops, the
+average duration of each kernel launch (forward kernel; backward kernel via the
+accumulate-only entry point).
+
+  value    = fwd+bwd algorithmic bytes / ms_per_step (GB/s).  Algorithmic bytes count each
+             tensor once at its API dtype: fwd reads value + sampling_loc_attn and writes the
+             output; bwd reads value + sampling_loc_attn + grad_output and writes grad_value +
+             grad_sampling_loc_attn.
+  roofline = the same figure for the dominant kernel alone, against 8 TB/s HBM3E peak.
+  cpu_baseline = the PyTorch restatement of the reference's naive path (oracle/torch_port.py:
+             grid_sample + softmax + autograd) in fp32 on the host CPU, on a query slice,
+             scaled linearly to the full query count.
+
+--all prints a per-configuration table (c1..c5, plus fp16 and fp32 forward at c5) to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "fwd+bwd ms & achieved HBM GB/s (% of peak), bf16 self-attn S=73728, 1 GPU"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def pct(xs, p):
+    xs = sorted(xs)
+    k = (len(xs) - 1) * p / 100.0
+    lo, hi = int(k), min(int(k) + 1, len(xs) - 1)
+    return xs[lo] + (xs[hi] - xs[lo]) * (k - lo)
+
+
+def _traffic_from_profiles(kernel: str, workload: str):
+    """HBM bytes per dispatch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled
+    by a copy-kernel calibration), read from profiles/pmc_<kernel>_<workload>.md."""
+    path = os.path.join(ROOT, "profiles", f"pmc_{kernel}_{workload}.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"hbm_bytes_per_dispatch:\s*([0-9.eE+]+)", open(path).read())
+    return float(m.group(1)) if m else None
+
+
+class Bench:
+    def __init__(self, w, dtype, device, seed=0):
+        import torch
+
+        from ops3d_amd.workloads import make_inputs
+
+        self.torch = torch
+        self.w = w
+        self.dtype = dtype
+        self.dev = device
+        inp = make_inputs(w, seed=seed, dtype=dtype, device=device)
+        self.inp = inp
+        self.value = inp["value"].requires_grad_(True)
+        self.sla = inp["sampling_loc_attn"].requires_grad_(True)
+        self.go = inp["grad_output"]
+        self.st = inp["spatial_shapes"]
+        self.lsi = inp["level_start_index"]
+        self.esize = self.value.element_size()
+
+    def step(self):
+        from ops3d_amd import FlashDeformAttnFunction
+
+        self.value.grad = None
+        self.sla.grad = None
+        out = FlashDeformAttnFunction.apply(self.value, self.st, self.lsi, self.sla, 64, self.w.K, True)
+        out.backward(self.go)
+
+    def fwd(self):
+        from ops3d_amd import FlashDeformAttnFunction
+
+        with self.torch.no_grad():
+            FlashDeformAttnFunction.apply(self.value, self.st, self.lsi, self.sla, 64, self.w.K, True)
+
+    def time_loop(self, fn, steps, warmup):
+        torch = self.torch
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        t0 = time.perf_counter()
+        for a, b in evs:
+            a.record()
+            fn()
+            b.record()
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e3
+        ms = [a.elapsed_time(b) for a, b in evs]
+        return {"total_ms": sum(ms), "wall_ms": wall, "median": statistics.median(ms),
+                "p10": pct(ms, 10), "p90": pct(ms, 90), "mean": sum(ms) / len(ms)}
+
+    def kernel_times(self, steps, warmup):
+        """Average launch duration (ms) of the forward kernel and of the backward kernel."""
+        from ops3d_amd import _C
+
+        torch = self.torch
+        v, s = self.value.detach(), self.sla.detach()
+        acc = torch.zeros(v.shape, dtype=torch.float32, device=self.dev)
+
+        def fk():
+            _C.flash_deform_attn_forward(v, self.st, self.lsi, s, 64, self.w.K)
+
+        def bk():
+            _C.flash_deform_attn_backward_accumulate(v, self.st, self.lsi, s, self.go, acc, 64, self.w.K)
+
+        return self.time_loop(fk, steps, warmup), self.time_loop(bk, steps, warmup)
+
+
+def measure(w, dtype, steps, warmup, device, with_kernels=True, fwd_only=False):
+    b = Bench(w, dtype, device)
+    res = {"workload": w.name, "dtype": dtype}
+    by = w.algorithmic_bytes(b.esize)
+    res["bytes"] = by
+    res["fwd"] = b.time_loop(b.fwd, steps, warmup)
+    if not fwd_only:
+        res["step"] = b.time_loop(b.step, steps, warmup)
+    if with_kernels:
+        fk, bk = b.kernel_times(steps, warmup)
+        res["fwd_kernel"], res["bwd_kernel"] = fk, bk
+    del b
+    import torch
+
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline(w, target_s=4.0, reps=3):
+    """fp32 PyTorch naive path on the host CPU, fwd+bwd over a query slice of `w`."""
+    import torch
+
+    from oracle import torch_port
+    from ops3d_amd.workloads import make_inputs
+
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        cores = min(cores, int(os.environ["OMP_NUM_THREADS"]))
+    torch.set_num_threads(cores)
+    nq = min(w.nq, 1024)
+    while True:
+        inp = make_inputs(w, seed=0, dtype="fp32", device="cpu", q_limit=nq)
+        t0 = time.perf_counter()
+        torch_port.forward_backward(inp["value"], inp["shapes"], inp["sampling_loc_attn"], inp["grad_output"], w.K)
+        dt = time.perf_counter() - t0
+        if dt >= target_s / 4 or nq >= w.nq:
+            break
+        nq = min(w.nq, nq * max(2, int(target_s / 4 / max(dt, 1e-3))))
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        torch_port.forward_backward(inp["value"], inp["shapes"], inp["sampling_loc_attn"], inp["grad_output"], w.K)
+        ts.append(time.perf_counter() - t0)
+    t = statistics.median(ts)
+    t_full = t * w.nq / nq
+    by = w.algorithmic_bytes(2 if w.dtype in ("bf16", "fp16") else 4)["total"]
+    cpu = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(by / t_full / 1e9, 4),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"oracle/torch_port fp32 fwd+bwd (grid_sample+softmax+autograd) on {nq} of {w.nq} "
+                   f"queries of {w.name}, median of {reps}, {t:.2f} s per rep, scaled linearly to the full "
+                   f"query count ({t_full * 1e3:.0f} ms extrapolated); CPU: {cpu}"),
+        "ms_extrapolated": round(t_full * 1e3, 1),
+    }
+
+
+def summary_line(r):
+    by = r["bytes"]
+    f = r["fwd"]["median"]
+    s = r.get("step", {}).get("median")
+    fk = r.get("fwd_kernel", {}).get("mean")
+    bk = r.get("bwd_kernel", {}).get("mean")
+    samples = r["samples"]
+    parts = [f"{r['workload']:>3} {r['dtype']:>4}", f"fwd {f * 1e3:8.1f} us ({by['fwd'] / f / 1e6:7.0f} GB/s, "
+             f"{100 * by['fwd'] / f / 1e6 / HBM_PEAK_GBS:5.1f}%)"]
+    if s:
+        parts.append(f"fwd+bwd {s * 1e3:8.1f} us ({by['total'] / s / 1e6:7.0f} GB/s, "
+                     f"{100 * by['total'] / s / 1e6 / HBM_PEAK_GBS:5.1f}%)")
+    if fk:
+        parts.append(f"k_fwd {fk * 1e3:7.1f} us")
+    if bk:
+        parts.append(f"k_bwd {bk * 1e3:7.1f} us")
+    parts.append(f"{samples / (s or f) / 1e6:.3g} Gsamples/s" if (s or f) else "")
+    return " | ".join(parts)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c4")
+    ap.add_argument("--all", action="store_true", help="also report every configuration (stderr)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--json-out", default=None, help="write all results as JSON to this path")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported: this build runs on one GPU only "
+              f"(the flash-deform-attn path has no multi-GPU mode); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import ops3d_amd
+    from ops3d_amd.workloads import WORKLOADS
+
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        sys.exit(1)
+    if ops3d_amd._C is None:
+        print("bench.py: libops3d_fda.so is not built (run __graft_entry__.build())", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    log(f"device: {torch.cuda.get_device_name(0)}; torch {torch.__version__}")
+
+    results = []
+    if args.all:
+        plan = [(n, WORKLOADS[n].dtype, False) for n in ("c1", "c2", "c3", "c4", "c5")]
+        plan += [("c5", "fp16", True), ("c5", "fp32", True)]
+        for name, dt, fo in plan:
+            w = WORKLOADS[name]
+            log(f"[bench] {name} {dt} fwd_only={fo}")
+            r = measure(w, dt, args.steps, args.warmup, dev, fwd_only=fo)
+            r["samples"] = w.samples()
+            results.append(r)
+            log(summary_line(r))
+
+    w = WORKLOADS[args.config]
+    log(f"[bench] headline {w.name} {w.dtype} steps={args.steps} warmup={args.warmup}")
+    r = measure(w, w.dtype, args.steps, args.warmup, dev)
+    r["samples"] = w.samples()
+    log(summary_line(r))
+    by = r["bytes"]
+    ms_step = r["step"]["total_ms"] / args.steps
+    kf, kb = r["fwd_kernel"]["mean"], r["bwd_kernel"]["mean"]
+    dominant, kms, kbytes = ("fda_backward_kernel", kb, by["bwd"]) if kb >= kf else ("fda_forward_kernel", kf, by["fwd"])
+    achieved = kbytes / (kms * 1e-3) / 1e9
+    traffic = _traffic_from_profiles(dominant, w.name)
+    line = {
+        "metric": METRIC,
+        "value": round(by["total"] / (ms_step * 1e-3) / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if w.dtype == "bf16" else w.dtype,
+        "data": "synthetic (seeded: value N(0,1), locations U(0,1), logits N(0,1), grad N(0,1))",
+        "config": {
+            "workload": f"{w.name}: {w.mode}-attention, levels {list(w.shapes)}, S={w.S}, B={w.B}, "
+                        f"Q={w.nq}, G={w.G}, D={w.D}, L={w.L}, K={w.K}, fwd+bwd",
+            "B": w.B, "Q": w.nq, "S": w.S, "G": w.G, "D": w.D, "L": w.L, "K": w.K,
+        },
+        "fwd_bwd_ms_median": round(r["step"]["median"], 5),
+        "fwd_bwd_ms_p10": round(r["step"]["p10"], 5),
+        "fwd_bwd_ms_p90": round(r["step"]["p90"], 5),
+        "fwd_ms_median": round(r["fwd"]["median"], 5),
+        "frac_of_hbm_peak": round(by["total"] / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "qhs_per_s": round(w.samples() / (ms_step * 1e-3), 1),
+        "kernels_us": {"fda_forward_kernel": round(kf * 1e3, 2), "fda_backward_kernel": round(kb * 1e3, 2)},
+        "roofline": {
+            "kernel": dominant,
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes": kbytes,
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        log("[bench] cpu baseline")
+        line["cpu_baseline"] = cpu_baseline(w)
+    if args.json_out:
+        with open(args.json_out, "w") as f:
+            json.dump({"headline": line, "configs": results + [r]}, f, indent=1, default=str)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,112 @@
+/*
+ * ops3d_fda.h -- C ABI of the MI355X (gfx950) Flash Deformable 3D Attention library
+ * (libops3d_fda.so).
+ *
+ * Plain pointers and sizes only; no torch or HIP types in the signatures.  Every device
+ * pointer must point to memory on the current HIP device; `stream` is a hipStream_t (or NULL
+ * for the null stream).  All entry points are asynchronous with respect to the host: they
+ * enqueue kernels on `stream` and return.  Validation errors are reported synchronously.
+ *
+ * Tensor layouts (all C-contiguous, identical to the reference's):
+ *   value                [B, S, G, D]      dtype
+ *   spatial_shapes       [L, 3] int64      rows (D_l, H_l, W_l), DEVICE memory (read by kernels)
+ *   level_start_index    [L]    int64      exclusive prefix sum of D_l*H_l*W_l, DEVICE memory
+ *   sampling_loc_attn    [B, Q, G, P]      dtype, P = L*K*3 + L*K, per (b,q,g) planar:
+ *                                          L*K (x,y,z) triples (level-major, point-minor),
+ *                                          then L*K raw attention logits
+ *   output / grad_output [B, Q, G*D]       dtype
+ *   grad_value           [B, S, G, D]      dtype
+ *   grad_sampling_loc_attn [B, Q, G, P]    dtype (logit part already through softmax backward)
+ *
+ * Return codes: OPS3D_FDA_OK, OPS3D_FDA_EINVAL (bad argument; a Python binding raises
+ * ValueError, as the reference's std::invalid_argument does through pybind), OPS3D_FDA_ERUNTIME
+ * (assertion-type error or HIP failure; RuntimeError).  ops3d_fda_last_error() returns the
+ * message of the last failure on the calling thread.
+ */
+#ifndef OPS3D_FDA_H
+#define OPS3D_FDA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifndef OPS3D_FDA_API
+#define OPS3D_FDA_API __attribute__((visibility("default")))
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { OPS3D_FDA_F32 = 0, OPS3D_FDA_F16 = 1, OPS3D_FDA_BF16 = 2 };
+enum { OPS3D_FDA_OK = 0, OPS3D_FDA_EINVAL = 1, OPS3D_FDA_ERUNTIME = 2 };
+
+/* ABI version of this header (bumped on any signature change). */
+OPS3D_FDA_API int ops3d_fda_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+OPS3D_FDA_API const char *ops3d_fda_last_error(void);
+
+/* 1 if (dtype, channels D) has a compiled kernel configuration, else 0. */
+OPS3D_FDA_API int ops3d_fda_supported(int dtype, int channels);
+
+/*
+ * Forward.  Replaces flash_deform_attn_forward (reference csrc/flash_deform_attn.h:7-25 ->
+ * csrc/cuda/flash_deform_attn_cuda.cu:20-91).  Writes every element of `output`
+ * ([B,Q,G*D], dtype), so the caller need not zero it.  The softmax over the L*K logits of each
+ * (b,q,g) is computed in fp32 inside the kernel; trilinear sampling uses zero padding and
+ * align_corners=False pixel coordinates (loc*size - 0.5).
+ *   im2col_step: batch chunk size of the reference; min(batch, im2col_step) must divide batch
+ *                (else OPS3D_FDA_ERUNTIME, as reference flash_deform_attn_cuda.cu:56-58).  Results
+ *                do not depend on it.
+ *   num_levels must be 1..5 and num_point 1..16 (else OPS3D_FDA_EINVAL).
+ */
+OPS3D_FDA_API int ops3d_fda_forward(const void *value, const int64_t *spatial_shapes,
+                      const int64_t *level_start_index, const void *sampling_loc_attn,
+                      void *output, int dtype, int batch, int spatial_size, int num_heads,
+                      int channels, int num_levels, int num_query, int num_point,
+                      int im2col_step, void *stream);
+
+/*
+ * Bytes of device workspace ops3d_fda_backward needs: an fp32 [B,S,G,D] accumulator for
+ * grad_value when dtype is f16/bf16, 0 for f32 (the fp32 output is accumulated in place).
+ */
+OPS3D_FDA_API size_t ops3d_fda_backward_workspace_bytes(int dtype, int batch, int spatial_size,
+                                          int num_heads, int channels);
+
+/*
+ * Backward.  Replaces flash_deform_attn_backward (reference csrc/flash_deform_attn.h:27-52 ->
+ * csrc/cuda/flash_deform_attn_cuda.cu:93-179).  Writes every element of grad_value and
+ * grad_sampling_loc_attn in `dtype` (the caller need not zero them).  grad_value is accumulated
+ * in fp32 (in `workspace`, at least ops3d_fda_backward_workspace_bytes() bytes, or in place
+ * for f32) and converted once at the end.  Samples whose pixel coordinate lies outside
+ * [-1, size) on any axis contribute nothing and get zero location gradients.
+ */
+OPS3D_FDA_API int ops3d_fda_backward(const void *value, const int64_t *spatial_shapes,
+                       const int64_t *level_start_index, const void *sampling_loc_attn,
+                       const void *grad_output, void *grad_value,
+                       void *grad_sampling_loc_attn, void *workspace, size_t workspace_bytes,
+                       int dtype, int batch, int spatial_size, int num_heads, int channels,
+                       int num_levels, int num_query, int num_point, int im2col_step,
+                       void *stream);
+
+/*
+ * Backward kernel only, accumulating into a caller-owned fp32 grad_value buffer
+ * ([B,S,G,D] fp32, NOT cleared: contributions are added to what it holds).
+ * grad_sampling_loc_attn is written in full in `dtype`.  No counterpart in the reference
+ * (its backward always zero-fills an fp32 buffer and casts it, flash_deform_attn_cuda.cu:
+ * 139-178); for callers that sum grad_value over several calls (micro-batches, several
+ * query sets attending the same value) or that want fp32 value gradients, and for timing
+ * the backward kernel alone.  Atomics make the summation order, hence the last bits of
+ * grad_value, nondeterministic.
+ */
+OPS3D_FDA_API int ops3d_fda_backward_accumulate_f32(
+    const void *value, const int64_t *spatial_shapes, const int64_t *level_start_index,
+    const void *sampling_loc_attn, const void *grad_output, float *grad_value_f32,
+    void *grad_sampling_loc_attn, int dtype, int batch, int spatial_size, int num_heads,
+    int channels, int num_levels, int num_query, int num_point, int im2col_step, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OPS3D_FDA_H */

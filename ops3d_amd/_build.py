@@ -1,0 +1,76 @@
+"""Build libops3d_fda.so (the gfx950 HIP kernels + C ABI) in-tree with hipcc.
+
+gfx950 only, no hipify, no CUDA headers.  Sources are compiled in parallel, then linked with
+hipcc.  Used by ``setup.py`` and ``__graft_entry__.build()``; also runnable as
+``python -m ops3d_amd._build``.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(PKG_DIR, "csrc")
+LIB_NAME = "libops3d_fda.so"
+LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
+SOURCES = ["fda_capi.hip", "fda_f32.hip", "fda_f16.hip", "fda_bf16.hip"]
+ARCH = "gfx950"
+
+# -packed-fp32-ops off: hipcc must not form v_pk_{add,mul,fma}_f32 on its own.
+# -munsafe-fp-atomics: fp32 atomics lower to the hardware add (no CAS loop); all our atomics
+# target coarse-grained device memory, where that is exact.
+HIP_FLAGS = [
+    "-std=c++17",
+    "-O3",
+    f"--offload-arch={ARCH}",
+    "-mcode-object-version=5",
+    "-fPIC",
+    "-fvisibility=hidden",
+    "-munsafe-fp-atomics",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+]
+
+
+def _hipcc() -> str:
+    cand = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(cand):
+        raise RuntimeError("hipcc not found; the ops3d_amd kernels need ROCm's hipcc")
+    return cand
+
+
+def _run(cmd: list[str]) -> None:
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass warns that it does not know the packed-fp32 feature: harmless
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
+    if res.returncode != 0:
+        raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}\n{err}")
+    if err.strip():
+        sys.stderr.write(err + "\n")
+
+
+def build(out_path: str = LIB_PATH, build_dir: str | None = None) -> str:
+    """Compile every source for gfx950 and link ``libops3d_fda.so``; return its path."""
+    hipcc = _hipcc()
+    build_dir = build_dir or os.path.join(PKG_DIR, "_build")
+    os.makedirs(build_dir, exist_ok=True)
+    objs = []
+    cmds = []
+    for src in SOURCES:
+        obj = os.path.join(build_dir, src.replace(".hip", ".o"))
+        objs.append(obj)
+        cmds.append([hipcc, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+    with ThreadPoolExecutor(max_workers=min(len(cmds), os.cpu_count() or 1)) as ex:
+        list(ex.map(_run, cmds))
+    tmp = out_path + ".tmp"
+    _run([hipcc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp])
+    os.replace(tmp, out_path)
+    return out_path
+
+
+if __name__ == "__main__":
+    print(build())

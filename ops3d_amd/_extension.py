@@ -1,0 +1,227 @@
+"""Load libops3d_fda.so and expose it as ``_C``, the extension-module object of the package.
+
+Mirrors the reference's loader contract (ops3d/_extension.py:13-55): importing the package
+never fails; when the native library cannot be loaded, ``_C`` is ``None`` and
+``FlashDeformAttnFunction`` raises ``RuntimeError`` (reference ops3d/flash_deform_attn.py:78-79).
+There is no fallback implementation.
+
+``_C.flash_deform_attn_forward`` / ``_C.flash_deform_attn_backward`` keep the argument lists
+of the reference's pybind entry points (csrc/vision.cpp:23-24, csrc/flash_deform_attn.h:7-52).
+They check what only the tensors know (device, dtype, contiguity, ranks), allocate outputs and
+the fp32 workspace with torch, and call the C ABI (include/ops3d_fda.h) on torch's current
+HIP stream.  Everything else (L/K/D limits, im2col_step divisibility, launch geometry) is
+checked by the C library.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # imported first: its HIP runtime is the one libops3d_fda.so binds to
+
+_PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG_DIR, "libops3d_fda.so")
+
+OPS3D_FDA_OK, OPS3D_FDA_EINVAL, OPS3D_FDA_ERUNTIME = 0, 1, 2
+_DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+_vp, _i, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+
+EXPORTED_SYMBOLS = (
+    "ops3d_fda_abi_version",
+    "ops3d_fda_last_error",
+    "ops3d_fda_supported",
+    "ops3d_fda_forward",
+    "ops3d_fda_backward_workspace_bytes",
+    "ops3d_fda_backward",
+    "ops3d_fda_backward_accumulate_f32",
+)
+
+
+def _declare(lib: ctypes.CDLL) -> None:
+    lib.ops3d_fda_abi_version.restype = _i
+    lib.ops3d_fda_abi_version.argtypes = []
+    lib.ops3d_fda_last_error.restype = ctypes.c_char_p
+    lib.ops3d_fda_last_error.argtypes = []
+    lib.ops3d_fda_supported.restype = _i
+    lib.ops3d_fda_supported.argtypes = [_i, _i]
+    lib.ops3d_fda_forward.restype = _i
+    lib.ops3d_fda_forward.argtypes = [_vp, _vp, _vp, _vp, _vp] + [_i] * 9 + [_vp]
+    lib.ops3d_fda_backward_workspace_bytes.restype = _sz
+    lib.ops3d_fda_backward_workspace_bytes.argtypes = [_i] * 5
+    lib.ops3d_fda_backward.restype = _i
+    lib.ops3d_fda_backward.argtypes = [_vp] * 8 + [_sz] + [_i] * 9 + [_vp]
+    lib.ops3d_fda_backward_accumulate_f32.restype = _i
+    lib.ops3d_fda_backward_accumulate_f32.argtypes = [_vp] * 7 + [_i] * 9 + [_vp]
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return t.data_ptr() if (t is not None and t.numel() > 0) else None
+
+
+class _NativeFDA:
+    """Host side of the flash-deform-attn extension, bound to libops3d_fda.so."""
+
+    ABI_VERSION = 1
+
+    def __init__(self, lib: ctypes.CDLL, path: str):
+        self._lib = lib
+        self.__file__ = path
+        ver = lib.ops3d_fda_abi_version()
+        if ver != self.ABI_VERSION:
+            raise ImportError(f"{path}: ABI version {ver}, expected {self.ABI_VERSION}")
+
+    # -- helpers ---------------------------------------------------------------------------
+    def _raise(self, rc: int, what: str) -> None:
+        msg = self._lib.ops3d_fda_last_error().decode(errors="replace") or what
+        if rc == OPS3D_FDA_EINVAL:
+            raise ValueError(msg)
+        raise RuntimeError(msg)
+
+    @staticmethod
+    def _check_inputs(tensors: dict, value: torch.Tensor) -> None:
+        for name, t in tensors.items():
+            if not isinstance(t, torch.Tensor):
+                raise TypeError(f"{name} must be a torch.Tensor")
+            if not t.is_cuda:
+                # reference csrc/flash_deform_attn.h:24,51
+                raise RuntimeError(f"Not implemented on the CPU ({name} is on {t.device})")
+            if not t.is_contiguous():
+                raise RuntimeError(f"{name} tensor has to be contiguous")
+            if t.device != value.device:
+                raise RuntimeError(f"{name} is on {t.device}, value on {value.device}")
+
+    def _common(self, value, spatial_shapes, level_start_index, sampling_loc_attn, K, extra):
+        tensors = {
+            "value": value,
+            "spatial_shapes": spatial_shapes,
+            "level_start_index": level_start_index,
+            "sampling_loc_attn": sampling_loc_attn,
+            **extra,
+        }
+        self._check_inputs(tensors, value)
+        if value.dtype not in _DTYPE_CODE:
+            raise ValueError(f"unsupported value dtype {value.dtype}")
+        for name in ("sampling_loc_attn", *extra):
+            if tensors[name].dtype != value.dtype:
+                raise ValueError(f"{name} dtype {tensors[name].dtype} differs from value dtype {value.dtype}")
+        if spatial_shapes.dtype != torch.int64 or level_start_index.dtype != torch.int64:
+            raise ValueError("spatial_shapes and level_start_index must be int64")
+        if value.dim() != 4:
+            raise ValueError(f"value must be [B, S, G, D], got shape {tuple(value.shape)}")
+        B, S, G, D = value.shape
+        L = spatial_shapes.shape[0]
+        if spatial_shapes.dim() != 2 or spatial_shapes.shape[1] != 3:
+            raise ValueError(f"spatial_shapes must be [L, 3], got {tuple(spatial_shapes.shape)}")
+        if level_start_index.shape != (L,):
+            raise ValueError(f"level_start_index must be [{L}], got {tuple(level_start_index.shape)}")
+        if sampling_loc_attn.dim() != 4 or sampling_loc_attn.shape[0] != B or sampling_loc_attn.shape[2] != G:
+            raise ValueError(
+                f"sampling_loc_attn must be [B={B}, Q, G={G}, P], got {tuple(sampling_loc_attn.shape)}"
+            )
+        P = L * K * 4
+        if sampling_loc_attn.shape[3] != P:
+            raise ValueError(
+                f"sampling_loc_attn last dimension ({sampling_loc_attn.shape[3]}) does not match "
+                f"L={L}, K={K} (expected {P})"
+            )
+        Q = sampling_loc_attn.shape[1]
+        return B, S, G, D, L, Q
+
+    # -- entry points (reference csrc/flash_deform_attn.h) -----------------------------------
+    def flash_deform_attn_forward(
+        self, value, spatial_shapes, level_start_index, sampling_loc_attn, im2col_step, K,
+        d_stride=8, block_thread=0, use_reg=True,
+    ):
+        """Forward; ``d_stride``, ``block_thread`` and ``use_reg`` are accepted and ignored
+        (the gfx950 launch geometry is chosen by the library).  Returns [B, Q, G*D]."""
+        B, S, G, D, L, Q = self._common(value, spatial_shapes, level_start_index, sampling_loc_attn, K, {})
+        out = torch.empty((B, Q, G * D), dtype=value.dtype, device=value.device)
+        stream = torch.cuda.current_stream(value.device).cuda_stream
+        with torch.cuda.device(value.device):
+            rc = self._lib.ops3d_fda_forward(
+                _ptr(value), _ptr(spatial_shapes), _ptr(level_start_index), _ptr(sampling_loc_attn),
+                _ptr(out), _DTYPE_CODE[value.dtype], B, S, G, D, L, Q, int(K), int(im2col_step), stream,
+            )
+        if rc != OPS3D_FDA_OK:
+            self._raise(rc, "flash_deform_attn_forward failed")
+        return out
+
+    def flash_deform_attn_backward(
+        self, value, spatial_shapes, level_start_index, sampling_loc_attn, grad_output,
+        im2col_step, K, d_stride=1, block_thread=0,
+    ):
+        """Backward; returns [grad_value, grad_sampling_loc_attn] in value's dtype."""
+        B, S, G, D, L, Q = self._common(
+            value, spatial_shapes, level_start_index, sampling_loc_attn, K, {"grad_output": grad_output}
+        )
+        if grad_output.numel() != B * Q * G * D:
+            raise ValueError(f"grad_output must have B*Q*G*D = {B * Q * G * D} elements, got {grad_output.numel()}")
+        code = _DTYPE_CODE[value.dtype]
+        grad_value = torch.empty_like(value)
+        grad_sla = torch.empty_like(sampling_loc_attn)
+        ws_bytes = self._lib.ops3d_fda_backward_workspace_bytes(code, B, S, G, D)
+        ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=value.device) if ws_bytes else None
+        stream = torch.cuda.current_stream(value.device).cuda_stream
+        with torch.cuda.device(value.device):
+            rc = self._lib.ops3d_fda_backward(
+                _ptr(value), _ptr(spatial_shapes), _ptr(level_start_index), _ptr(sampling_loc_attn),
+                _ptr(grad_output), _ptr(grad_value), _ptr(grad_sla), _ptr(ws), ws_bytes,
+                code, B, S, G, D, L, Q, int(K), int(im2col_step), stream,
+            )
+        if rc != OPS3D_FDA_OK:
+            self._raise(rc, "flash_deform_attn_backward failed")
+        return [grad_value, grad_sla]
+
+    def flash_deform_attn_backward_accumulate(
+        self, value, spatial_shapes, level_start_index, sampling_loc_attn, grad_output,
+        grad_value_f32, im2col_step, K,
+    ):
+        """Backward kernel only: adds value gradients into the fp32 tensor ``grad_value_f32``
+        ([B,S,G,D], not cleared) and returns a new grad_sampling_loc_attn (value dtype)."""
+        B, S, G, D, L, Q = self._common(
+            value, spatial_shapes, level_start_index, sampling_loc_attn, K, {"grad_output": grad_output}
+        )
+        if grad_value_f32.dtype != torch.float32 or grad_value_f32.shape != value.shape:
+            raise ValueError("grad_value_f32 must be an fp32 tensor shaped like value")
+        self._check_inputs({"grad_value_f32": grad_value_f32}, value)
+        grad_sla = torch.empty_like(sampling_loc_attn)
+        stream = torch.cuda.current_stream(value.device).cuda_stream
+        with torch.cuda.device(value.device):
+            rc = self._lib.ops3d_fda_backward_accumulate_f32(
+                _ptr(value), _ptr(spatial_shapes), _ptr(level_start_index), _ptr(sampling_loc_attn),
+                _ptr(grad_output), _ptr(grad_value_f32), _ptr(grad_sla),
+                _DTYPE_CODE[value.dtype], B, S, G, D, L, Q, int(K), int(im2col_step), stream,
+            )
+        if rc != OPS3D_FDA_OK:
+            self._raise(rc, "flash_deform_attn_backward_accumulate failed")
+        return grad_sla
+
+    def supported(self, dtype: torch.dtype, channels: int) -> bool:
+        return dtype in _DTYPE_CODE and bool(self._lib.ops3d_fda_supported(_DTYPE_CODE[dtype], int(channels)))
+
+
+def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
+    """dlopen libops3d_fda.so and declare its C signatures (raises OSError if absent)."""
+    lib = ctypes.CDLL(path)
+    _declare(lib)
+    return lib
+
+
+def _load():
+    try:
+        return _NativeFDA(load_library(LIB_PATH), LIB_PATH)
+    except (OSError, ImportError, AttributeError):
+        return None
+
+
+_C = _load()
+
+
+def reload() -> None:
+    """Re-resolve ``_C`` (after building the library in this process)."""
+    global _C
+    _C = _load()
+    from . import flash_deform_attn as _fda
+
+    _fda._C = _C

@@ -1,0 +1,331 @@
+// Device-side building blocks of the gfx950 Flash Deformable 3D Attention kernels.
+//
+// Work decomposition (shared by forward and backward):
+//   * a "unit" is one (b, q, g) triple: one query, one head.  LPU consecutive lanes of a wave64
+//     own a unit; each lane owns CPL consecutive channels of the head (CPL*sizeof(T) bytes,
+//     one 16-byte load for bf16/fp16 with CPL=8 or fp32 with CPL=4).
+//   * a workgroup is 4 waves = UPB = 4*64/LPU units, all of the SAME (b, g) and consecutive q.
+//     Blocks are mapped to heads XCD-first (map_tile): the hardware dispatches workgroup i to
+//     XCD i % 8, so with G = 8 each XCD only ever gathers (and, in backward, scatters) the
+//     channels of one head and its 4 MB L2 holds that head's slice of the value volume.
+//   * the unit's packed record (L*K*3 locations + L*K logits, reference layout
+//     csrc/cuda/flash_deform_im2col_cuda.cuh:151-153,217-219) is staged once into LDS as fp32
+//     by the unit's own lanes; the softmax over the L*K logits runs cooperatively across the
+//     LPU lanes with cross-lane reductions (no block barrier; a unit never leaves its wave).
+//   * corner gathers are raw buffer loads: a corner outside the level volume gets the offset
+//     OOB_ELEM, and the buffer hardware returns zeros (loads) or drops the write (atomics).
+//     This is the zero padding of the reference (common.h:99-117) without branches.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ops3d_fda {
+
+constexpr int kWave = 64;
+constexpr int kWavesPerBlock = 4;
+constexpr int kBlock = kWave * kWavesPerBlock;
+// Corner offsets are kept in ELEMENTS.  A corner outside the volume gets OOB_ELEM; scaled to
+// bytes (x2 or x4) it lands at >= 2^30, beyond every buffer we create (the host limits
+// S*G*D to 2^28 elements, i.e. <= 1 GiB of fp32 per batch item), so the buffer unit returns 0
+// for loads and drops atomics.
+constexpr uint32_t OOB_ELEM = 0x20000000u;
+constexpr int64_t kMaxLevelElems = (int64_t)1 << 28;
+constexpr int kBufferFlags = 0x00020000;      // dword3 of a gfx9-family raw buffer resource
+
+struct Args {
+  const void *value;          // [B,S,G,D] T
+  const int64_t *shapes;      // [L,3] (D,H,W)
+  const int64_t *lsi;         // [L]
+  const void *loc_attn;       // [B,Q,G,P] T
+  const void *grad_out;       // [B,Q,G*D] T          (backward)
+  void *out;                  // [B,Q,G*D] T          (forward)
+  float *grad_value;          // [B,S,G,D] fp32 acc   (backward)
+  void *grad_loc_attn;        // [B,Q,G,P] T          (backward)
+  int B, S, G, D, L, K, Q, P;
+  int nqb;                    // query blocks per batch = ceil(Q / UPB)
+  int ncol;                   // B * nqb
+  int xcd_mode;               // 0: G % 8 == 0, 1: 8 % G == 0, 2: no XCD affinity
+  int hpx;                    // heads per XCD (mode 0)
+  int xpg;                    // XCDs per head (mode 1)
+};
+
+// blockIdx.x -> (b, g, qb).  Returns false for padding blocks of mode 1.
+__device__ __forceinline__ bool map_tile(const Args &a, int bid, int &b, int &g, int &qb) {
+  int col;
+  if (a.xcd_mode == 0) {
+    const int xcd = bid & 7, r = bid >> 3;
+    g = xcd * a.hpx + r % a.hpx;
+    col = r / a.hpx;
+  } else if (a.xcd_mode == 1) {
+    const int xcd = bid & 7;
+    g = xcd % a.G;
+    col = (bid >> 3) * a.xpg + xcd / a.G;
+    if (col >= a.ncol) return false;
+  } else {
+    g = bid % a.G;
+    col = bid / a.G;
+  }
+  b = col / a.nqb;
+  qb = col - b * a.nqb;
+  return true;
+}
+
+// ---------------------------------------------------------------------------------------------
+// element types: float, _Float16, __bf16.  Conversions go through 32-bit words.
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static constexpr int kPerWord = 1;
+  static __device__ __forceinline__ void unpack(uint32_t w, float *f) { f[0] = __uint_as_float(w); }
+  static __device__ __forceinline__ uint32_t pack(const float *f) { return __float_as_uint(f[0]); }
+};
+template <> struct Elem<__bf16> {
+  static constexpr int kPerWord = 2;
+  static __device__ __forceinline__ void unpack(uint32_t w, float *f) {
+    f[0] = __uint_as_float(w << 16);
+    f[1] = __uint_as_float(w & 0xffff0000u);
+  }
+  static __device__ __forceinline__ uint32_t pack(const float *f) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    bf2 h;
+    h.x = (__bf16)f[0];   // round to nearest even (v_cvt_pk_bf16_f32)
+    h.y = (__bf16)f[1];
+    return __builtin_bit_cast(uint32_t, h);
+  }
+};
+template <> struct Elem<_Float16> {
+  static constexpr int kPerWord = 2;
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  static __device__ __forceinline__ void unpack(uint32_t w, float *f) {
+    h2 h = __builtin_bit_cast(h2, w);
+    f[0] = (float)h.x;
+    f[1] = (float)h.y;
+  }
+  static __device__ __forceinline__ uint32_t pack(const float *f) {
+    h2 h;
+    h.x = (_Float16)f[0];
+    h.y = (_Float16)f[1];
+    return __builtin_bit_cast(uint32_t, h);
+  }
+};
+
+// ---------------------------------------------------------------------------------------------
+// raw buffer access
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                           kBufferFlags);
+}
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Load NB bytes (NB in {4, 8, 12, 16, 24, 32, 48}) at byte offset `off` into words w[NB/4].
+template <int NB>
+__device__ __forceinline__ void bload(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t *w) {
+  static_assert(NB % 4 == 0, "whole words only");
+  if constexpr (NB == 4) {
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+  } else if constexpr (NB == 8) {
+    u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    w[0] = v.x; w[1] = v.y;
+  } else if constexpr (NB == 12) {
+    u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(r, off, 0, 0);
+    w[0] = v.x; w[1] = v.y; w[2] = v.z;
+  } else if constexpr (NB % 16 == 0) {
+#pragma unroll
+    for (int i = 0; i < NB / 16; ++i) {
+      u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * i, 0, 0);
+      w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+    }
+  } else if constexpr (NB == 24) {
+    u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    u32x2 t = __builtin_amdgcn_raw_buffer_load_b64(r, off + 16, 0, 0);
+    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w; w[4] = t.x; w[5] = t.y;
+  } else {
+    static_assert(NB == 4, "unsupported vector width");
+  }
+}
+
+// Load N elements of T (N*sizeof(T) bytes) at byte offset `off` and widen to fp32.
+template <typename T, int N>
+__device__ __forceinline__ void load_elems(__amdgpu_buffer_rsrc_t r, uint32_t off, float *f) {
+  constexpr int NB = N * (int)sizeof(T);
+  uint32_t w[NB / 4];
+  bload<NB>(r, off, w);
+#pragma unroll
+  for (int i = 0; i < NB / 4; ++i) Elem<T>::unpack(w[i], f + i * Elem<T>::kPerWord);
+}
+
+// Store N fp32 values as T to a plain global pointer (aligned to N*sizeof(T) or 16 bytes).
+template <typename T, int N>
+__device__ __forceinline__ void store_elems(T *p, const float *f) {
+  constexpr int NB = N * (int)sizeof(T);
+  constexpr int NW = NB / 4;
+  uint32_t w[NW];
+#pragma unroll
+  for (int i = 0; i < NW; ++i) w[i] = Elem<T>::pack(f + i * Elem<T>::kPerWord);
+  uint32_t *q = reinterpret_cast<uint32_t *>(p);
+  if constexpr (NB % 16 == 0) {
+#pragma unroll
+    for (int i = 0; i < NW / 4; ++i)
+      *reinterpret_cast<u32x4 *>(q + 4 * i) = u32x4{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]};
+  } else if constexpr (NB % 8 == 0) {
+#pragma unroll
+    for (int i = 0; i < NW / 2; ++i) *reinterpret_cast<u32x2 *>(q + 2 * i) = u32x2{w[2 * i], w[2 * i + 1]};
+  } else {
+#pragma unroll
+    for (int i = 0; i < NW; ++i) q[i] = w[i];
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// cross-lane sums/max inside a unit of LPU lanes (LPU a power of two, units aligned to LPU).
+template <int M>
+__device__ __forceinline__ float xor_lane(float v) {
+  if constexpr (M == 1) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+  } else if constexpr (M == 2) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+  } else if constexpr (M == 8) {
+    // row_ror:8 inside a row of 16 lanes == lane ^ 8
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
+  } else if constexpr (M == 4 || M == 16) {
+    // ds_swizzle bit mode: and_mask = 0x1f, or_mask = 0, xor_mask = M
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (M << 10) | 0x1f));
+  } else {
+    return __shfl_xor(v, M, kWave);
+  }
+}
+
+template <int LPU>
+__device__ __forceinline__ float unit_sum(float v) {
+#pragma unroll
+  for (int m = 1; m < LPU; m <<= 1) {
+    if (m == 1) v += xor_lane<1>(v);
+    else if (m == 2) v += xor_lane<2>(v);
+    else if (m == 4) v += xor_lane<4>(v);
+    else if (m == 8) v += xor_lane<8>(v);
+    else if (m == 16) v += xor_lane<16>(v);
+    else v += xor_lane<32>(v);
+  }
+  return v;
+}
+
+template <int LPU>
+__device__ __forceinline__ float unit_max(float v) {
+#pragma unroll
+  for (int m = 1; m < LPU; m <<= 1) {
+    float o;
+    if (m == 1) o = xor_lane<1>(v);
+    else if (m == 2) o = xor_lane<2>(v);
+    else if (m == 4) o = xor_lane<4>(v);
+    else if (m == 8) o = xor_lane<8>(v);
+    else if (m == 16) o = xor_lane<16>(v);
+    else o = xor_lane<32>(v);
+    v = fmaxf(v, o);
+  }
+  return v;
+}
+
+// Make this wave's LDS writes visible to the other lanes of the same wave.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// ---------------------------------------------------------------------------------------------
+// Stage one unit's packed record (P elements of T) into LDS as fp32; lane j of the unit loads
+// words j, j+LPU, ...  Dead units (q >= Q) stage zeros.
+template <typename T, int LPU>
+__device__ __forceinline__ void stage_record(const T *rec_g, int P, int j, bool live, float *rec) {
+  constexpr int EPW = Elem<T>::kPerWord;
+  const int nw = P / EPW;
+  const uint32_t *src = reinterpret_cast<const uint32_t *>(rec_g);
+  for (int w = j; w < nw; w += LPU) {
+    float f[EPW];
+    const uint32_t word = live ? src[w] : 0u;
+    Elem<T>::unpack(word, f);
+#pragma unroll
+    for (int e = 0; e < EPW; ++e) rec[w * EPW + e] = f[e];
+  }
+}
+
+// Write one unit's record (P fp32 values in LDS) to global memory as T.
+template <typename T, int LPU>
+__device__ __forceinline__ void write_record(T *rec_g, int P, int j, const float *rec) {
+  constexpr int EPW = Elem<T>::kPerWord;
+  const int nw = P / EPW;
+  uint32_t *dst = reinterpret_cast<uint32_t *>(rec_g);
+  for (int w = j; w < nw; w += LPU) {
+    float f[EPW];
+#pragma unroll
+    for (int e = 0; e < EPW; ++e) f[e] = rec[w * EPW + e];
+    dst[w] = Elem<T>::pack(f);
+  }
+}
+
+// In-place fp32 softmax over logits[0..n) of one unit (reference im2col.cuh:222-240: max,
+// exp(x - max), divide by the sum; over all L*K jointly).  Lane j handles j, j+LPU, ...
+template <int LPU>
+__device__ __forceinline__ void unit_softmax(float *logits, int n, int j) {
+  float m = -INFINITY;
+  for (int s = j; s < n; s += LPU) m = fmaxf(m, logits[s]);
+  m = unit_max<LPU>(m);
+  float sum = 0.f;
+  for (int s = j; s < n; s += LPU) {
+    const float e = expf(logits[s] - m);
+    logits[s] = e;
+    sum += e;
+  }
+  sum = unit_sum<LPU>(sum);
+  for (int s = j; s < n; s += LPU) logits[s] = logits[s] / sum;
+}
+
+// Pixel coordinate of a normalised location exactly as torch's grid_sample computes it for
+// align_corners=False on grid = 2*loc - 1:  ((grid + 1) * size - 1) / 2, each step rounded in
+// fp32 (no contraction), so the kernel samples at the same coordinate as the PyTorch path.
+// (Reference CUDA: loc * size - 0.5, flash_deform_im2col_cuda.cuh:268-270; equal up to 1 ulp.)
+__device__ __forceinline__ float pixel_coord(float loc, float size) {
+  const float grid = __fsub_rn(__fmul_rn(2.f, loc), 1.f);
+  return __fmul_rn(__fsub_rn(__fmul_rn(__fadd_rn(grid, 1.f), size), 1.f), 0.5f);
+}
+
+// Per-sample trilinear set-up shared by forward and backward.
+struct Sample {
+  uint32_t off[8];   // element offsets (voxel*G*D) inside the level, OOB_ELEM if outside
+  float wx[2], wy[2], wz[2];
+};
+
+// Returns false when every corner lies outside the volume (coordinate outside [-1, size) on some
+// axis, or NaN): such a sample contributes nothing, as with zero padding.
+__device__ __forceinline__ bool sample_setup(float lx, float ly, float lz, int Wl, int Hl, int Dl,
+                                             int GD, Sample &sm) {
+  const float x = pixel_coord(lx, (float)Wl);
+  const float y = pixel_coord(ly, (float)Hl);
+  const float z = pixel_coord(lz, (float)Dl);
+  if (!(x >= -1.f && y >= -1.f && z >= -1.f && x < (float)Wl && y < (float)Hl && z < (float)Dl))
+    return false;
+  const float x0f = floorf(x), y0f = floorf(y), z0f = floorf(z);
+  const int x0 = (int)x0f, y0 = (int)y0f, z0 = (int)z0f;
+  sm.wx[1] = x - x0f; sm.wx[0] = (x0f + 1.f) - x;
+  sm.wy[1] = y - y0f; sm.wy[0] = (y0f + 1.f) - y;
+  sm.wz[1] = z - z0f; sm.wz[0] = (z0f + 1.f) - z;
+  const bool vx0 = x0 >= 0, vx1 = x0 + 1 < Wl;
+  const bool vy0 = y0 >= 0, vy1 = y0 + 1 < Hl;
+  const bool vz0 = z0 >= 0, vz1 = z0 + 1 < Dl;
+  const uint32_t sx = (uint32_t)GD, sy = (uint32_t)(Wl * GD), sz = (uint32_t)(Hl * Wl) * (uint32_t)GD;
+  const uint32_t ox0 = (uint32_t)x0 * sx, oy0 = (uint32_t)y0 * sy, oz0 = (uint32_t)z0 * sz;
+  const uint32_t ox[2] = {ox0, ox0 + sx}, oy[2] = {oy0, oy0 + sy}, oz[2] = {oz0, oz0 + sz};
+  const bool vx[2] = {vx0, vx1}, vy[2] = {vy0, vy1}, vz[2] = {vz0, vz1};
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const int dz = c >> 2, dy = (c >> 1) & 1, dx = c & 1;
+    const bool ok = vz[dz] && vy[dy] && vx[dx];
+    sm.off[c] = ok ? oz[dz] + oy[dy] + ox[dx] : OOB_ELEM;
+  }
+  return true;
+}
+
+}  // namespace ops3d_fda

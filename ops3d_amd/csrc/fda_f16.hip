@@ -1,0 +1,15 @@
+// Kernel instantiations for element type _Float16 (channels per lane 8 or 12).
+#include "fda_kernels.h"
+
+namespace ops3d_fda {
+
+hipError_t launch_f16(bool backward, int cpl, int lpu, const Args &a, unsigned grid, size_t lds,
+                     hipStream_t st) {
+  switch (cpl) {
+    case 8: return launch_cpl<_Float16, 8>(backward, lpu, a, grid, lds, st);
+    case 12: return launch_cpl<_Float16, 12>(backward, lpu, a, grid, lds, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace ops3d_fda

@@ -1,0 +1,245 @@
+// gfx950 forward and backward kernels of Flash Deformable 3D Attention.
+//
+// Forward (replaces forward_kernel_reg, reference csrc/cuda/flash_deform_im2col_cuda.cuh:190-295):
+//   out[b,q,g,:] = sum_{l,k} softmax(logits[b,q,g,:])[l,k] *
+//                  trilinear(value_l[b,:,g,:], pixel(loc[b,q,g,l,k]))
+// Backward (replaces backward_kernel_warp_primitive, flash_deform_col2im_cuda.cuh:248-429, and
+// ms_deform_attn_col2im_trilinear, common.h:141-353):
+//   grad_value  += attn * w_corner * grad_out           (fp32 buffer atomics, dropped when OOB)
+//   grad_loc     = attn * size * sum_c grad_out[c] * d(interp_c)/d(pixel)
+//   grad_attn    = sum_c grad_out[c] * interp_c, then softmax backward
+//                  grad_logit_i = a_i * (grad_attn_i - sum_j a_j grad_attn_j)
+// The per-sample location/attention partials are formed from U_i = sum_c grad_out[c] * V_i[c]
+// (one dot product per corner) so the channel loop costs one FMA per corner and channel, and
+// are summed over the unit's LPU lanes with DPP / ds_swizzle reductions.
+#pragma once
+
+#include "fda_device.h"
+
+namespace ops3d_fda {
+
+template <typename T, int N>
+__device__ __forceinline__ void load_global_elems(const T *p, float *f) {
+  constexpr int NB = N * (int)sizeof(T);
+  constexpr int NW = NB / 4;
+  uint32_t w[NW];
+  const uint32_t *q = reinterpret_cast<const uint32_t *>(p);
+  if constexpr (NB % 16 == 0) {
+#pragma unroll
+    for (int i = 0; i < NW / 4; ++i) {
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(q + 4 * i);
+      w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+    }
+  } else if constexpr (NB % 8 == 0) {
+#pragma unroll
+    for (int i = 0; i < NW / 2; ++i) {
+      const u32x2 v = *reinterpret_cast<const u32x2 *>(q + 2 * i);
+      w[2 * i] = v.x; w[2 * i + 1] = v.y;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NW; ++i) w[i] = q[i];
+  }
+#pragma unroll
+  for (int i = 0; i < NW; ++i) Elem<T>::unpack(w[i], f + i * Elem<T>::kPerWord);
+}
+
+// ---------------------------------------------------------------------------------------------
+template <typename T, int CPL, int LPU>
+__global__ __launch_bounds__(kBlock) void fda_forward_kernel(const Args a) {
+  extern __shared__ float lds[];
+  constexpr int UPW = kWave / LPU, UPB = kWavesPerBlock * UPW;
+  int b, g, qb;
+  if (!map_tile(a, blockIdx.x, b, g, qb)) return;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int j = lane & (LPU - 1);
+  const int ub = wave * UPW + lane / LPU;
+  const int q = qb * UPB + ub;
+  const bool live = q < a.Q;
+  const int L = a.L, K = a.K, LK = L * K, P = a.P;
+  float *rec = lds + ub * (P + 1);
+  const int64_t unit = ((int64_t)b * a.Q + (live ? q : 0)) * a.G + g;
+
+  stage_record<T, LPU>(static_cast<const T *>(a.loc_attn) + unit * P, P, j, live, rec);
+  wave_lds_sync();
+  unit_softmax<LPU>(rec + 3 * LK, LK, j);
+  wave_lds_sync();
+
+  float acc[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) acc[c] = 0.f;
+
+  const int GD = a.G * a.D;
+  const uint32_t lane_elem = (uint32_t)(g * a.D + j * CPL);
+  const T *vb = static_cast<const T *>(a.value) + (int64_t)b * a.S * GD;
+  int s = 0;
+  for (int l = 0; l < L; ++l) {
+    const int Dl = (int)a.shapes[3 * l], Hl = (int)a.shapes[3 * l + 1], Wl = (int)a.shapes[3 * l + 2];
+    const int64_t st = a.lsi[l];
+    const uint32_t nbytes = (uint32_t)((int64_t)Dl * Hl * Wl * GD * (int64_t)sizeof(T));
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb + st * GD, nbytes);
+#pragma unroll 2
+    for (int k = 0; k < K; ++k, ++s) {
+      const float lx = rec[3 * s], ly = rec[3 * s + 1], lz = rec[3 * s + 2];
+      const float at = rec[3 * LK + s];
+      Sample sm;
+      if (live && sample_setup(lx, ly, lz, Wl, Hl, Dl, GD, sm)) {
+        float v[8][CPL];
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+          load_elems<T, CPL>(rv, (sm.off[c] + lane_elem) * (uint32_t)sizeof(T), v[c]);
+        float w[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) w[c] = (sm.wx[c & 1] * sm.wy[(c >> 1) & 1]) * sm.wz[c >> 2];
+#pragma unroll
+        for (int ch = 0; ch < CPL; ++ch) {
+          float t = v[0][ch] * w[0];
+#pragma unroll
+          for (int c = 1; c < 8; ++c) t = fmaf(v[c][ch], w[c], t);
+          acc[ch] = fmaf(at, t, acc[ch]);
+        }
+      }
+    }
+  }
+  if (live) store_elems<T, CPL>(static_cast<T *>(a.out) + unit * a.D + j * CPL, acc);
+}
+
+// ---------------------------------------------------------------------------------------------
+template <typename T, int CPL, int LPU>
+__global__ __launch_bounds__(kBlock) void fda_backward_kernel(const Args a) {
+  extern __shared__ float lds[];
+  constexpr int UPW = kWave / LPU, UPB = kWavesPerBlock * UPW;
+  int b, g, qb;
+  if (!map_tile(a, blockIdx.x, b, g, qb)) return;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int j = lane & (LPU - 1);
+  const int ub = wave * UPW + lane / LPU;
+  const int q = qb * UPB + ub;
+  const bool live = q < a.Q;
+  const int L = a.L, K = a.K, LK = L * K, P = a.P;
+  float *rec = lds + ub * (P + LK + 1);   // [0,P): record, later its gradient; [P,P+LK): grad_attn
+  float *gat_s = rec + P;
+  const int64_t unit = ((int64_t)b * a.Q + (live ? q : 0)) * a.G + g;
+
+  stage_record<T, LPU>(static_cast<const T *>(a.loc_attn) + unit * P, P, j, live, rec);
+  wave_lds_sync();
+  unit_softmax<LPU>(rec + 3 * LK, LK, j);
+  wave_lds_sync();
+
+  float tg[CPL];
+  if (live) {
+    load_global_elems<T, CPL>(static_cast<const T *>(a.grad_out) + unit * a.D + j * CPL, tg);
+  } else {
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) tg[c] = 0.f;
+  }
+
+  const int GD = a.G * a.D;
+  const uint32_t lane_elem = (uint32_t)(g * a.D + j * CPL);
+  const T *vb = static_cast<const T *>(a.value) + (int64_t)b * a.S * GD;
+  float *gvb = a.grad_value + (int64_t)b * a.S * GD;
+  int s = 0;
+  for (int l = 0; l < L; ++l) {
+    const int Dl = (int)a.shapes[3 * l], Hl = (int)a.shapes[3 * l + 1], Wl = (int)a.shapes[3 * l + 2];
+    const int64_t st = a.lsi[l];
+    const int64_t nel = (int64_t)Dl * Hl * Wl * GD;
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb + st * GD, (uint32_t)(nel * (int64_t)sizeof(T)));
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(gvb + st * GD, (uint32_t)(nel * 4));
+    for (int k = 0; k < K; ++k, ++s) {
+      const float lx = rec[3 * s], ly = rec[3 * s + 1], lz = rec[3 * s + 2];
+      const float at = rec[3 * LK + s];
+      float gx = 0.f, gy = 0.f, gz = 0.f, ga = 0.f;
+      Sample sm;
+      if (live && sample_setup(lx, ly, lz, Wl, Hl, Dl, GD, sm)) {
+        float U[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          float v[CPL];
+          load_elems<T, CPL>(rv, (sm.off[c] + lane_elem) * (uint32_t)sizeof(T), v);
+          float u = v[0] * tg[0];
+#pragma unroll
+          for (int ch = 1; ch < CPL; ++ch) u = fmaf(v[ch], tg[ch], u);
+          U[c] = u;
+        }
+        float w[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) w[c] = (sm.wx[c & 1] * sm.wy[(c >> 1) & 1]) * sm.wz[c >> 2];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const float aw = at * w[c];
+          const uint32_t o = (sm.off[c] + lane_elem) * 4u;
+#pragma unroll
+          for (int ch = 0; ch < CPL; ++ch)
+            __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(aw * tg[ch], rg, o + 4u * ch, 0, 0);
+        }
+#pragma unroll
+        for (int c = 0; c < 8; ++c) ga = fmaf(w[c], U[c], ga);
+        // d w_c / dx = (dx ? +1 : -1) * wy * wz, and likewise for y, z
+#pragma unroll
+        for (int zy = 0; zy < 4; ++zy) {
+          const int dz = zy >> 1, dy = zy & 1;
+          gx = fmaf(sm.wy[dy] * sm.wz[dz], U[4 * dz + 2 * dy + 1] - U[4 * dz + 2 * dy], gx);
+        }
+#pragma unroll
+        for (int zx = 0; zx < 4; ++zx) {
+          const int dz = zx >> 1, dx = zx & 1;
+          gy = fmaf(sm.wx[dx] * sm.wz[dz], U[4 * dz + 2 + dx] - U[4 * dz + dx], gy);
+        }
+#pragma unroll
+        for (int yx = 0; yx < 4; ++yx) {
+          const int dy = yx >> 1, dx = yx & 1;
+          gz = fmaf(sm.wx[dx] * sm.wy[dy], U[4 + 2 * dy + dx] - U[2 * dy + dx], gz);
+        }
+      }
+      gx = unit_sum<LPU>(gx);
+      gy = unit_sum<LPU>(gy);
+      gz = unit_sum<LPU>(gz);
+      ga = unit_sum<LPU>(ga);
+      if (j == 0) {
+        // d(pixel)/d(loc) = size (grid_sample: size/2 per unit of grid, grid = 2*loc - 1)
+        rec[3 * s] = gx * at * (float)Wl;
+        rec[3 * s + 1] = gy * at * (float)Hl;
+        rec[3 * s + 2] = gz * at * (float)Dl;
+        gat_s[s] = ga;
+      }
+    }
+  }
+  wave_lds_sync();
+  // softmax backward over the unit's L*K attention weights
+  float dot = 0.f;
+  for (int t = j; t < LK; t += LPU) dot = fmaf(rec[3 * LK + t], gat_s[t], dot);
+  dot = unit_sum<LPU>(dot);
+  for (int t = j; t < LK; t += LPU) {
+    const float at = rec[3 * LK + t];
+    rec[3 * LK + t] = at * (gat_s[t] - dot);
+  }
+  wave_lds_sync();
+  if (live) write_record<T, LPU>(static_cast<T *>(a.grad_loc_attn) + unit * P, P, j, rec);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Launch one (T, CPL) family, LPU chosen at run time.
+template <typename T, int CPL, int LPU>
+hipError_t launch_one(bool backward, const Args &a, unsigned grid, size_t lds, hipStream_t st) {
+  if (backward)
+    hipLaunchKernelGGL((fda_backward_kernel<T, CPL, LPU>), dim3(grid), dim3(kBlock), lds, st, a);
+  else
+    hipLaunchKernelGGL((fda_forward_kernel<T, CPL, LPU>), dim3(grid), dim3(kBlock), lds, st, a);
+  return hipGetLastError();
+}
+
+template <typename T, int CPL>
+hipError_t launch_cpl(bool backward, int lpu, const Args &a, unsigned grid, size_t lds,
+                      hipStream_t st) {
+  switch (lpu) {
+    case 1: return launch_one<T, CPL, 1>(backward, a, grid, lds, st);
+    case 2: return launch_one<T, CPL, 2>(backward, a, grid, lds, st);
+    case 4: return launch_one<T, CPL, 4>(backward, a, grid, lds, st);
+    case 8: return launch_one<T, CPL, 8>(backward, a, grid, lds, st);
+    case 16: return launch_one<T, CPL, 16>(backward, a, grid, lds, st);
+    case 32: return launch_one<T, CPL, 32>(backward, a, grid, lds, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace ops3d_fda

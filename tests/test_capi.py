@@ -1,0 +1,83 @@
+"""The C ABI library loads, exports every function include/ops3d_fda.h declares, and rejects
+bad arguments before touching the GPU (no compute calls here)."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ops3d_fda.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"OPS3D_FDA_API\s+[\w\s\*]*?\b(ops3d_fda_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from ops3d_amd import _extension
+
+    if not os.path.exists(_extension.LIB_PATH):
+        pytest.skip("libops3d_fda.so not built")
+    return _extension.load_library()
+
+
+def test_header_declares_all_bound_symbols():
+    from ops3d_amd._extension import EXPORTED_SYMBOLS
+
+    assert _declared() == sorted(EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_and_support_table(lib):
+    assert lib.ops3d_fda_abi_version() == 1
+    F32, F16, BF16 = 0, 1, 2
+    for d in (8, 16, 24, 32, 48, 64, 96, 128, 192, 256):
+        assert lib.ops3d_fda_supported(BF16, d) == 1, d
+        assert lib.ops3d_fda_supported(F16, d) == 1, d
+    for d in (8, 16, 24, 32, 48, 64, 96, 128, 192):
+        assert lib.ops3d_fda_supported(F32, d) == 1, d
+    for d in (0, 5, 20, 40, 7):
+        assert lib.ops3d_fda_supported(BF16, d) == 0, d
+    assert lib.ops3d_fda_supported(9, 32) == 0
+
+
+def test_workspace_bytes(lib):
+    assert lib.ops3d_fda_backward_workspace_bytes(2, 1, 73728, 8, 32) == 73728 * 256 * 4
+    assert lib.ops3d_fda_backward_workspace_bytes(0, 1, 73728, 8, 32) == 0
+
+
+def _fwd(lib, **kw):
+    a = dict(dtype=2, B=1, S=576, G=8, D=32, L=2, Q=576, K=4, step=64)
+    a.update(kw)
+    return lib.ops3d_fda_forward(None, None, None, None, None, a["dtype"], a["B"], a["S"], a["G"], a["D"],
+                                 a["L"], a["Q"], a["K"], a["step"], None)
+
+
+def test_argument_errors_before_device_work(lib):
+    assert _fwd(lib, L=6) == 1 and b"invalid number of scales" in lib.ops3d_fda_last_error()
+    assert _fwd(lib, L=0) == 1
+    assert _fwd(lib, K=0) == 1 and _fwd(lib, K=17) == 1
+    assert _fwd(lib, D=20) == 1 and b"unsupported channels" in lib.ops3d_fda_last_error()
+    assert _fwd(lib, dtype=7) == 1
+    assert _fwd(lib, B=5, step=2) == 2 and b"must divide" in lib.ops3d_fda_last_error()
+    assert _fwd(lib, step=0) == 1
+    assert _fwd(lib, S=1 << 26) == 1 and b"too large" in lib.ops3d_fda_last_error()
+    # valid sizes but NULL pointers are rejected, not dereferenced
+    assert _fwd(lib) == 1 and b"NULL" in lib.ops3d_fda_last_error()
+    # nothing to do: B*Q == 0 succeeds without touching any pointer
+    assert _fwd(lib, Q=0) == 0
+
+
+def test_backward_workspace_check(lib):
+    rc = lib.ops3d_fda_backward(None, None, None, None, None, ctypes.c_void_p(256), None, None, 0,
+                                2, 1, 576, 8, 32, 2, 576, 4, 64, None)
+    assert rc == 1 and b"workspace too small" in lib.ops3d_fda_last_error()

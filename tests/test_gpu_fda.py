@@ -1,0 +1,235 @@
+"""GPU parity of the gfx950 kernels against the float64 C oracle, through the public API
+(FlashDeformAttnFunction -> ops3d_amd._C -> libops3d_fda.so).
+
+Coverage follows the reference's tests (tests/test_flash_deform_attn.py,
+tests/test_flash_deform_attn_stress.py): the benchmark configurations c1..c5, edge shapes
+(1^3 volumes, anisotropic, uneven levels, B=64), K in {4, 8}, L up to 5, D in {32, 48, 64},
+fp32/fp16/bf16, out-of-volume samples, value scales 0 / 1e-6 / 1e4, zero upstream gradient,
+im2col_step invariance and the error contracts.  Tolerances: fp32 rtol 1e-5 / atol 1e-6,
+bf16 and fp16 rtol 2e-2 / atol 2e-2 (fda_helpers.TOL).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from fda_helpers import TOL, assert_close, compare_all, log, random_inputs, run_gpu, run_oracle
+from ops3d_amd import FlashDeformAttnFunction
+from ops3d_amd.workloads import WORKLOADS, level_meta, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(tag, inp, device, dtype, backward=True, tol=None, im2col_step=64):
+    log(f"[case] {tag}: shapes={inp['shapes']} value={tuple(inp['value'].shape)} "
+        f"sla={tuple(inp['sampling_loc_attn'].shape)} dtype={dtype} bwd={backward}")
+    got = run_gpu(inp, device, backward=backward, im2col_step=im2col_step)
+    ref = run_oracle(inp, backward=backward)
+    compare_all(tag, got, ref, len(inp["shapes"]), inp["K"], dtype, tol, inp=inp)
+
+
+# --- benchmark configurations --------------------------------------------------------------
+def test_c1_fp32(gpu_device):
+    w = WORKLOADS["c1"]
+    inp = make_inputs(w, seed=0, dtype=torch.float32)
+    _check("c1 fp32", inp, gpu_device, torch.float32)
+
+
+def test_golden_fixture_fp32(gpu_device):
+    import os
+
+    fx = np.load(os.path.join(os.path.dirname(__file__), "golden", "c1_small.npz"))
+    inp = {
+        "value": torch.from_numpy(fx["value"]),
+        "sampling_loc_attn": torch.from_numpy(fx["sampling_loc_attn"]),
+        "grad_output": torch.from_numpy(fx["grad_output"]),
+        "shapes": [tuple(int(t) for t in s) for s in fx["shapes"]],
+        "K": int(fx["K"]),
+    }
+    log("[case] golden c1_small fp32")
+    out, gv, gs = run_gpu(inp, gpu_device)
+    # fixture coordinates are exact float64 (the kernel rounds them in fp32, as torch does)
+    assert_close("golden output", out, fx["output"], 1e-5, 1e-5)
+    assert_close("golden grad_value", gv, fx["grad_value"], 1e-5, 1e-5)
+    assert_close("golden grad_sla", gs, fx["grad_sampling_loc_attn"], 1e-4, 1e-4)
+
+
+@pytest.mark.parametrize("name", ["c2", "c3"])
+def test_bf16_configs(gpu_device, name):
+    w = WORKLOADS[name]
+    inp = make_inputs(w, seed=0, dtype=torch.bfloat16)
+    _check(f"{name} bf16", inp, gpu_device, torch.bfloat16)
+
+
+def test_c4_bf16_full(gpu_device):
+    w = WORKLOADS["c4"]
+    inp = make_inputs(w, seed=0, dtype=torch.bfloat16)
+    _check("c4 bf16", inp, gpu_device, torch.bfloat16)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
+def test_c5_query_slice(gpu_device, dt):
+    """c5 at full size on the GPU.  Forward and location/logit gradients are per query, so a
+    query slice is checked directly; grad_value is checked exactly by zeroing the upstream
+    gradient outside the slice (the kernel still scatters from every query)."""
+    w = WORKLOADS["c5"]
+    inp = make_inputs(w, seed=0, dtype=dt)
+    nq = 2048
+    sel = torch.arange(0, w.nq, w.nq // nq)[:nq]
+    mask = torch.zeros(w.nq, dtype=torch.bool)
+    mask[sel] = True
+    go = inp["grad_output"].clone()
+    go[:, ~mask] = 0
+    inp["grad_output"] = go
+    backward = dt == torch.bfloat16
+    log(f"[case] c5 {dt} full-size, oracle on {nq} queries, backward={backward}")
+    out, gv, gs = run_gpu(inp, gpu_device, backward=backward)
+    sub = dict(inp)
+    sub["sampling_loc_attn"] = inp["sampling_loc_attn"][:, sel]
+    sub["grad_output"] = go[:, sel]
+    ref = run_oracle(sub, backward=backward)
+    rtol, atol = TOL[dt]
+    assert_close("c5 output", out[:, sel.to(out.device)], ref[0], rtol, atol)
+    if backward:
+        assert_close("c5 grad_value", gv, ref[1], rtol, atol)
+        assert_close("c5 grad_sla", gs[:, sel.to(gs.device)], ref[2], rtol, atol)
+
+
+# --- reference stress shapes (tests/test_flash_deform_attn_stress.py:47-97) ------------------
+EDGE_SHAPE_CASES = [
+    (1, (1, 1, 1), 1), (1, (4, 4, 4), 1), (1, (7, 7, 7), 1), (1, (8, 8, 8), 1),
+    (1, (16, 16, 16), 1), (2, (4, 4, 4), 1), (2, (8, 8, 8), 1), (3, (4, 4, 4), 1),
+    (3, (16, 16, 16), 1), (4, (8, 8, 8), 2), (5, (4, 4, 4), 1), (1, (32, 16, 8), 1),
+    (2, (16, 8, 4), 1), (1, (8, 4, 2), 1), (2, (32, 16, 8), 1), (1, (8, 8, 8), 64),
+]
+
+
+@pytest.mark.parametrize("L,spatial,B", EDGE_SHAPE_CASES)
+@pytest.mark.parametrize("K", [4, 8])
+def test_edge_shapes_fp32(gpu_device, L, spatial, B, K):
+    d, h, w = spatial
+    Q = max(1, min(64, d * h * w))
+    inp = random_inputs([spatial] * L, B, Q, 4, 32, K, torch.float32, seed=42)
+    _check(f"edge L={L} {spatial} B={B} K={K}", inp, gpu_device, torch.float32, im2col_step=B)
+
+
+def test_uneven_levels(gpu_device):
+    inp = random_inputs([(1, 1, 1), (64, 64, 64)], 1, 64, 4, 32, 4, torch.float32, seed=42)
+    _check("uneven 1^3+64^3", inp, gpu_device, torch.float32)
+
+
+def test_anisotropic_multilevel(gpu_device):
+    inp = random_inputs([(32, 16, 8), (16, 8, 4)], 1, 64, 4, 32, 4, torch.float32, seed=42)
+    _check("anisotropic", inp, gpu_device, torch.float32)
+
+
+def test_out_of_volume_fp32(gpu_device):
+    inp = random_inputs([(6, 5, 7), (3, 2, 4)], 2, 300, 8, 32, 4, torch.float32, seed=5, lo=-0.3, hi=1.3)
+    _check("oob fp32", inp, gpu_device, torch.float32)
+
+
+# --- head widths, head counts (XCD mappings), dtypes ---------------------------------------
+@pytest.mark.parametrize("D", [8, 16, 24, 32, 48, 64, 96, 128])
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16])
+def test_head_width(gpu_device, D, dt):
+    inp = random_inputs([(5, 6, 7), (3, 3, 4)], 1, 150, 8, D, 4, dt, seed=D)
+    _check(f"D={D} {dt}", inp, gpu_device, dt)
+
+
+@pytest.mark.parametrize("G", [1, 2, 3, 4, 6, 8, 16, 24])
+def test_head_count(gpu_device, G):
+    inp = random_inputs([(6, 6, 6), (3, 3, 3)], 2, 333, G, 32, 4, torch.float32, seed=G)
+    _check(f"G={G}", inp, gpu_device, torch.float32)
+
+
+def test_reference_forward_params_fp16(gpu_device):
+    """Reference default_forward_params (tests/conftest.py:27-57) with Lq reduced 4x:
+    D=64, L=4, K=8, levels 64^3/32^3/16^3/8^3, fp16."""
+    shapes = [(64, 64, 64), (32, 32, 32), (16, 16, 16), (8, 8, 8)]
+    inp = random_inputs(shapes, 1, 1024, 8, 64, 8, torch.float16, seed=42)
+    _check("ref fwd params fp16", inp, gpu_device, torch.float16, backward=False)
+
+
+def test_reference_backward_params_fp16(gpu_device):
+    """Reference default_backward_params (tests/conftest.py:60-87), D=48, L=2, K=4,
+    levels 64^3/32^3, Lq reduced to 8192."""
+    inp = random_inputs([(64, 64, 64), (32, 32, 32)], 1, 8192, 8, 48, 4, torch.float16, seed=42)
+    _check("ref bwd params fp16", inp, gpu_device, torch.float16)
+
+
+# --- numerics (stress :240-377, :385-405) -------------------------------------------------
+def test_zero_values(gpu_device):
+    inp = random_inputs([(4, 4, 4)], 1, 64, 4, 32, 4, torch.float32, value_scale=0.0)
+    out, _, _ = run_gpu(inp, gpu_device, backward=False)
+    assert torch.all(out == 0)
+
+
+@pytest.mark.parametrize("scale", [1e-6, 1e4])
+def test_value_scales_fp32(gpu_device, scale):
+    inp = random_inputs([(4, 4, 4)], 1, 64, 4, 32, 4, torch.float32, value_scale=scale)
+    rtol, atol = TOL[torch.float32]
+    _check(f"scale {scale}", inp, gpu_device, torch.float32, tol=(rtol, atol * max(1.0, scale)))
+
+
+def test_zero_upstream_grad_gives_zero_grads(gpu_device):
+    inp = random_inputs([(4, 4, 4), (4, 4, 4)], 1, 64, 4, 32, 4, torch.float32)
+    inp["grad_output"] = torch.zeros_like(inp["grad_output"])
+    _, gv, gs = run_gpu(inp, gpu_device)
+    assert gv.abs().max().item() == 0 and gs.abs().max().item() == 0
+
+
+def test_im2col_step_invariance_and_determinism(gpu_device):
+    inp = random_inputs([(5, 5, 5), (2, 3, 4)], 4, 77, 8, 32, 4, torch.bfloat16, seed=9)
+    outs = [run_gpu(inp, gpu_device, backward=False, im2col_step=s)[0] for s in (1, 2, 4, 64)]
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+
+
+def test_empty_queries(gpu_device):
+    inp = random_inputs([(4, 4, 4)], 1, 0, 4, 32, 4, torch.float32)
+    out, gv, gs = run_gpu(inp, gpu_device)
+    assert out.shape == (1, 0, 128) and gs.shape == (1, 0, 4, 16)
+    assert torch.all(gv == 0)
+
+
+# --- error contracts (stress :151-232) ----------------------------------------------------
+def _apply(inp, device, step=1):
+    st, lsi = level_meta(inp["shapes"], device)
+    return FlashDeformAttnFunction.apply(
+        inp["value"].to(device), st, lsi, inp["sampling_loc_attn"].to(device), step, inp["K"], True
+    )
+
+
+def test_error_batch_not_divisible(gpu_device):
+    inp = random_inputs([(4, 4, 4), (4, 4, 4)], 5, 64, 4, 32, 4, torch.float32)
+    with pytest.raises(RuntimeError, match="must divide"):
+        _apply(inp, gpu_device, step=2)
+
+
+def test_error_six_levels(gpu_device):
+    inp = random_inputs([(4, 4, 4)] * 6, 1, 64, 4, 32, 4, torch.float32)
+    with pytest.raises(ValueError, match="invalid number of scales"):
+        _apply(inp, gpu_device)
+
+
+def test_error_shape_mismatch(gpu_device):
+    inp = random_inputs([(4, 4, 4), (4, 4, 4)], 1, 64, 4, 32, 4, torch.float32)
+    inp["sampling_loc_attn"] = inp["sampling_loc_attn"][..., :16].contiguous()
+    with pytest.raises(ValueError, match="does not match"):
+        _apply(inp, gpu_device)
+
+
+def test_error_non_contiguous(gpu_device):
+    inp = random_inputs([(4, 4, 4)], 1, 64, 4, 32, 4, torch.float32)
+    st, lsi = level_meta(inp["shapes"], gpu_device)
+    v = inp["value"].to(gpu_device).transpose(1, 2).contiguous().transpose(1, 2)
+    with pytest.raises(RuntimeError, match="contiguous"):
+        FlashDeformAttnFunction.apply(v, st, lsi, inp["sampling_loc_attn"].to(gpu_device), 1, 4, True)
+
+
+def test_error_unsupported_channels(gpu_device):
+    inp = random_inputs([(4, 4, 4)], 1, 8, 2, 20, 4, torch.bfloat16)
+    with pytest.raises(ValueError, match="unsupported channels"):
+        _apply(inp, gpu_device)
