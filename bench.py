@@ -112,20 +112,31 @@ class Bench:
                 "p10": pct(ms, 10), "p90": pct(ms, 90), "mean": sum(ms) / len(ms)}
 
     def kernel_times(self, steps, warmup):
-        """Average launch duration (ms) of the forward kernel and of the backward kernel."""
+        """Average launch duration (ms) of the forward kernel (events around its one-kernel
+        call) and of each backward phase (events the library records between its launches)."""
         from ops3d_amd import _C
 
         torch = self.torch
         v, s = self.value.detach(), self.sla.detach()
-        acc = torch.zeros(v.shape, dtype=torch.float32, device=self.dev)
 
         def fk():
             _C.flash_deform_attn_forward(v, self.st, self.lsi, s, 64, self.w.K)
 
-        def bk():
-            _C.flash_deform_attn_backward_accumulate(v, self.st, self.lsi, s, self.go, acc, 64, self.w.K)
-
-        return self.time_loop(fk, steps, warmup), self.time_loop(bk, steps, warmup)
+        fwd = self.time_loop(fk, steps, warmup)
+        _C.profile_enable(True)
+        try:
+            phases = {}
+            for i in range(warmup + steps):
+                _C.flash_deform_attn_backward(v, self.st, self.lsi, s, self.go, 64, self.w.K)
+                r = _C.profile_read()
+                if i >= warmup:
+                    for k, t in r.items():
+                        phases.setdefault(k, []).append(t)
+        finally:
+            _C.profile_enable(False)
+        bwd = {k: {"mean": sum(t) / len(t), "median": statistics.median(t)} for k, t in phases.items()}
+        bwd["total"] = {"mean": sum(x["mean"] for x in bwd.values())}
+        return fwd, bwd
 
 
 def measure(w, dtype, steps, warmup, device, with_kernels=True, fwd_only=False):
@@ -202,7 +213,7 @@ def summary_line(r):
     f = r["fwd"]["median"]
     s = r.get("step", {}).get("median")
     fk = r.get("fwd_kernel", {}).get("mean")
-    bk = r.get("bwd_kernel", {}).get("mean")
+    bk = r.get("bwd_kernel", {}).get("total", {}).get("mean")
     samples = r["samples"]
     parts = [f"{r['workload']:>3} {r['dtype']:>4}", f"fwd {f * 1e3:8.1f} us ({by['fwd'] / f / 1e6:7.0f} GB/s, "
              f"{100 * by['fwd'] / f / 1e6 / HBM_PEAK_GBS:5.1f}%)"]
@@ -212,7 +223,9 @@ def summary_line(r):
     if fk:
         parts.append(f"k_fwd {fk * 1e3:7.1f} us")
     if bk:
-        parts.append(f"k_bwd {bk * 1e3:7.1f} us")
+        ph = r["bwd_kernel"]
+        parts.append(f"bwd {bk * 1e3:7.1f} us [q {ph['query_kernel']['mean'] * 1e3:.1f} sort {ph['sort']['mean'] * 1e3:.1f} "
+                     f"bins {ph['bin_offsets']['mean'] * 1e3:.1f} v {ph['value_kernel']['mean'] * 1e3:.1f}]")
     parts.append(f"{samples / (s or f) / 1e6:.3g} Gsamples/s" if (s or f) else "")
     return " | ".join(parts)
 
@@ -266,9 +279,25 @@ def main():
     log(summary_line(r))
     by = r["bytes"]
     ms_step = r["step"]["total_ms"] / args.steps
-    kf, kb = r["fwd_kernel"]["mean"], r["bwd_kernel"]["mean"]
-    dominant, kms, kbytes = ("fda_backward_kernel", kb, by["bwd"]) if kb >= kf else ("fda_forward_kernel", kf, by["fwd"])
+    ph = r["bwd_kernel"]
+    e = 2 if w.dtype in ("bf16", "fp16") else 4
+    V, R, O = w.B * w.S * w.G * w.D * e, w.B * w.nq * w.G * w.P * e, w.B * w.nq * w.G * w.D * e
+    # per-kernel algorithmic bytes (each API tensor the kernel must touch, once):
+    #   forward: read value + sampling_loc_attn, write output
+    #   backward query kernel: read value + sampling_loc_attn + grad_output, write grad_sampling_loc_attn
+    #   backward value kernel: read grad_output, write grad_value
+    kern = {
+        "fda_forward_kernel": (r["fwd_kernel"]["mean"], V + R + O),
+        "fda_bwd_query_kernel": (ph["query_kernel"]["mean"], V + 2 * R + O),
+        "fda_bwd_value_kernel": (ph["value_kernel"]["mean"], O + V),
+        "radix_sort": (ph["sort"]["mean"], None),
+    }
+    dominant = max(kern, key=lambda k: kern[k][0])
+    kms, kbytes = kern[dominant]
+    if kbytes is None:  # the sort moves only internal keys; report the backward as a whole
+        dominant, kms, kbytes = "backward (all phases)", ph["total"]["mean"], by["bwd"]
     achieved = kbytes / (kms * 1e-3) / 1e9
+    kf, kb = r["fwd_kernel"]["mean"], ph["total"]["mean"]
     traffic = _traffic_from_profiles(dominant, w.name)
     line = {
         "metric": METRIC,
@@ -294,7 +323,8 @@ def main():
         "fwd_ms_median": round(r["fwd"]["median"], 5),
         "frac_of_hbm_peak": round(by["total"] / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "qhs_per_s": round(w.samples() / (ms_step * 1e-3), 1),
-        "kernels_us": {"fda_forward_kernel": round(kf * 1e3, 2), "fda_backward_kernel": round(kb * 1e3, 2)},
+        "kernels_us": {**{k: round(v[0] * 1e3, 2) for k, v in kern.items()},
+                       "bin_offsets": round(ph["bin_offsets"]["mean"] * 1e3, 2), "backward_total": round(kb * 1e3, 2)},
         "roofline": {
             "kernel": dominant,
             "bound": "hbm",

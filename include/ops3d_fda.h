@@ -67,19 +67,24 @@ OPS3D_FDA_API int ops3d_fda_forward(const void *value, const int64_t *spatial_sh
                       int im2col_step, void *stream);
 
 /*
- * Bytes of device workspace ops3d_fda_backward needs: an fp32 [B,S,G,D] accumulator for
- * grad_value when dtype is f16/bf16, 0 for f32 (the fp32 output is accumulated in place).
+ * Bytes of device workspace ops3d_fda_backward / ops3d_fda_backward_accumulate_f32 need (0 on
+ * invalid sizes, or when no HIP device is present to size the sort for): per sample (N = B*Q*G*L*K) a sort key, an index and a 16-byte stash, their
+ * sorted copies, per spatial bin (<= 8*B*G*S) a start offset, and the radix sort's temporary
+ * storage.  The pointer passed must be 256-byte aligned.
  */
 OPS3D_FDA_API size_t ops3d_fda_backward_workspace_bytes(int dtype, int batch, int spatial_size,
-                                          int num_heads, int channels);
+                                                        int num_heads, int channels,
+                                                        int num_levels, int num_query,
+                                                        int num_point);
 
 /*
  * Backward.  Replaces flash_deform_attn_backward (reference csrc/flash_deform_attn.h:27-52 ->
  * csrc/cuda/flash_deform_attn_cuda.cu:93-179).  Writes every element of grad_value and
- * grad_sampling_loc_attn in `dtype` (the caller need not zero them).  grad_value is accumulated
- * in fp32 (in `workspace`, at least ops3d_fda_backward_workspace_bytes() bytes, or in place
- * for f32) and converted once at the end.  Samples whose pixel coordinate lies outside
- * [-1, size) on any axis contribute nothing and get zero location gradients.
+ * grad_sampling_loc_attn in `dtype` (the caller need not zero them).  grad_value is a gather:
+ * the samples are sorted by base corner (in `workspace`, at least
+ * ops3d_fda_backward_workspace_bytes() bytes) and each grad_value row is summed in fp32 by one
+ * owner and written once, so the result is deterministic.  Samples whose pixel coordinate lies
+ * outside [-1, size) on any axis contribute nothing and get zero location gradients.
  */
 OPS3D_FDA_API int ops3d_fda_backward(const void *value, const int64_t *spatial_shapes,
                        const int64_t *level_start_index, const void *sampling_loc_attn,
@@ -90,20 +95,30 @@ OPS3D_FDA_API int ops3d_fda_backward(const void *value, const int64_t *spatial_s
                        void *stream);
 
 /*
- * Backward kernel only, accumulating into a caller-owned fp32 grad_value buffer
- * ([B,S,G,D] fp32, NOT cleared: contributions are added to what it holds).
- * grad_sampling_loc_attn is written in full in `dtype`.  No counterpart in the reference
- * (its backward always zero-fills an fp32 buffer and casts it, flash_deform_attn_cuda.cu:
- * 139-178); for callers that sum grad_value over several calls (micro-batches, several
- * query sets attending the same value) or that want fp32 value gradients, and for timing
- * the backward kernel alone.  Atomics make the summation order, hence the last bits of
- * grad_value, nondeterministic.
+ * Backward that ADDS the value gradient into a caller-owned fp32 buffer grad_value_f32
+ * ([B,S,G,D] fp32, not cleared) instead of writing it in `dtype`; grad_sampling_loc_attn is
+ * written in full in `dtype`.  Same workspace as ops3d_fda_backward.  No counterpart in the
+ * reference (its backward always returns freshly zeroed-and-cast gradients,
+ * flash_deform_attn_cuda.cu:139-178); for callers that sum value gradients over several calls
+ * (micro-batches, several query sets attending the same value) or want them in fp32.
  */
 OPS3D_FDA_API int ops3d_fda_backward_accumulate_f32(
     const void *value, const int64_t *spatial_shapes, const int64_t *level_start_index,
     const void *sampling_loc_attn, const void *grad_output, float *grad_value_f32,
-    void *grad_sampling_loc_attn, int dtype, int batch, int spatial_size, int num_heads,
-    int channels, int num_levels, int num_query, int num_point, int im2col_step, void *stream);
+    void *grad_sampling_loc_attn, void *workspace, size_t workspace_bytes, int dtype, int batch,
+    int spatial_size, int num_heads, int channels, int num_levels, int num_query, int num_point,
+    int im2col_step, void *stream);
+
+/*
+ * Phase timing of the backward (no counterpart in the reference; for benchmarks and
+ * profilers).  After ops3d_fda_profile_enable(1), every backward call records HIP events on
+ * its stream around its phases; ops3d_fda_profile_read() waits for the last call to finish and
+ * writes up to n durations in ms: [0] query-major kernel, [1] sort, [2] bin offsets,
+ * [3] value-gradient kernel.  Returns the number written (0 if nothing was recorded).
+ * Process-wide state, not thread-safe; enable on the device the calls run on.
+ */
+OPS3D_FDA_API int ops3d_fda_profile_enable(int on);
+OPS3D_FDA_API int ops3d_fda_profile_read(float *ms, int n);
 
 #ifdef __cplusplus
 }

@@ -35,6 +35,8 @@ EXPORTED_SYMBOLS = (
     "ops3d_fda_backward_workspace_bytes",
     "ops3d_fda_backward",
     "ops3d_fda_backward_accumulate_f32",
+    "ops3d_fda_profile_enable",
+    "ops3d_fda_profile_read",
 )
 
 
@@ -48,11 +50,15 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ops3d_fda_forward.restype = _i
     lib.ops3d_fda_forward.argtypes = [_vp, _vp, _vp, _vp, _vp] + [_i] * 9 + [_vp]
     lib.ops3d_fda_backward_workspace_bytes.restype = _sz
-    lib.ops3d_fda_backward_workspace_bytes.argtypes = [_i] * 5
+    lib.ops3d_fda_backward_workspace_bytes.argtypes = [_i] * 8
     lib.ops3d_fda_backward.restype = _i
     lib.ops3d_fda_backward.argtypes = [_vp] * 8 + [_sz] + [_i] * 9 + [_vp]
+    lib.ops3d_fda_profile_enable.restype = _i
+    lib.ops3d_fda_profile_enable.argtypes = [_i]
+    lib.ops3d_fda_profile_read.restype = _i
+    lib.ops3d_fda_profile_read.argtypes = [ctypes.POINTER(ctypes.c_float), _i]
     lib.ops3d_fda_backward_accumulate_f32.restype = _i
-    lib.ops3d_fda_backward_accumulate_f32.argtypes = [_vp] * 7 + [_i] * 9 + [_vp]
+    lib.ops3d_fda_backward_accumulate_f32.argtypes = [_vp] * 8 + [_sz] + [_i] * 9 + [_vp]
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -62,7 +68,7 @@ def _ptr(t: torch.Tensor | None) -> int | None:
 class _NativeFDA:
     """Host side of the flash-deform-attn extension, bound to libops3d_fda.so."""
 
-    ABI_VERSION = 1
+    ABI_VERSION = 2
 
     def __init__(self, lib: ctypes.CDLL, path: str):
         self._lib = lib
@@ -160,8 +166,7 @@ class _NativeFDA:
         code = _DTYPE_CODE[value.dtype]
         grad_value = torch.empty_like(value)
         grad_sla = torch.empty_like(sampling_loc_attn)
-        ws_bytes = self._lib.ops3d_fda_backward_workspace_bytes(code, B, S, G, D)
-        ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=value.device) if ws_bytes else None
+        ws, ws_bytes = self._workspace(code, B, S, G, D, L, Q, K, value.device)
         stream = torch.cuda.current_stream(value.device).cuda_stream
         with torch.cuda.device(value.device):
             rc = self._lib.ops3d_fda_backward(
@@ -173,11 +178,17 @@ class _NativeFDA:
             self._raise(rc, "flash_deform_attn_backward failed")
         return [grad_value, grad_sla]
 
+    def _workspace(self, code, B, S, G, D, L, Q, K, device):
+        n = self._lib.ops3d_fda_backward_workspace_bytes(code, B, S, G, D, L, Q, int(K))
+        if n == 0:
+            return None, 0
+        return torch.empty(n, dtype=torch.uint8, device=device), n
+
     def flash_deform_attn_backward_accumulate(
         self, value, spatial_shapes, level_start_index, sampling_loc_attn, grad_output,
         grad_value_f32, im2col_step, K,
     ):
-        """Backward kernel only: adds value gradients into the fp32 tensor ``grad_value_f32``
+        """Backward that adds the value gradient into the fp32 tensor ``grad_value_f32``
         ([B,S,G,D], not cleared) and returns a new grad_sampling_loc_attn (value dtype)."""
         B, S, G, D, L, Q = self._common(
             value, spatial_shapes, level_start_index, sampling_loc_attn, K, {"grad_output": grad_output}
@@ -186,16 +197,30 @@ class _NativeFDA:
             raise ValueError("grad_value_f32 must be an fp32 tensor shaped like value")
         self._check_inputs({"grad_value_f32": grad_value_f32}, value)
         grad_sla = torch.empty_like(sampling_loc_attn)
+        code = _DTYPE_CODE[value.dtype]
+        ws, ws_bytes = self._workspace(code, B, S, G, D, L, Q, K, value.device)
         stream = torch.cuda.current_stream(value.device).cuda_stream
         with torch.cuda.device(value.device):
             rc = self._lib.ops3d_fda_backward_accumulate_f32(
                 _ptr(value), _ptr(spatial_shapes), _ptr(level_start_index), _ptr(sampling_loc_attn),
-                _ptr(grad_output), _ptr(grad_value_f32), _ptr(grad_sla),
-                _DTYPE_CODE[value.dtype], B, S, G, D, L, Q, int(K), int(im2col_step), stream,
+                _ptr(grad_output), _ptr(grad_value_f32), _ptr(grad_sla), _ptr(ws), ws_bytes,
+                code, B, S, G, D, L, Q, int(K), int(im2col_step), stream,
             )
         if rc != OPS3D_FDA_OK:
             self._raise(rc, "flash_deform_attn_backward_accumulate failed")
         return grad_sla
+
+    def profile_enable(self, on: bool = True) -> None:
+        """Record HIP events around the backward phases of every following call."""
+        if self._lib.ops3d_fda_profile_enable(1 if on else 0) != OPS3D_FDA_OK:
+            self._raise(OPS3D_FDA_ERUNTIME, "profile_enable failed")
+
+    def profile_read(self) -> dict:
+        """Phase durations (ms) of the last backward call (waits for it to finish)."""
+        buf = (ctypes.c_float * 4)()
+        n = self._lib.ops3d_fda_profile_read(buf, 4)
+        names = ("query_kernel", "sort", "bin_offsets", "value_kernel")
+        return {names[i]: buf[i] for i in range(n)}
 
     def supported(self, dtype: torch.dtype, channels: int) -> bool:
         return dtype in _DTYPE_CODE and bool(self._lib.ops3d_fda_supported(_DTYPE_CODE[dtype], int(channels)))

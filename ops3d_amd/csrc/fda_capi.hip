@@ -1,4 +1,4 @@
-// C ABI of libops3d_fda.so: argument validation, launch geometry and the two entry points.
+// C ABI of libops3d_fda.so: argument validation, launch geometry and the entry points.
 //
 // Replaces the ATen host code of the reference (csrc/cuda/flash_deform_attn_cuda.cu:20-179)
 // and its template launchers (flash_deform_im2col_cuda.cuh:298-593,
@@ -8,20 +8,25 @@
 //     hints are accepted by the Python layer and ignored;
 //   * the whole batch is one launch: im2col_step chunking gives identical results, so it is
 //     only validated (min(B, step) must divide B, as flash_deform_attn_cuda.cu:56-58);
-//   * outputs are written in full by the kernels (no zero-fill of output / grad_offset), and
-//     only the fp32 grad_value accumulator is cleared and converted.
+//   * outputs are written in full by the kernels, in the value dtype: no zero-fill of output,
+//     grad_offset or grad_value and no fp32 -> dtype cast passes;
+//   * grad_value is a gather, not a scatter: the backward sorts its samples by base corner
+//     and every grad_value row is summed by one owner (fp32 global atomics on gfx950 run at
+//     ~0.5 lanes/clock per CU, far below what 8 corners x D channels per sample need).
 #include <stdarg.h>
 #include <stdio.h>
 
 #include <string>
 
+#include <hipcub/hipcub.hpp>
+
 #include "../../include/ops3d_fda.h"
 #include "fda_device.h"
 
 namespace ops3d_fda {
-hipError_t launch_f32(bool, int, int, const Args &, unsigned, size_t, hipStream_t);
-hipError_t launch_f16(bool, int, int, const Args &, unsigned, size_t, hipStream_t);
-hipError_t launch_bf16(bool, int, int, const Args &, unsigned, size_t, hipStream_t);
+hipError_t launch_f32(int, int, int, const Args &, unsigned, size_t, hipStream_t);
+hipError_t launch_f16(int, int, int, const Args &, unsigned, size_t, hipStream_t);
+hipError_t launch_bf16(int, int, int, const Args &, unsigned, size_t, hipStream_t);
 }  // namespace ops3d_fda
 
 using namespace ops3d_fda;
@@ -29,6 +34,16 @@ using namespace ops3d_fda;
 namespace {
 
 thread_local std::string g_last_error;
+
+// backward phase timing (ops3d_fda_profile_*)
+bool g_prof_on = false;
+bool g_prof_recorded = false;
+hipEvent_t g_prof_ev[5];
+bool g_prof_created = false;
+
+void prof_mark(int i, hipStream_t st) {
+  if (g_prof_on) (void)hipEventRecord(g_prof_ev[i], st);
+}
 
 int fail(int code, const char *fmt, ...) {
   char buf[512];
@@ -128,51 +143,98 @@ int common_checks(int dtype, int B, int S, int G, int D, int L, int Q, int K, in
 
 bool misaligned(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 3u) != 0; }
 
-hipError_t launch(int dtype, bool backward, const Geometry &g, hipStream_t st) {
+hipError_t launch(int dtype, int which, const Geometry &g, hipStream_t st) {
   switch (dtype) {
-    case OPS3D_FDA_F32: return launch_f32(backward, g.cpl, g.lpu, g.a, g.grid, g.lds, st);
-    case OPS3D_FDA_F16: return launch_f16(backward, g.cpl, g.lpu, g.a, g.grid, g.lds, st);
-    default: return launch_bf16(backward, g.cpl, g.lpu, g.a, g.grid, g.lds, st);
+    case OPS3D_FDA_F32: return launch_f32(which, g.cpl, g.lpu, g.a, g.grid, g.lds, st);
+    case OPS3D_FDA_F16: return launch_f16(which, g.cpl, g.lpu, g.a, g.grid, g.lds, st);
+    default: return launch_bf16(which, g.cpl, g.lpu, g.a, g.grid, g.lds, st);
   }
 }
 
-// Fill n floats with zero (a kernel, not hipMemsetAsync, so a captured graph replays correctly).
-__global__ __launch_bounds__(256) void zero_f32_kernel(float *p, int64_t n) {
-  const int64_t n4 = n >> 2;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride)
-    reinterpret_cast<float4 *>(p)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t < (n & 3)) p[(n4 << 2) + t] = 0.f;
+// XCD-aware grid over (b, g, column) for `ncol_per_b` columns per batch item (see map_tile).
+void set_grid(Args &a, int ncol_per_b, unsigned &grid_out) {
+  a.nqb = ncol_per_b;
+  a.ncol = a.B * ncol_per_b;
+  int64_t grid;
+  if (a.xcd_mode == 0) grid = (int64_t)a.G * a.ncol;
+  else if (a.xcd_mode == 1) grid = 8 * (((int64_t)a.ncol + a.xpg - 1) / a.xpg);
+  else grid = (int64_t)a.G * a.ncol;
+  grid_out = (unsigned)grid;
 }
 
-// fp32 -> T, 4 elements per thread and step.
-template <typename T>
-__global__ __launch_bounds__(256) void convert_kernel(const float *src, T *dst, int64_t n) {
-  const int64_t n4 = n >> 2;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
-    const float4 v = reinterpret_cast<const float4 *>(src)[i];
-    const float f[4] = {v.x, v.y, v.z, v.w};
-    const uint32_t w0 = Elem<T>::pack(f), w1 = Elem<T>::pack(f + 2);
-    reinterpret_cast<u32x2 *>(dst)[i] = u32x2{w0, w1};
+// Workspace of the backward gather (all offsets 256-byte aligned):
+//   keys_in, keys_out, vals_in, vals_out : N uint32 each, N = B*Q*G*L*K samples
+//   stash                               : N float4
+//   bin_start                           : nbins_bound + 1 uint32
+//   sort temporary storage              : as hipcub reports
+// nbins_bound = B*G*8*S bounds the real bin count sum_l (D+1)(H+1)(W+1) without reading the
+// device-resident level shapes on the host.
+struct BwdLayout {
+  uint64_t n, nbins_bound;
+  int key_bits;
+  size_t off_keys_in, off_keys_out, off_vals_in, off_vals_out, off_stash, off_bins, off_temp;
+  size_t temp_bytes, total;
+};
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+int bwd_layout(int B, int S, int G, int L, int Q, int K, BwdLayout &ly) {
+  ly = BwdLayout{};
+  ly.n = (uint64_t)B * Q * G * L * K;
+  ly.nbins_bound = (uint64_t)B * G * 8 * (uint64_t)S;
+  if (ly.n >= 0xffffffffull || ly.nbins_bound >= 0xfffffff0ull)
+    return fail(OPS3D_FDA_EINVAL, "backward too large for 32-bit sample/bin indices (N=%llu, bins<=%llu)",
+                (unsigned long long)ly.n, (unsigned long long)ly.nbins_bound);
+  int bits = 1;
+  while (bits < 32 && (ly.nbins_bound >> bits) != 0) ++bits;
+  ly.key_bits = bits;
+  size_t temp = 0;
+  if (ly.n > 0) {
+    hipError_t e = hipcub::DeviceRadixSort::SortPairs(nullptr, temp, (uint32_t *)nullptr, (uint32_t *)nullptr,
+                                                      (uint32_t *)nullptr, (uint32_t *)nullptr, (int)ly.n, 0,
+                                                      bits, (hipStream_t)0);
+    if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "radix sort size query failed: %s", hipGetErrorString(e));
   }
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t < (n & 3)) dst[(n4 << 2) + t] = (T)src[(n4 << 2) + t];
+  ly.temp_bytes = temp;
+  size_t o = 0;
+  const size_t n4 = align256(ly.n * 4);
+  ly.off_keys_in = o; o += n4;
+  ly.off_keys_out = o; o += n4;
+  ly.off_vals_in = o; o += n4;
+  ly.off_vals_out = o; o += n4;
+  ly.off_stash = o; o += align256(ly.n * 16);
+  ly.off_bins = o; o += align256((ly.nbins_bound + 1) * 4);
+  ly.off_temp = o; o += align256(temp);
+  ly.total = o;
+  return OPS3D_FDA_OK;
 }
 
-unsigned elementwise_grid(int64_t n) {
-  int64_t blocks = ((n >> 2) + 255) / 256;
-  if (blocks < 1) blocks = 1;
-  if (blocks > 8192) blocks = 8192;
-  return (unsigned)blocks;
+// bin_start[b] = first position of key >= b in the sorted keys, for b in [0, nbins_real],
+// nbins_real = B*G*sum_l (D+1)(H+1)(W+1) read from the device-resident level shapes.
+__global__ __launch_bounds__(256) void bin_start_kernel(const uint32_t *keys, uint32_t n, uint32_t *bin_start,
+                                                        uint32_t nbins_bound, const int64_t *shapes, int L,
+                                                        int BG) {
+  uint32_t per = 0;
+  for (int l = 0; l < L; ++l) per += level_bins(shapes, l);
+  const uint64_t real = (uint64_t)per * (uint64_t)BG;
+  const uint64_t last = real < nbins_bound ? real : nbins_bound;
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t bb = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; bb <= last; bb += stride) {
+    uint32_t lo = 0, hi = n;
+    while (lo < hi) {
+      const uint32_t mid = (lo + hi) >> 1;
+      if (keys[mid] < (uint32_t)bb) lo = mid + 1;
+      else hi = mid;
+    }
+    bin_start[bb] = lo;
+  }
 }
 
 }  // namespace
 
 extern "C" {
 
-int ops3d_fda_abi_version(void) { return 1; }
+int ops3d_fda_abi_version(void) { return 2; }
 
 const char *ops3d_fda_last_error(void) { return g_last_error.c_str(); }
 
@@ -210,60 +272,132 @@ int ops3d_fda_forward(const void *value, const int64_t *spatial_shapes,
 }
 
 size_t ops3d_fda_backward_workspace_bytes(int dtype, int batch, int spatial_size, int num_heads,
-                                          int channels) {
-  if (dtype == OPS3D_FDA_F32 || batch <= 0 || spatial_size <= 0 || num_heads <= 0 || channels <= 0)
+                                          int channels, int num_levels, int num_query, int num_point) {
+  if (elem_size(dtype) == 0 || batch < 0 || spatial_size < 0 || num_heads <= 0 || channels <= 0 ||
+      num_levels < 1 || num_query < 0 || num_point < 1)
     return 0;
-  return (size_t)batch * spatial_size * num_heads * channels * sizeof(float);
+  BwdLayout ly;
+  if (bwd_layout(batch, spatial_size, num_heads, num_levels, num_query, num_point, ly)) return 0;
+  return ly.total;
 }
 
 static int backward_impl(const void *value, const int64_t *spatial_shapes,
                          const int64_t *level_start_index, const void *sampling_loc_attn,
-                         const void *grad_output, float *acc, void *grad_sampling_loc_attn,
+                         const void *grad_output, void *grad_value, bool out_f32_accumulate,
+                         void *grad_sampling_loc_attn, void *workspace, size_t workspace_bytes,
                          int dtype, int batch, int spatial_size, int num_heads, int channels,
                          int num_levels, int num_query, int num_point, int im2col_step,
-                         hipStream_t st, bool zero_first, void *convert_to) {
+                         hipStream_t st) {
   Geometry geo;
   int rc = common_checks(dtype, batch, spatial_size, num_heads, channels, num_levels, num_query,
                          num_point, im2col_step, true, geo);
   if (rc) return rc;
+  BwdLayout ly;
+  rc = bwd_layout(batch, spatial_size, num_heads, num_levels, num_query, num_point, ly);
+  if (rc) return rc;
   const int64_t nval = (int64_t)batch * spatial_size * num_heads * channels;
   const bool work = (int64_t)batch * num_query > 0;
-  if (nval > 0 && !acc) return fail(OPS3D_FDA_EINVAL, "grad_value is NULL");
-  if (work && (!spatial_shapes || !level_start_index || !sampling_loc_attn || !grad_output ||
-               !grad_sampling_loc_attn || (!value && spatial_size > 0)))
+  if (nval == 0 && !work) return OPS3D_FDA_OK;
+  if (nval > 0 && !grad_value) return fail(OPS3D_FDA_EINVAL, "grad_value is NULL");
+  if (!spatial_shapes || !level_start_index) return fail(OPS3D_FDA_EINVAL, "NULL pointer argument");
+  if (work && (!sampling_loc_attn || !grad_output || !grad_sampling_loc_attn || (!value && spatial_size > 0)))
     return fail(OPS3D_FDA_EINVAL, "NULL pointer argument");
+  if (!workspace || workspace_bytes < ly.total)
+    return fail(OPS3D_FDA_EINVAL, "workspace too small: %zu bytes given, %zu needed", workspace_bytes, ly.total);
   if (misaligned(value) || misaligned(sampling_loc_attn) || misaligned(grad_output) ||
-      misaligned(grad_sampling_loc_attn) || misaligned(acc) || misaligned(convert_to))
+      misaligned(grad_sampling_loc_attn) || misaligned(grad_value))
     return fail(OPS3D_FDA_EINVAL, "tensor data pointers must be 4-byte aligned");
-  if (zero_first && nval > 0) {
-    hipLaunchKernelGGL(zero_f32_kernel, dim3(elementwise_grid(nval)), dim3(256), 0, st, acc, nval);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "zero-fill launch failed: %s", hipGetErrorString(e));
-  }
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+    return fail(OPS3D_FDA_EINVAL, "workspace must be 256-byte aligned");
+
+  char *ws = static_cast<char *>(workspace);
+  uint32_t *keys_in = reinterpret_cast<uint32_t *>(ws + ly.off_keys_in);
+  uint32_t *keys_out = reinterpret_cast<uint32_t *>(ws + ly.off_keys_out);
+  uint32_t *vals_in = reinterpret_cast<uint32_t *>(ws + ly.off_vals_in);
+  uint32_t *vals_out = reinterpret_cast<uint32_t *>(ws + ly.off_vals_out);
+  float4 *stash = reinterpret_cast<float4 *>(ws + ly.off_stash);
+  uint32_t *bins = reinterpret_cast<uint32_t *>(ws + ly.off_bins);
+  void *temp = ws + ly.off_temp;
+
+  Args &a = geo.a;
+  a.value = value;
+  a.shapes = spatial_shapes;
+  a.lsi = level_start_index;
+  a.loc_attn = sampling_loc_attn;
+  a.grad_out = grad_output;
+  a.grad_loc_attn = grad_sampling_loc_attn;
+  a.keys = keys_in;
+  a.vals = vals_in;
+  a.stash = stash;
+  a.key_invalid = (uint32_t)ly.nbins_bound;
+  a.inv_lk = 1.0 / (double)(num_levels * num_point);
+  hipError_t e;
+  prof_mark(0, st);
   if (work) {
-    geo.a.value = value;
-    geo.a.shapes = spatial_shapes;
-    geo.a.lsi = level_start_index;
-    geo.a.loc_attn = sampling_loc_attn;
-    geo.a.grad_out = grad_output;
-    geo.a.grad_value = acc;
-    geo.a.grad_loc_attn = grad_sampling_loc_attn;
-    hipError_t e = launch(dtype, true, geo, st);
+    // phase 1: location / logit gradients, per-sample bin keys and stash
+    e = launch(dtype, 1, geo, st);
     if (e != hipSuccess)
-      return fail(OPS3D_FDA_ERUNTIME, "backward kernel launch failed: %s (grid=%u, lds=%zu)",
+      return fail(OPS3D_FDA_ERUNTIME, "backward query kernel launch failed: %s (grid=%u, lds=%zu)",
                   hipGetErrorString(e), geo.grid, geo.lds);
+    prof_mark(1, st);
+    // phase 2: stable radix sort of (bin, sample) pairs
+    size_t tb = ly.temp_bytes;
+    e = hipcub::DeviceRadixSort::SortPairs(temp, tb, keys_in, keys_out, vals_in, vals_out, (int)ly.n, 0,
+                                           ly.key_bits, st);
+    if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "radix sort failed: %s", hipGetErrorString(e));
+  } else {
+    prof_mark(1, st);
   }
-  if (convert_to && nval > 0) {
-    if (dtype == OPS3D_FDA_F16)
-      hipLaunchKernelGGL(convert_kernel<_Float16>, dim3(elementwise_grid(nval)), dim3(256), 0, st,
-                         acc, static_cast<_Float16 *>(convert_to), nval);
-    else
-      hipLaunchKernelGGL(convert_kernel<__bf16>, dim3(elementwise_grid(nval)), dim3(256), 0, st,
-                         acc, static_cast<__bf16 *>(convert_to), nval);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "convert launch failed: %s", hipGetErrorString(e));
+  prof_mark(2, st);
+  {
+    const uint64_t nb = ly.nbins_bound + 1;
+    unsigned blocks = (unsigned)((nb + 255) / 256);
+    if (blocks > 16384) blocks = 16384;
+    hipLaunchKernelGGL(bin_start_kernel, dim3(blocks), dim3(256), 0, st, keys_out, work ? (uint32_t)ly.n : 0u,
+                       bins, (uint32_t)ly.nbins_bound, spatial_shapes, num_levels, batch * num_heads);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "bin kernel launch failed: %s", hipGetErrorString(e));
   }
+  prof_mark(3, st);
+  if (nval > 0) {
+    // phase 3: one owner per grad_value row, gathered from 8 bins, written once
+    Geometry g3 = geo;
+    const int UPB = kWavesPerBlock * (kWave / geo.lpu);
+    const int nvb_bound = (int)(((int64_t)spatial_size + UPB - 1) / UPB) + num_levels;
+    set_grid(g3.a, nvb_bound, g3.grid);
+    g3.a.sorted_vals = vals_out;
+    g3.a.bin_start = bins;
+    g3.a.out = grad_value;
+    g3.a.accumulate = out_f32_accumulate ? 1 : 0;
+    g3.lds = 0;
+    e = launch(dtype, 2, g3, st);
+    if (e != hipSuccess)
+      return fail(OPS3D_FDA_ERUNTIME, "backward value kernel launch failed: %s (grid=%u)", hipGetErrorString(e),
+                  g3.grid);
+  }
+  prof_mark(4, st);
+  if (g_prof_on) g_prof_recorded = true;
   return OPS3D_FDA_OK;
+}
+
+int ops3d_fda_profile_enable(int on) {
+  if (on && !g_prof_created) {
+    for (int i = 0; i < 5; ++i)
+      if (hipEventCreate(&g_prof_ev[i]) != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "hipEventCreate failed");
+    g_prof_created = true;
+  }
+  g_prof_on = on != 0;
+  g_prof_recorded = false;
+  return OPS3D_FDA_OK;
+}
+
+int ops3d_fda_profile_read(float *ms, int n) {
+  if (!g_prof_recorded || !ms) return 0;
+  if (hipEventSynchronize(g_prof_ev[4]) != hipSuccess) return 0;
+  int k = 0;
+  for (int i = 0; i < 4 && k < n; ++i, ++k)
+    if (hipEventElapsedTime(&ms[k], g_prof_ev[i], g_prof_ev[i + 1]) != hipSuccess) ms[k] = -1.f;
+  return k;
 }
 
 int ops3d_fda_backward(const void *value, const int64_t *spatial_shapes,
@@ -274,31 +408,24 @@ int ops3d_fda_backward(const void *value, const int64_t *spatial_shapes,
                        int num_levels, int num_query, int num_point, int im2col_step,
                        void *stream) {
   g_last_error.clear();
-  if (elem_size(dtype) == 0) return fail(OPS3D_FDA_EINVAL, "unsupported dtype code %d", dtype);
-  const size_t need = ops3d_fda_backward_workspace_bytes(dtype, batch, spatial_size, num_heads, channels);
-  if (need > 0 && (!workspace || workspace_bytes < need))
-    return fail(OPS3D_FDA_EINVAL, "workspace too small: %zu bytes given, %zu needed", workspace_bytes, need);
-  const bool f32 = dtype == OPS3D_FDA_F32;
-  float *acc = f32 ? static_cast<float *>(grad_value) : static_cast<float *>(workspace);
-  if (!f32 && need > 0 && !grad_value) return fail(OPS3D_FDA_EINVAL, "grad_value is NULL");
-  return backward_impl(value, spatial_shapes, level_start_index, sampling_loc_attn, grad_output, acc,
-                       grad_sampling_loc_attn, dtype, batch, spatial_size, num_heads, channels,
-                       num_levels, num_query, num_point, im2col_step, static_cast<hipStream_t>(stream),
-                       true, f32 ? nullptr : grad_value);
+  return backward_impl(value, spatial_shapes, level_start_index, sampling_loc_attn, grad_output, grad_value,
+                       false, grad_sampling_loc_attn, workspace, workspace_bytes, dtype, batch, spatial_size,
+                       num_heads, channels, num_levels, num_query, num_point, im2col_step,
+                       static_cast<hipStream_t>(stream));
 }
 
 int ops3d_fda_backward_accumulate_f32(const void *value, const int64_t *spatial_shapes,
                                       const int64_t *level_start_index,
                                       const void *sampling_loc_attn, const void *grad_output,
                                       float *grad_value_f32, void *grad_sampling_loc_attn,
-                                      int dtype, int batch, int spatial_size, int num_heads,
-                                      int channels, int num_levels, int num_query, int num_point,
-                                      int im2col_step, void *stream) {
+                                      void *workspace, size_t workspace_bytes, int dtype, int batch,
+                                      int spatial_size, int num_heads, int channels, int num_levels,
+                                      int num_query, int num_point, int im2col_step, void *stream) {
   g_last_error.clear();
   return backward_impl(value, spatial_shapes, level_start_index, sampling_loc_attn, grad_output,
-                       grad_value_f32, grad_sampling_loc_attn, dtype, batch, spatial_size, num_heads,
-                       channels, num_levels, num_query, num_point, im2col_step,
-                       static_cast<hipStream_t>(stream), false, nullptr);
+                       grad_value_f32, true, grad_sampling_loc_attn, workspace, workspace_bytes, dtype, batch,
+                       spatial_size, num_heads, channels, num_levels, num_query, num_point, im2col_step,
+                       static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -42,6 +42,15 @@ struct Args {
   void *out;                  // [B,Q,G*D] T          (forward)
   float *grad_value;          // [B,S,G,D] fp32 acc   (backward)
   void *grad_loc_attn;        // [B,Q,G,P] T          (backward)
+  // backward, gather formulation of grad_value
+  uint32_t *keys;             // [N] bin of each sample's base corner (key_invalid if skipped)
+  uint32_t *vals;             // [N] sample index (iota), sort payload
+  float4 *stash;              // [N] (fx, fy, fz, attn) of each sample
+  const uint32_t *sorted_vals;  // [N] sample indices sorted by bin
+  const uint32_t *bin_start;    // [nbins_bound + 1] first sorted position of each bin
+  uint32_t key_invalid;       // = nbins_bound, sorts after every real bin
+  int accumulate;             // phase 3: add into grad_value instead of overwriting
+  double inv_lk;              // 1.0 / (L*K), for sample -> unit
   int B, S, G, D, L, K, Q, P;
   int nqb;                    // query blocks per batch = ceil(Q / UPB)
   int ncol;                   // B * nqb
@@ -296,6 +305,7 @@ __device__ __forceinline__ float pixel_coord(float loc, float size) {
 struct Sample {
   uint32_t off[8];   // element offsets (voxel*G*D) inside the level, OOB_ELEM if outside
   float wx[2], wy[2], wz[2];
+  int x0, y0, z0;    // base corner (may be -1)
 };
 
 // Returns false when every corner lies outside the volume (coordinate outside [-1, size) on some
@@ -309,6 +319,7 @@ __device__ __forceinline__ bool sample_setup(float lx, float ly, float lz, int W
     return false;
   const float x0f = floorf(x), y0f = floorf(y), z0f = floorf(z);
   const int x0 = (int)x0f, y0 = (int)y0f, z0 = (int)z0f;
+  sm.x0 = x0; sm.y0 = y0; sm.z0 = z0;
   sm.wx[1] = x - x0f; sm.wx[0] = (x0f + 1.f) - x;
   sm.wy[1] = y - y0f; sm.wy[0] = (y0f + 1.f) - y;
   sm.wz[1] = z - z0f; sm.wz[0] = (z0f + 1.f) - z;
@@ -326,6 +337,14 @@ __device__ __forceinline__ bool sample_setup(float lx, float ly, float lz, int W
     sm.off[c] = ok ? oz[dz] + oy[dy] + ox[dx] : OOB_ELEM;
   }
   return true;
+}
+
+// Bins of the backward gather: per (b, g) and level, one bin per possible base corner
+// (x0, y0, z0) in [-1, W) x [-1, H) x [-1, D), i.e. (W+1)(H+1)(D+1) bins (0 for an empty
+// level), <= 8 * D*H*W.  Returns the bins of one (b, g) and the offset of level `lvl`.
+__device__ __forceinline__ uint32_t level_bins(const int64_t *shapes, int l) {
+  const uint32_t d = (uint32_t)shapes[3 * l], h = (uint32_t)shapes[3 * l + 1], w = (uint32_t)shapes[3 * l + 2];
+  return (d == 0 || h == 0 || w == 0) ? 0u : (d + 1) * (h + 1) * (w + 1);
 }
 
 }  // namespace ops3d_fda

@@ -3,11 +3,11 @@
 
 namespace ops3d_fda {
 
-hipError_t launch_f16(bool backward, int cpl, int lpu, const Args &a, unsigned grid, size_t lds,
+hipError_t launch_f16(int which, int cpl, int lpu, const Args &a, unsigned grid, size_t lds,
                      hipStream_t st) {
   switch (cpl) {
-    case 8: return launch_cpl<_Float16, 8>(backward, lpu, a, grid, lds, st);
-    case 12: return launch_cpl<_Float16, 12>(backward, lpu, a, grid, lds, st);
+    case 8: return launch_cpl<_Float16, 8>(which, lpu, a, grid, lds, st);
+    case 12: return launch_cpl<_Float16, 12>(which, lpu, a, grid, lds, st);
     default: return hipErrorInvalidValue;
   }
 }

@@ -4,11 +4,14 @@
 //   out[b,q,g,:] = sum_{l,k} softmax(logits[b,q,g,:])[l,k] *
 //                  trilinear(value_l[b,:,g,:], pixel(loc[b,q,g,l,k]))
 // Backward (replaces backward_kernel_warp_primitive, flash_deform_col2im_cuda.cuh:248-429, and
-// ms_deform_attn_col2im_trilinear, common.h:141-353):
-//   grad_value  += attn * w_corner * grad_out           (fp32 buffer atomics, dropped when OOB)
-//   grad_loc     = attn * size * sum_c grad_out[c] * d(interp_c)/d(pixel)
-//   grad_attn    = sum_c grad_out[c] * interp_c, then softmax backward
-//                  grad_logit_i = a_i * (grad_attn_i - sum_j a_j grad_attn_j)
+// ms_deform_attn_col2im_trilinear, common.h:141-353), in two kernels around a sort:
+//   phase 1 (query-major)  grad_loc  = attn * size * sum_c grad_out[c] * d(interp_c)/d(pixel)
+//                          grad_attn = sum_c grad_out[c] * interp_c, then softmax backward
+//                          grad_logit_i = a_i * (grad_attn_i - sum_j a_j grad_attn_j)
+//                          + per sample: key = bin of its base corner, stash (fx,fy,fz,attn)
+//   phase 2                stable radix sort of (key, sample) pairs
+//   phase 3 (voxel-major)  grad_value[v] = sum over samples s with a corner at v of
+//                          attn_s * w_corner(s) * grad_out[unit(s)]     (register sums, no atomics)
 // The per-sample location/attention partials are formed from U_i = sum_c grad_out[c] * V_i[c]
 // (one dot product per corner) so the channel loop costs one FMA per corner and channel, and
 // are summed over the unit's LPU lanes with DPP / ds_swizzle reductions.
@@ -105,8 +108,10 @@ __global__ __launch_bounds__(kBlock) void fda_forward_kernel(const Args a) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// Backward phase 1, query-major: gradients of the locations and logits of one unit, plus one
+// (bin, sample, stash) record per sample for the value-gradient gather of phase 3.  No atomics.
 template <typename T, int CPL, int LPU>
-__global__ __launch_bounds__(kBlock) void fda_backward_kernel(const Args a) {
+__global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
   extern __shared__ float lds[];
   constexpr int UPW = kWave / LPU, UPB = kWavesPerBlock * UPW;
   int b, g, qb;
@@ -134,23 +139,27 @@ __global__ __launch_bounds__(kBlock) void fda_backward_kernel(const Args a) {
     for (int c = 0; c < CPL; ++c) tg[c] = 0.f;
   }
 
+  uint32_t bins_bg = 0;
+  for (int l = 0; l < L; ++l) bins_bg += level_bins(a.shapes, l);
+  uint32_t bin_base = (uint32_t)(b * a.G + g) * bins_bg;
+
   const int GD = a.G * a.D;
   const uint32_t lane_elem = (uint32_t)(g * a.D + j * CPL);
   const T *vb = static_cast<const T *>(a.value) + (int64_t)b * a.S * GD;
-  float *gvb = a.grad_value + (int64_t)b * a.S * GD;
+  const int64_t gs0 = unit * LK;
   int s = 0;
   for (int l = 0; l < L; ++l) {
     const int Dl = (int)a.shapes[3 * l], Hl = (int)a.shapes[3 * l + 1], Wl = (int)a.shapes[3 * l + 2];
     const int64_t st = a.lsi[l];
     const int64_t nel = (int64_t)Dl * Hl * Wl * GD;
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb + st * GD, (uint32_t)(nel * (int64_t)sizeof(T)));
-    const __amdgpu_buffer_rsrc_t rg = make_rsrc(gvb + st * GD, (uint32_t)(nel * 4));
     for (int k = 0; k < K; ++k, ++s) {
       const float lx = rec[3 * s], ly = rec[3 * s + 1], lz = rec[3 * s + 2];
       const float at = rec[3 * LK + s];
       float gx = 0.f, gy = 0.f, gz = 0.f, ga = 0.f;
       Sample sm;
-      if (live && sample_setup(lx, ly, lz, Wl, Hl, Dl, GD, sm)) {
+      const bool in = live && sample_setup(lx, ly, lz, Wl, Hl, Dl, GD, sm);
+      if (in) {
         float U[8];
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
@@ -164,14 +173,6 @@ __global__ __launch_bounds__(kBlock) void fda_backward_kernel(const Args a) {
         float w[8];
 #pragma unroll
         for (int c = 0; c < 8; ++c) w[c] = (sm.wx[c & 1] * sm.wy[(c >> 1) & 1]) * sm.wz[c >> 2];
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          const float aw = at * w[c];
-          const uint32_t o = (sm.off[c] + lane_elem) * 4u;
-#pragma unroll
-          for (int ch = 0; ch < CPL; ++ch)
-            __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(aw * tg[ch], rg, o + 4u * ch, 0, 0);
-        }
 #pragma unroll
         for (int c = 0; c < 8; ++c) ga = fmaf(w[c], U[c], ga);
         // d w_c / dx = (dx ? +1 : -1) * wy * wz, and likewise for y, z
@@ -201,8 +202,19 @@ __global__ __launch_bounds__(kBlock) void fda_backward_kernel(const Args a) {
         rec[3 * s + 1] = gy * at * (float)Hl;
         rec[3 * s + 2] = gz * at * (float)Dl;
         gat_s[s] = ga;
+        if (live) {
+          const int64_t gsi = gs0 + s;
+          uint32_t key = a.key_invalid;
+          if (in) {
+            key = bin_base + (uint32_t)(((sm.z0 + 1) * (Hl + 1) + (sm.y0 + 1)) * (Wl + 1) + (sm.x0 + 1));
+            a.stash[gsi] = make_float4(sm.wx[1], sm.wy[1], sm.wz[1], at);
+          }
+          a.keys[gsi] = key;
+          a.vals[gsi] = (uint32_t)gsi;
+        }
       }
     }
+    bin_base += level_bins(a.shapes, l);
   }
   wave_lds_sync();
   // softmax backward over the unit's L*K attention weights
@@ -218,26 +230,108 @@ __global__ __launch_bounds__(kBlock) void fda_backward_kernel(const Args a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Launch one (T, CPL) family, LPU chosen at run time.
+// Backward phase 3, voxel-major: each unit owns one row grad_value[b, v, g, :] of level l and
+// sums, in registers, attn * w_corner * grad_out over every sample whose corner is v.  Those
+// samples are the ones whose base corner is v - (dz,dy,dx) for the 8 offsets, i.e. the
+// contents of 8 bins of the sorted sample list.  Every output row is written exactly once, in
+// T, in a deterministic order (stable sort of fixed-position keys): no zero-fill, no atomics.
+// Blocks are (b, g, level-voxel-block); heads are mapped to XCDs as in the query kernels.
 template <typename T, int CPL, int LPU>
-hipError_t launch_one(bool backward, const Args &a, unsigned grid, size_t lds, hipStream_t st) {
-  if (backward)
-    hipLaunchKernelGGL((fda_backward_kernel<T, CPL, LPU>), dim3(grid), dim3(kBlock), lds, st, a);
-  else
+__global__ __launch_bounds__(kBlock) void fda_bwd_value_kernel(const Args a) {
+  constexpr int UPW = kWave / LPU, UPB = kWavesPerBlock * UPW;
+  int b, g, vb;
+  if (!map_tile(a, blockIdx.x, b, g, vb)) return;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int j = lane & (LPU - 1);
+  const int ub = wave * UPW + lane / LPU;
+  // locate the level of voxel block vb
+  int l = 0, Dl = 0, Hl = 0, Wl = 0;
+  uint32_t bin_lvl = 0, bins_bg = 0;
+  int64_t vstart = 0;
+  bool found = false;
+  int rem = vb;
+  for (int t = 0; t < a.L; ++t) {
+    const int d = (int)a.shapes[3 * t], h = (int)a.shapes[3 * t + 1], w = (int)a.shapes[3 * t + 2];
+    const int64_t n = (int64_t)d * h * w;
+    const int nvb = (int)((n + UPB - 1) / UPB);
+    if (!found) {
+      if (rem < nvb) {
+        found = true; l = t; Dl = d; Hl = h; Wl = w; bin_lvl = bins_bg; vstart = a.lsi[t];
+      } else {
+        rem -= nvb;
+      }
+    }
+    bins_bg += level_bins(a.shapes, t);
+  }
+  if (!found) return;
+  (void)l;
+  const int64_t nvox = (int64_t)Dl * Hl * Wl;
+  const int64_t v = (int64_t)rem * UPB + ub;
+  if (v >= nvox) return;
+  const int x = (int)(v % Wl), y = (int)((v / Wl) % Hl), z = (int)(v / ((int64_t)Wl * Hl));
+  const uint32_t bin_lb = (uint32_t)(b * a.G + g) * bins_bg + bin_lvl;
+  const T *go = static_cast<const T *>(a.grad_out);
+  const int D = a.D, GD = a.G * a.D;
+
+  float acc[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) acc[c] = 0.f;
+#pragma unroll 1
+  for (int d = 0; d < 8; ++d) {
+    const int dz = d >> 2, dy = (d >> 1) & 1, dx = d & 1;
+    const uint32_t bin = bin_lb + (uint32_t)(((z - dz + 1) * (Hl + 1) + (y - dy + 1)) * (Wl + 1) + (x - dx + 1));
+    const uint32_t i0 = a.bin_start[bin], i1 = a.bin_start[bin + 1];
+#pragma unroll 2
+    for (uint32_t i = i0; i < i1; ++i) {
+      const uint32_t gsi = a.sorted_vals[i];
+      const float4 st = a.stash[gsi];
+      const uint32_t u = (uint32_t)(((double)gsi + 0.5) * a.inv_lk);   // gsi / (L*K), exact
+      float tg[CPL];
+      load_global_elems<T, CPL>(go + (int64_t)u * D + j * CPL, tg);
+      const float wx = dx ? st.x : 1.f - st.x;
+      const float wy = dy ? st.y : 1.f - st.y;
+      const float wz = dz ? st.z : 1.f - st.z;
+      const float aw = st.w * ((wx * wy) * wz);
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) acc[c] = fmaf(aw, tg[c], acc[c]);
+    }
+  }
+  const int64_t o = ((int64_t)b * a.S + vstart + v) * GD + g * D + j * CPL;
+  if (a.accumulate) {   // caller-owned fp32 buffer: add to what it holds (sole owner, no atomics)
+    float *dst = static_cast<float *>(a.out) + o;
+    float old[CPL];
+    load_global_elems<float, CPL>(dst, old);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) acc[c] += old[c];
+    store_elems<float, CPL>(dst, acc);
+  } else {
+    store_elems<T, CPL>(static_cast<T *>(a.out) + o, acc);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Launch one (T, CPL) family, LPU chosen at run time.
+// which: 0 forward, 1 backward phase 1 (query-major), 2 backward phase 3 (voxel-major)
+template <typename T, int CPL, int LPU>
+hipError_t launch_one(int which, const Args &a, unsigned grid, size_t lds, hipStream_t st) {
+  if (which == 0)
     hipLaunchKernelGGL((fda_forward_kernel<T, CPL, LPU>), dim3(grid), dim3(kBlock), lds, st, a);
+  else if (which == 1)
+    hipLaunchKernelGGL((fda_bwd_query_kernel<T, CPL, LPU>), dim3(grid), dim3(kBlock), lds, st, a);
+  else
+    hipLaunchKernelGGL((fda_bwd_value_kernel<T, CPL, LPU>), dim3(grid), dim3(kBlock), 0, st, a);
   return hipGetLastError();
 }
 
 template <typename T, int CPL>
-hipError_t launch_cpl(bool backward, int lpu, const Args &a, unsigned grid, size_t lds,
-                      hipStream_t st) {
+hipError_t launch_cpl(int which, int lpu, const Args &a, unsigned grid, size_t lds, hipStream_t st) {
   switch (lpu) {
-    case 1: return launch_one<T, CPL, 1>(backward, a, grid, lds, st);
-    case 2: return launch_one<T, CPL, 2>(backward, a, grid, lds, st);
-    case 4: return launch_one<T, CPL, 4>(backward, a, grid, lds, st);
-    case 8: return launch_one<T, CPL, 8>(backward, a, grid, lds, st);
-    case 16: return launch_one<T, CPL, 16>(backward, a, grid, lds, st);
-    case 32: return launch_one<T, CPL, 32>(backward, a, grid, lds, st);
+    case 1: return launch_one<T, CPL, 1>(which, a, grid, lds, st);
+    case 2: return launch_one<T, CPL, 2>(which, a, grid, lds, st);
+    case 4: return launch_one<T, CPL, 4>(which, a, grid, lds, st);
+    case 8: return launch_one<T, CPL, 8>(which, a, grid, lds, st);
+    case 16: return launch_one<T, CPL, 16>(which, a, grid, lds, st);
+    case 32: return launch_one<T, CPL, 32>(which, a, grid, lds, st);
     default: return hipErrorInvalidValue;
   }
 }

@@ -80,8 +80,8 @@ def level_meta(shapes, device):
 
 
 def pack(locs: torch.Tensor, logits: torch.Tensor) -> torch.Tensor:
-    B, Q, G = locs.shape[:3]
-    return torch.cat([locs.reshape(B, Q, G, -1), logits.reshape(B, Q, G, -1)], dim=-1).contiguous()
+    B, Q, G, L, K = locs.shape[:5]
+    return torch.cat([locs.reshape(B, Q, G, 3 * L * K), logits.reshape(B, Q, G, L * K)], dim=-1).contiguous()
 
 
 def make_inputs(w: Workload, seed: int = 0, dtype=None, device="cpu", q_limit: int | None = None):

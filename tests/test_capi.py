@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_support_table(lib):
-    assert lib.ops3d_fda_abi_version() == 1
+    assert lib.ops3d_fda_abi_version() == 2
     F32, F16, BF16 = 0, 1, 2
     for d in (8, 16, 24, 32, 48, 64, 96, 128, 192, 256):
         assert lib.ops3d_fda_supported(BF16, d) == 1, d
@@ -50,9 +50,23 @@ def test_abi_version_and_support_table(lib):
     assert lib.ops3d_fda_supported(9, 32) == 0
 
 
+def _has_device():
+    import torch
+
+    return torch.cuda.is_available()
+
+
 def test_workspace_bytes(lib):
-    assert lib.ops3d_fda_backward_workspace_bytes(2, 1, 73728, 8, 32) == 73728 * 256 * 4
-    assert lib.ops3d_fda_backward_workspace_bytes(0, 1, 73728, 8, 32) == 0
+    n = 73728 * 8 * 8  # c4 samples
+    ws = lib.ops3d_fda_backward_workspace_bytes(2, 1, 73728, 8, 32, 2, 73728, 4)
+    if not _has_device():
+        # the radix sort sizes its temporary storage for the device it will run on
+        assert ws == 0
+        return
+    # 4 index arrays + stash + bin starts (<= 8*B*G*S + 1) + sort temporary storage
+    assert ws >= n * (4 * 4 + 16) + (8 * 8 * 73728 + 1) * 4
+    assert ws < n * (4 * 4 + 16) * 3
+    assert lib.ops3d_fda_backward_workspace_bytes(9, 1, 73728, 8, 32, 2, 73728, 4) == 0
 
 
 def _fwd(lib, **kw):
@@ -78,6 +92,12 @@ def test_argument_errors_before_device_work(lib):
 
 
 def test_backward_workspace_check(lib):
-    rc = lib.ops3d_fda_backward(None, None, None, None, None, ctypes.c_void_p(256), None, None, 0,
-                                2, 1, 576, 8, 32, 2, 576, 4, 64, None)
-    assert rc == 1 and b"workspace too small" in lib.ops3d_fda_last_error()
+    p = ctypes.c_void_p(256)
+    rc = lib.ops3d_fda_backward(p, p, p, p, p, p, p, None, 0, 2, 1, 576, 8, 32, 2, 576, 4, 64, None)
+    if _has_device():
+        assert rc == 1 and b"workspace too small" in lib.ops3d_fda_last_error()
+    else:
+        assert rc == 2 and b"radix sort" in lib.ops3d_fda_last_error()
+    # argument errors are still reported before anything else
+    rc = lib.ops3d_fda_backward(p, p, p, p, p, p, p, None, 0, 2, 1, 576, 8, 32, 6, 576, 4, 64, None)
+    assert rc == 1 and b"invalid number of scales" in lib.ops3d_fda_last_error()

@@ -187,6 +187,37 @@ def test_im2col_step_invariance_and_determinism(gpu_device):
         assert torch.equal(o, outs[0])
 
 
+def test_backward_deterministic(gpu_device):
+    """grad_value is a sorted gather: bitwise identical across runs (the reference's atomic
+    scatter is not)."""
+    inp = random_inputs([(8, 8, 8), (4, 4, 4)], 2, 500, 8, 32, 4, torch.bfloat16, seed=11)
+    a = run_gpu(inp, gpu_device)
+    b = run_gpu(inp, gpu_device)
+    assert torch.equal(a[1], b[1]) and torch.equal(a[2], b[2])
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_backward_accumulate_f32(gpu_device, dt):
+    """_C.flash_deform_attn_backward_accumulate adds the value gradient into an fp32 buffer."""
+    from ops3d_amd import _C
+
+    inp = random_inputs([(6, 5, 4), (3, 3, 2)], 1, 200, 8, 32, 4, dt, seed=3)
+    st, lsi = level_meta(inp["shapes"], gpu_device)
+    v = inp["value"].to(gpu_device)
+    s = inp["sampling_loc_attn"].to(gpu_device)
+    go = inp["grad_output"].to(gpu_device)
+    acc = torch.full(v.shape, 0.25, dtype=torch.float32, device=gpu_device)
+    g1 = _C.flash_deform_attn_backward_accumulate(v, st, lsi, s, go, acc, 64, 4)
+    g2 = _C.flash_deform_attn_backward_accumulate(v, st, lsi, s, go, acc, 64, 4)
+    torch.cuda.synchronize()
+    _, rgv, rgs = run_oracle(inp)
+    rtol, atol = TOL[torch.float32] if dt == torch.float32 else (1e-5, 1e-5)
+    assert_close("accumulated grad_value", acc, 0.25 + 2 * rgv, rtol, 2 * atol)
+    assert torch.equal(g1, g2)
+    assert_close("grad_sla", g1, rgs, *TOL[dt], extra=None if dt != torch.float32 else
+                 __import__("fda_helpers").fp32_allowance(inp))
+
+
 def test_empty_queries(gpu_device):
     inp = random_inputs([(4, 4, 4)], 1, 0, 4, 32, 4, torch.float32)
     out, gv, gs = run_gpu(inp, gpu_device)
