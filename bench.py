@@ -119,23 +119,25 @@ class Bench:
         torch = self.torch
         v, s = self.value.detach(), self.sla.detach()
 
-        def fk():
-            _C.flash_deform_attn_forward(v, self.st, self.lsi, s, 64, self.w.K)
-
-        fwd = self.time_loop(fk, steps, warmup)
-        _C.profile_enable(True)
-        try:
+        def run(fn, which):
             phases = {}
             for i in range(warmup + steps):
-                _C.flash_deform_attn_backward(v, self.st, self.lsi, s, self.go, 64, self.w.K)
-                r = _C.profile_read()
+                fn()
+                r = _C.profile_read(which)
                 if i >= warmup:
                     for k, t in r.items():
                         phases.setdefault(k, []).append(t)
+            out = {k: {"mean": sum(t) / len(t), "median": statistics.median(t)} for k, t in phases.items()}
+            out["total"] = {"mean": sum(x["mean"] for x in out.values())}
+            return out
+
+        _C.profile_enable(True)
+        try:
+            fwd = run(lambda: _C.flash_deform_attn_forward(v, self.st, self.lsi, s, 64, self.w.K), "forward")
+            bwd = run(lambda: _C.flash_deform_attn_backward(v, self.st, self.lsi, s, self.go, 64, self.w.K),
+                      "backward")
         finally:
             _C.profile_enable(False)
-        bwd = {k: {"mean": sum(t) / len(t), "median": statistics.median(t)} for k, t in phases.items()}
-        bwd["total"] = {"mean": sum(x["mean"] for x in bwd.values())}
         return fwd, bwd
 
 
@@ -212,7 +214,7 @@ def summary_line(r):
     by = r["bytes"]
     f = r["fwd"]["median"]
     s = r.get("step", {}).get("median")
-    fk = r.get("fwd_kernel", {}).get("mean")
+    fk = r.get("fwd_kernel", {}).get("total", {}).get("mean")
     bk = r.get("bwd_kernel", {}).get("total", {}).get("mean")
     samples = r["samples"]
     parts = [f"{r['workload']:>3} {r['dtype']:>4}", f"fwd {f * 1e3:8.1f} us ({by['fwd'] / f / 1e6:7.0f} GB/s, "
@@ -221,10 +223,13 @@ def summary_line(r):
         parts.append(f"fwd+bwd {s * 1e3:8.1f} us ({by['total'] / s / 1e6:7.0f} GB/s, "
                      f"{100 * by['total'] / s / 1e6 / HBM_PEAK_GBS:5.1f}%)")
     if fk:
-        parts.append(f"k_fwd {fk * 1e3:7.1f} us")
+        fp = r["fwd_kernel"]
+        parts.append(f"fwd call {fk * 1e3:7.1f} us [copy {fp['head_major_copy']['mean'] * 1e3:.1f} "
+                     f"k {fp['forward_kernel']['mean'] * 1e3:.1f}]")
     if bk:
         ph = r["bwd_kernel"]
-        parts.append(f"bwd {bk * 1e3:7.1f} us [q {ph['query_kernel']['mean'] * 1e3:.1f} sort {ph['sort']['mean'] * 1e3:.1f} "
+        parts.append(f"bwd {bk * 1e3:7.1f} us [copy {ph['head_major_copies']['mean'] * 1e3:.1f} "
+                     f"q {ph['query_kernel']['mean'] * 1e3:.1f} sort {ph['sort']['mean'] * 1e3:.1f} "
                      f"bins {ph['bin_offsets']['mean'] * 1e3:.1f} v {ph['value_kernel']['mean'] * 1e3:.1f}]")
     parts.append(f"{samples / (s or f) / 1e6:.3g} Gsamples/s" if (s or f) else "")
     return " | ".join(parts)
@@ -239,6 +244,10 @@ def main():
     ap.add_argument("--all", action="store_true", help="also report every configuration (stderr)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--json-out", default=None, help="write all results as JSON to this path")
+    ap.add_argument("--kernels-only", action="store_true",
+                    help="only the per-kernel loops of --config (for profilers); prints no JSON line")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a device-to-device copy of MIB MiB, 5 times (HBM counter calibration)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -259,6 +268,21 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     log(f"device: {torch.cuda.get_device_name(0)}; torch {torch.__version__}")
+    if args.copy_calibration:
+        src = torch.empty(args.copy_calibration << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copied {args.copy_calibration} MiB 5 times")
+        return
+    if args.kernels_only:
+        w = WORKLOADS[args.config]
+        b = Bench(w, w.dtype, dev)
+        fk, bk = b.kernel_times(args.steps, args.warmup)
+        log(f"{w.name}: forward " + ", ".join(f"{k} {v['mean'] * 1e3:.1f} us" for k, v in fk.items())
+            + "; backward " + ", ".join(f"{k} {v['mean'] * 1e3:.1f} us" for k, v in bk.items()))
+        return
 
     results = []
     if args.all:
@@ -287,7 +311,7 @@ def main():
     #   backward query kernel: read value + sampling_loc_attn + grad_output, write grad_sampling_loc_attn
     #   backward value kernel: read grad_output, write grad_value
     kern = {
-        "fda_forward_kernel": (r["fwd_kernel"]["mean"], V + R + O),
+        "fda_forward_kernel": (r["fwd_kernel"]["forward_kernel"]["mean"], V + R + O),
         "fda_bwd_query_kernel": (ph["query_kernel"]["mean"], V + 2 * R + O),
         "fda_bwd_value_kernel": (ph["value_kernel"]["mean"], O + V),
         "radix_sort": (ph["sort"]["mean"], None),
@@ -297,7 +321,7 @@ def main():
     if kbytes is None:  # the sort moves only internal keys; report the backward as a whole
         dominant, kms, kbytes = "backward (all phases)", ph["total"]["mean"], by["bwd"]
     achieved = kbytes / (kms * 1e-3) / 1e9
-    kf, kb = r["fwd_kernel"]["mean"], ph["total"]["mean"]
+    kf, kb = r["fwd_kernel"]["total"]["mean"], ph["total"]["mean"]
     traffic = _traffic_from_profiles(dominant, w.name)
     line = {
         "metric": METRIC,
@@ -324,7 +348,10 @@ def main():
         "frac_of_hbm_peak": round(by["total"] / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "qhs_per_s": round(w.samples() / (ms_step * 1e-3), 1),
         "kernels_us": {**{k: round(v[0] * 1e3, 2) for k, v in kern.items()},
-                       "bin_offsets": round(ph["bin_offsets"]["mean"] * 1e3, 2), "backward_total": round(kb * 1e3, 2)},
+                       "head_major_copy_fwd": round(r["fwd_kernel"]["head_major_copy"]["mean"] * 1e3, 2),
+                       "head_major_copies_bwd": round(ph["head_major_copies"]["mean"] * 1e3, 2),
+                       "bin_offsets": round(ph["bin_offsets"]["mean"] * 1e3, 2),
+                       "forward_total": round(kf * 1e3, 2), "backward_total": round(kb * 1e3, 2)},
         "roofline": {
             "kernel": dominant,
             "bound": "hbm",

@@ -50,27 +50,40 @@ OPS3D_FDA_API const char *ops3d_fda_last_error(void);
 OPS3D_FDA_API int ops3d_fda_supported(int dtype, int channels);
 
 /*
+ * Bytes of optional device workspace for ops3d_fda_forward: room for a head-major copy
+ * [B,G,S,D] of value (0 when G == 1 or on invalid sizes).
+ */
+OPS3D_FDA_API size_t ops3d_fda_forward_workspace_bytes(int dtype, int batch, int spatial_size,
+                                                       int num_heads, int channels);
+
+/*
  * Forward.  Replaces flash_deform_attn_forward (reference csrc/flash_deform_attn.h:7-25 ->
  * csrc/cuda/flash_deform_attn_cuda.cu:20-91).  Writes every element of `output`
  * ([B,Q,G*D], dtype), so the caller need not zero it.  The softmax over the L*K logits of each
  * (b,q,g) is computed in fp32 inside the kernel; trilinear sampling uses zero padding and
  * align_corners=False pixel coordinates (loc*size - 0.5).
+ *   workspace:   optional (NULL/0 allowed).  With ops3d_fda_forward_workspace_bytes() bytes the
+ *                library first copies value head-major, so that each head's rows are contiguous
+ *                and, with heads mapped to XCDs, stay in one XCD's L2 (faster; same results).
  *   im2col_step: batch chunk size of the reference; min(batch, im2col_step) must divide batch
  *                (else OPS3D_FDA_ERUNTIME, as reference flash_deform_attn_cuda.cu:56-58).  Results
  *                do not depend on it.
  *   num_levels must be 1..5 and num_point 1..16 (else OPS3D_FDA_EINVAL).
  */
 OPS3D_FDA_API int ops3d_fda_forward(const void *value, const int64_t *spatial_shapes,
-                      const int64_t *level_start_index, const void *sampling_loc_attn,
-                      void *output, int dtype, int batch, int spatial_size, int num_heads,
-                      int channels, int num_levels, int num_query, int num_point,
-                      int im2col_step, void *stream);
+                                    const int64_t *level_start_index,
+                                    const void *sampling_loc_attn, void *output, void *workspace,
+                                    size_t workspace_bytes, int dtype, int batch,
+                                    int spatial_size, int num_heads, int channels,
+                                    int num_levels, int num_query, int num_point,
+                                    int im2col_step, void *stream);
 
 /*
  * Bytes of device workspace ops3d_fda_backward / ops3d_fda_backward_accumulate_f32 need (0 on
- * invalid sizes, or when no HIP device is present to size the sort for): per sample (N = B*Q*G*L*K) a sort key, an index and a 16-byte stash, their
- * sorted copies, per spatial bin (<= 8*B*G*S) a start offset, and the radix sort's temporary
- * storage.  The pointer passed must be 256-byte aligned.
+ * invalid sizes, or when no HIP device is present to size the sort for): per sample
+ * (N = B*Q*G*L*K) a sort key, an index and a 16-byte stash and their sorted copies, per
+ * spatial bin (<= 8*B*G*S) a start offset, the radix sort's temporary storage, and head-major
+ * copies of value and grad_output (G > 1).  The pointer passed must be 256-byte aligned.
  */
 OPS3D_FDA_API size_t ops3d_fda_backward_workspace_bytes(int dtype, int batch, int spatial_size,
                                                         int num_heads, int channels,
@@ -110,15 +123,16 @@ OPS3D_FDA_API int ops3d_fda_backward_accumulate_f32(
     int im2col_step, void *stream);
 
 /*
- * Phase timing of the backward (no counterpart in the reference; for benchmarks and
- * profilers).  After ops3d_fda_profile_enable(1), every backward call records HIP events on
- * its stream around its phases; ops3d_fda_profile_read() waits for the last call to finish and
- * writes up to n durations in ms: [0] query-major kernel, [1] sort, [2] bin offsets,
- * [3] value-gradient kernel.  Returns the number written (0 if nothing was recorded).
+ * Phase timing (no counterpart in the reference; for benchmarks and profilers).  After
+ * ops3d_fda_profile_enable(1), every call records HIP events on its stream around its phases.
+ * ops3d_fda_profile_read(which, ms, n) waits for the last call of that kind to finish and writes
+ * up to n durations in ms; which = 0 (backward): [0] head-major copies, [1] query-major kernel,
+ * [2] sort + permute, [3] bin offsets, [4] value-gradient kernel; which = 1 (forward):
+ * [0] head-major copy, [1] forward kernel.  Returns the number written (0 if nothing recorded).
  * Process-wide state, not thread-safe; enable on the device the calls run on.
  */
 OPS3D_FDA_API int ops3d_fda_profile_enable(int on);
-OPS3D_FDA_API int ops3d_fda_profile_read(float *ms, int n);
+OPS3D_FDA_API int ops3d_fda_profile_read(int which, float *ms, int n);
 
 #ifdef __cplusplus
 }

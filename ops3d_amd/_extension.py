@@ -31,6 +31,7 @@ EXPORTED_SYMBOLS = (
     "ops3d_fda_abi_version",
     "ops3d_fda_last_error",
     "ops3d_fda_supported",
+    "ops3d_fda_forward_workspace_bytes",
     "ops3d_fda_forward",
     "ops3d_fda_backward_workspace_bytes",
     "ops3d_fda_backward",
@@ -47,8 +48,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ops3d_fda_last_error.argtypes = []
     lib.ops3d_fda_supported.restype = _i
     lib.ops3d_fda_supported.argtypes = [_i, _i]
+    lib.ops3d_fda_forward_workspace_bytes.restype = _sz
+    lib.ops3d_fda_forward_workspace_bytes.argtypes = [_i] * 5
     lib.ops3d_fda_forward.restype = _i
-    lib.ops3d_fda_forward.argtypes = [_vp, _vp, _vp, _vp, _vp] + [_i] * 9 + [_vp]
+    lib.ops3d_fda_forward.argtypes = [_vp] * 6 + [_sz] + [_i] * 9 + [_vp]
     lib.ops3d_fda_backward_workspace_bytes.restype = _sz
     lib.ops3d_fda_backward_workspace_bytes.argtypes = [_i] * 8
     lib.ops3d_fda_backward.restype = _i
@@ -56,7 +59,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ops3d_fda_profile_enable.restype = _i
     lib.ops3d_fda_profile_enable.argtypes = [_i]
     lib.ops3d_fda_profile_read.restype = _i
-    lib.ops3d_fda_profile_read.argtypes = [ctypes.POINTER(ctypes.c_float), _i]
+    lib.ops3d_fda_profile_read.argtypes = [_i, ctypes.POINTER(ctypes.c_float), _i]
     lib.ops3d_fda_backward_accumulate_f32.restype = _i
     lib.ops3d_fda_backward_accumulate_f32.argtypes = [_vp] * 8 + [_sz] + [_i] * 9 + [_vp]
 
@@ -68,7 +71,7 @@ def _ptr(t: torch.Tensor | None) -> int | None:
 class _NativeFDA:
     """Host side of the flash-deform-attn extension, bound to libops3d_fda.so."""
 
-    ABI_VERSION = 2
+    ABI_VERSION = 3
 
     def __init__(self, lib: ctypes.CDLL, path: str):
         self._lib = lib
@@ -143,11 +146,14 @@ class _NativeFDA:
         (the gfx950 launch geometry is chosen by the library).  Returns [B, Q, G*D]."""
         B, S, G, D, L, Q = self._common(value, spatial_shapes, level_start_index, sampling_loc_attn, K, {})
         out = torch.empty((B, Q, G * D), dtype=value.dtype, device=value.device)
+        code = _DTYPE_CODE[value.dtype]
+        n = self._lib.ops3d_fda_forward_workspace_bytes(code, B, S, G, D) if B * Q > 0 else 0
+        ws = torch.empty(n, dtype=torch.uint8, device=value.device) if n else None
         stream = torch.cuda.current_stream(value.device).cuda_stream
         with torch.cuda.device(value.device):
             rc = self._lib.ops3d_fda_forward(
                 _ptr(value), _ptr(spatial_shapes), _ptr(level_start_index), _ptr(sampling_loc_attn),
-                _ptr(out), _DTYPE_CODE[value.dtype], B, S, G, D, L, Q, int(K), int(im2col_step), stream,
+                _ptr(out), _ptr(ws), n, code, B, S, G, D, L, Q, int(K), int(im2col_step), stream,
             )
         if rc != OPS3D_FDA_OK:
             self._raise(rc, "flash_deform_attn_forward failed")
@@ -215,11 +221,15 @@ class _NativeFDA:
         if self._lib.ops3d_fda_profile_enable(1 if on else 0) != OPS3D_FDA_OK:
             self._raise(OPS3D_FDA_ERUNTIME, "profile_enable failed")
 
-    def profile_read(self) -> dict:
-        """Phase durations (ms) of the last backward call (waits for it to finish)."""
-        buf = (ctypes.c_float * 4)()
-        n = self._lib.ops3d_fda_profile_read(buf, 4)
-        names = ("query_kernel", "sort", "bin_offsets", "value_kernel")
+    def profile_read(self, which: str = "backward") -> dict:
+        """Phase durations (ms) of the last backward / forward call (waits for it to finish)."""
+        buf = (ctypes.c_float * 8)()
+        if which == "backward":
+            n = self._lib.ops3d_fda_profile_read(0, buf, 8)
+            names = ("head_major_copies", "query_kernel", "sort", "bin_offsets", "value_kernel")
+        else:
+            n = self._lib.ops3d_fda_profile_read(1, buf, 8)
+            names = ("head_major_copy", "forward_kernel")
         return {names[i]: buf[i] for i in range(n)}
 
     def supported(self, dtype: torch.dtype, channels: int) -> bool:

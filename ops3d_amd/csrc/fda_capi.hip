@@ -36,9 +36,12 @@ namespace {
 thread_local std::string g_last_error;
 
 // backward phase timing (ops3d_fda_profile_*)
+// events 0..5: backward (copies | query kernel | sort+permute | bin offsets | value kernel)
+// events 6..8: forward (head-major copy | forward kernel)
+constexpr int kProfEvents = 9;
 bool g_prof_on = false;
-bool g_prof_recorded = false;
-hipEvent_t g_prof_ev[5];
+bool g_prof_recorded[2] = {false, false};
+hipEvent_t g_prof_ev[kProfEvents];
 bool g_prof_created = false;
 
 void prof_mark(int i, hipStream_t st) {
@@ -115,8 +118,8 @@ int common_checks(int dtype, int B, int S, int G, int D, int L, int Q, int K, in
                 (long long)S * G * D, (long long)kMaxLevelElems);
   const int LK = L * K, P = 4 * LK;
   const int UPB = kWavesPerBlock * (kWave / geo.lpu);
-  const size_t lds = (size_t)UPB * (size_t)(P + (backward ? LK : 0) + 1) * sizeof(float);
-  if (lds > 64 * 1024)
+  const size_t lds = (size_t)UPB * (size_t)(backward ? bwd_query_lds_floats(P, LK) : P + 1) * sizeof(float);
+  if (lds > 160 * 1024)   // gfx950: 160 KB of LDS per workgroup
     return fail(OPS3D_FDA_EINVAL, "L*K=%d too large for D=%d (needs %zu bytes of LDS per block)", LK, D, lds);
 
   Args &a = geo.a;
@@ -164,7 +167,8 @@ void set_grid(Args &a, int ncol_per_b, unsigned &grid_out) {
 
 // Workspace of the backward gather (all offsets 256-byte aligned):
 //   keys_in, keys_out, vals_in, vals_out : N uint32 each, N = B*Q*G*L*K samples
-//   stash                               : N float4
+//   stash, sorted stash                 : N float4 each
+//   sorted grad_output rows             : N uint32
 //   bin_start                           : nbins_bound + 1 uint32
 //   sort temporary storage              : as hipcub reports
 // nbins_bound = B*G*8*S bounds the real bin count sum_l (D+1)(H+1)(W+1) without reading the
@@ -172,13 +176,14 @@ void set_grid(Args &a, int ncol_per_b, unsigned &grid_out) {
 struct BwdLayout {
   uint64_t n, nbins_bound;
   int key_bits;
-  size_t off_keys_in, off_keys_out, off_vals_in, off_vals_out, off_stash, off_bins, off_temp;
+  size_t off_keys_in, off_keys_out, off_vals_in, off_vals_out, off_stash, off_sstash, off_srow, off_bins,
+      off_temp, off_vhm, off_ghm;
   size_t temp_bytes, total;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-int bwd_layout(int B, int S, int G, int L, int Q, int K, BwdLayout &ly) {
+int bwd_layout(int B, int S, int G, int D, int e, int L, int Q, int K, BwdLayout &ly) {
   ly = BwdLayout{};
   ly.n = (uint64_t)B * Q * G * L * K;
   ly.nbins_bound = (uint64_t)B * G * 8 * (uint64_t)S;
@@ -203,10 +208,64 @@ int bwd_layout(int B, int S, int G, int L, int Q, int K, BwdLayout &ly) {
   ly.off_vals_in = o; o += n4;
   ly.off_vals_out = o; o += n4;
   ly.off_stash = o; o += align256(ly.n * 16);
+  ly.off_sstash = o; o += align256(ly.n * 16);
+  ly.off_srow = o; o += n4;
   ly.off_bins = o; o += align256((ly.nbins_bound + 1) * 4);
   ly.off_temp = o; o += align256(temp);
+  // head-major copies of value and grad_output (G > 1)
+  ly.off_vhm = o; o += G > 1 ? align256((size_t)B * S * G * D * e) : 0;
+  ly.off_ghm = o; o += G > 1 ? align256((size_t)B * Q * G * D * e) : 0;
   ly.total = o;
   return OPS3D_FDA_OK;
+}
+
+// After the sort: the stash and the grad_output row of every sorted sample, in sorted order,
+// so that the value kernel streams them instead of chasing sample -> stash -> row.
+__global__ __launch_bounds__(256) void fda_bwd_permute_kernel(const Args a, uint32_t n) {
+  const uint32_t stride = gridDim.x * blockDim.x;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const uint32_t gsi = a.sorted_vals[i];
+    const uint32_t t = (uint32_t)(((double)gsi + 0.5) * a.inv_lk);   // gsi / (L*K), exact
+    const uint32_t bg = t / (uint32_t)a.Q, q = t - bg * (uint32_t)a.Q;
+    const uint32_t b = bg / (uint32_t)a.G, g = bg - b * (uint32_t)a.G;
+    const_cast<float4 *>(a.sorted_stash)[i] = a.stash[gsi];
+    const_cast<uint32_t *>(a.sorted_row)[i] = a.ghm ? t : (b * (uint32_t)a.Q + q) * (uint32_t)a.G + g;
+  }
+}
+
+// [B, N, G, R words] -> [B, G, N, R words]: the head-major copy of value / grad_output, so that
+// one head's rows are contiguous (one head per XCD then keeps its slice in that XCD's L2).
+// One 16-byte chunk per thread and step when R is a multiple of 4 words, else one word.
+__global__ __launch_bounds__(256) void head_major_kernel(const uint32_t *src, uint32_t *dst, int64_t B,
+                                                         int64_t N, int G, int R) {
+  const bool vec = (R & 3) == 0;
+  const int Rc = vec ? R / 4 : R;                  // chunks per row
+  const int64_t total = B * N * G * Rc;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t c = i % Rc;
+    const int64_t row = i / Rc;                      // (b, n, g)
+    const int64_t g = row % G;
+    const int64_t bn = row / G;
+    const int64_t n = bn % N, b = bn / N;
+    const int64_t o = ((b * G + g) * N + n) * Rc + c;
+    if (vec)
+      reinterpret_cast<u32x4 *>(dst)[o] = reinterpret_cast<const u32x4 *>(src)[i];
+    else
+      dst[o] = src[i];
+  }
+}
+
+hipError_t launch_head_major(const void *src, void *dst, int64_t B, int64_t N, int G, int D, int esize,
+                             hipStream_t st) {
+  const int R = D * esize / 4;
+  const int64_t chunks = B * N * G * ((R & 3) == 0 ? R / 4 : R);
+  int64_t blocks = (chunks + 255) / 256;
+  if (blocks > 16384) blocks = 16384;
+  if (blocks < 1) return hipSuccess;
+  hipLaunchKernelGGL(head_major_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
+                     static_cast<const uint32_t *>(src), static_cast<uint32_t *>(dst), B, N, G, R);
+  return hipGetLastError();
 }
 
 // bin_start[b] = first position of key >= b in the sorted keys, for b in [0, nbins_real],
@@ -234,7 +293,7 @@ __global__ __launch_bounds__(256) void bin_start_kernel(const uint32_t *keys, ui
 
 extern "C" {
 
-int ops3d_fda_abi_version(void) { return 2; }
+int ops3d_fda_abi_version(void) { return 3; }
 
 const char *ops3d_fda_last_error(void) { return g_last_error.c_str(); }
 
@@ -243,11 +302,18 @@ int ops3d_fda_supported(int dtype, int channels) {
   return pick_config(dtype, channels, cpl, lpu) ? 1 : 0;
 }
 
+size_t ops3d_fda_forward_workspace_bytes(int dtype, int batch, int spatial_size, int num_heads,
+                                         int channels) {
+  const int e = elem_size(dtype);
+  if (e == 0 || batch <= 0 || spatial_size <= 0 || num_heads <= 1 || channels <= 0) return 0;
+  return align256((size_t)batch * spatial_size * num_heads * channels * e);
+}
+
 int ops3d_fda_forward(const void *value, const int64_t *spatial_shapes,
                       const int64_t *level_start_index, const void *sampling_loc_attn,
-                      void *output, int dtype, int batch, int spatial_size, int num_heads,
-                      int channels, int num_levels, int num_query, int num_point,
-                      int im2col_step, void *stream) {
+                      void *output, void *workspace, size_t workspace_bytes, int dtype, int batch,
+                      int spatial_size, int num_heads, int channels, int num_levels,
+                      int num_query, int num_point, int im2col_step, void *stream) {
   g_last_error.clear();
   Geometry geo;
   int rc = common_checks(dtype, batch, spatial_size, num_heads, channels, num_levels, num_query,
@@ -257,17 +323,30 @@ int ops3d_fda_forward(const void *value, const int64_t *spatial_shapes,
   if (!value && spatial_size > 0) return fail(OPS3D_FDA_EINVAL, "value is NULL");
   if (!spatial_shapes || !level_start_index || !sampling_loc_attn || !output)
     return fail(OPS3D_FDA_EINVAL, "NULL pointer argument");
-  if (misaligned(value) || misaligned(sampling_loc_attn) || misaligned(output))
+  if (misaligned(value) || misaligned(sampling_loc_attn) || misaligned(output) || misaligned(workspace))
     return fail(OPS3D_FDA_EINVAL, "tensor data pointers must be 4-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
   geo.a.value = value;
+  prof_mark(6, st);
+  const size_t need = ops3d_fda_forward_workspace_bytes(dtype, batch, spatial_size, num_heads, channels);
+  if (need > 0 && workspace && workspace_bytes >= need) {
+    hipError_t e = launch_head_major(value, workspace, batch, spatial_size, num_heads, channels,
+                                     elem_size(dtype), st);
+    if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "head-major copy failed: %s", hipGetErrorString(e));
+    geo.a.value = workspace;
+    geo.a.vhm = 1;
+  }
   geo.a.shapes = spatial_shapes;
   geo.a.lsi = level_start_index;
   geo.a.loc_attn = sampling_loc_attn;
   geo.a.out = output;
-  hipError_t e = launch(dtype, false, geo, static_cast<hipStream_t>(stream));
+  prof_mark(7, st);
+  hipError_t e = launch(dtype, 0, geo, st);
   if (e != hipSuccess)
     return fail(OPS3D_FDA_ERUNTIME, "forward kernel launch failed: %s (grid=%u, lds=%zu)",
                 hipGetErrorString(e), geo.grid, geo.lds);
+  prof_mark(8, st);
+  if (g_prof_on) g_prof_recorded[1] = true;
   return OPS3D_FDA_OK;
 }
 
@@ -277,7 +356,8 @@ size_t ops3d_fda_backward_workspace_bytes(int dtype, int batch, int spatial_size
       num_levels < 1 || num_query < 0 || num_point < 1)
     return 0;
   BwdLayout ly;
-  if (bwd_layout(batch, spatial_size, num_heads, num_levels, num_query, num_point, ly)) return 0;
+  if (bwd_layout(batch, spatial_size, num_heads, channels, elem_size(dtype), num_levels, num_query, num_point, ly))
+    return 0;
   return ly.total;
 }
 
@@ -293,7 +373,7 @@ static int backward_impl(const void *value, const int64_t *spatial_shapes,
                          num_point, im2col_step, true, geo);
   if (rc) return rc;
   BwdLayout ly;
-  rc = bwd_layout(batch, spatial_size, num_heads, num_levels, num_query, num_point, ly);
+  rc = bwd_layout(batch, spatial_size, num_heads, channels, elem_size(dtype), num_levels, num_query, num_point, ly);
   if (rc) return rc;
   const int64_t nval = (int64_t)batch * spatial_size * num_heads * channels;
   const bool work = (int64_t)batch * num_query > 0;
@@ -316,6 +396,8 @@ static int backward_impl(const void *value, const int64_t *spatial_shapes,
   uint32_t *vals_in = reinterpret_cast<uint32_t *>(ws + ly.off_vals_in);
   uint32_t *vals_out = reinterpret_cast<uint32_t *>(ws + ly.off_vals_out);
   float4 *stash = reinterpret_cast<float4 *>(ws + ly.off_stash);
+  float4 *sstash = reinterpret_cast<float4 *>(ws + ly.off_sstash);
+  uint32_t *srow = reinterpret_cast<uint32_t *>(ws + ly.off_srow);
   uint32_t *bins = reinterpret_cast<uint32_t *>(ws + ly.off_bins);
   void *temp = ws + ly.off_temp;
 
@@ -333,22 +415,43 @@ static int backward_impl(const void *value, const int64_t *spatial_shapes,
   a.inv_lk = 1.0 / (double)(num_levels * num_point);
   hipError_t e;
   prof_mark(0, st);
+  if (work && num_heads > 1) {
+    // head-major copies: one head's value rows / grad_output rows become contiguous
+    e = launch_head_major(value, ws + ly.off_vhm, batch, spatial_size, num_heads, channels, elem_size(dtype), st);
+    if (e == hipSuccess)
+      e = launch_head_major(grad_output, ws + ly.off_ghm, batch, num_query, num_heads, channels, elem_size(dtype), st);
+    if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "head-major copy failed: %s", hipGetErrorString(e));
+    a.value = ws + ly.off_vhm;
+    a.vhm = 1;
+    a.grad_out = ws + ly.off_ghm;
+    a.ghm = 1;
+  }
+  prof_mark(1, st);
   if (work) {
     // phase 1: location / logit gradients, per-sample bin keys and stash
     e = launch(dtype, 1, geo, st);
     if (e != hipSuccess)
       return fail(OPS3D_FDA_ERUNTIME, "backward query kernel launch failed: %s (grid=%u, lds=%zu)",
                   hipGetErrorString(e), geo.grid, geo.lds);
-    prof_mark(1, st);
+    prof_mark(2, st);
     // phase 2: stable radix sort of (bin, sample) pairs
     size_t tb = ly.temp_bytes;
     e = hipcub::DeviceRadixSort::SortPairs(temp, tb, keys_in, keys_out, vals_in, vals_out, (int)ly.n, 0,
                                            ly.key_bits, st);
     if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "radix sort failed: %s", hipGetErrorString(e));
+    // stash and grad_output row of every sample in sorted order
+    a.sorted_vals = vals_out;
+    a.sorted_stash = sstash;
+    a.sorted_row = srow;
+    unsigned pblocks = (unsigned)((ly.n + 255) / 256);
+    if (pblocks > 16384) pblocks = 16384;
+    hipLaunchKernelGGL(fda_bwd_permute_kernel, dim3(pblocks), dim3(256), 0, st, a, (uint32_t)ly.n);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "permute kernel launch failed: %s", hipGetErrorString(e));
   } else {
-    prof_mark(1, st);
+    prof_mark(2, st);
   }
-  prof_mark(2, st);
+  prof_mark(3, st);
   {
     const uint64_t nb = ly.nbins_bound + 1;
     unsigned blocks = (unsigned)((nb + 255) / 256);
@@ -358,14 +461,16 @@ static int backward_impl(const void *value, const int64_t *spatial_shapes,
     e = hipGetLastError();
     if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "bin kernel launch failed: %s", hipGetErrorString(e));
   }
-  prof_mark(3, st);
+  prof_mark(4, st);
   if (nval > 0) {
     // phase 3: one owner per grad_value row, gathered from 8 bins, written once
     Geometry g3 = geo;
-    const int UPB = kWavesPerBlock * (kWave / geo.lpu);
-    const int nvb_bound = (int)(((int64_t)spatial_size + UPB - 1) / UPB) + num_levels;
+    const int VPB = value_voxels_per_block(geo.lpu);
+    const int nvb_bound = (int)(((int64_t)spatial_size + VPB - 1) / VPB) + num_levels;
     set_grid(g3.a, nvb_bound, g3.grid);
     g3.a.sorted_vals = vals_out;
+    g3.a.sorted_stash = sstash;
+    g3.a.sorted_row = srow;
     g3.a.bin_start = bins;
     g3.a.out = grad_value;
     g3.a.accumulate = out_f32_accumulate ? 1 : 0;
@@ -375,27 +480,28 @@ static int backward_impl(const void *value, const int64_t *spatial_shapes,
       return fail(OPS3D_FDA_ERUNTIME, "backward value kernel launch failed: %s (grid=%u)", hipGetErrorString(e),
                   g3.grid);
   }
-  prof_mark(4, st);
-  if (g_prof_on) g_prof_recorded = true;
+  prof_mark(5, st);
+  if (g_prof_on) g_prof_recorded[0] = true;
   return OPS3D_FDA_OK;
 }
 
 int ops3d_fda_profile_enable(int on) {
   if (on && !g_prof_created) {
-    for (int i = 0; i < 5; ++i)
+    for (int i = 0; i < kProfEvents; ++i)
       if (hipEventCreate(&g_prof_ev[i]) != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "hipEventCreate failed");
     g_prof_created = true;
   }
   g_prof_on = on != 0;
-  g_prof_recorded = false;
+  g_prof_recorded[0] = g_prof_recorded[1] = false;
   return OPS3D_FDA_OK;
 }
 
-int ops3d_fda_profile_read(float *ms, int n) {
-  if (!g_prof_recorded || !ms) return 0;
-  if (hipEventSynchronize(g_prof_ev[4]) != hipSuccess) return 0;
+int ops3d_fda_profile_read(int which, float *ms, int n) {
+  if (which < 0 || which > 1 || !g_prof_recorded[which] || !ms) return 0;
+  const int first = which == 0 ? 0 : 6, last = which == 0 ? 5 : 8;
+  if (hipEventSynchronize(g_prof_ev[last]) != hipSuccess) return 0;
   int k = 0;
-  for (int i = 0; i < 4 && k < n; ++i, ++k)
+  for (int i = first; i < last && k < n; ++i, ++k)
     if (hipEventElapsedTime(&ms[k], g_prof_ev[i], g_prof_ev[i + 1]) != hipSuccess) ms[k] = -1.f;
   return k;
 }

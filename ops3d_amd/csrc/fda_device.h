@@ -48,8 +48,12 @@ struct Args {
   float4 *stash;              // [N] (fx, fy, fz, attn) of each sample
   const uint32_t *sorted_vals;  // [N] sample indices sorted by bin
   const uint32_t *bin_start;    // [nbins_bound + 1] first sorted position of each bin
+  const float4 *sorted_stash;   // [N] stash in sorted order
+  const uint32_t *sorted_row;   // [N] grad_output row (b*Q + q)*G + g in sorted order
   uint32_t key_invalid;       // = nbins_bound, sorts after every real bin
   int accumulate;             // phase 3: add into grad_value instead of overwriting
+  int vhm;                    // value is head-major [B,G,S,D] (a transposed copy)
+  int ghm;                    // grad_out is head-major [B,G,Q,D] (a transposed copy)
   double inv_lk;              // 1.0 / (L*K), for sample -> unit
   int B, S, G, D, L, K, Q, P;
   int nqb;                    // query blocks per batch = ceil(Q / UPB)
@@ -337,6 +341,39 @@ __device__ __forceinline__ bool sample_setup(float lx, float ly, float lz, int W
     sm.off[c] = ok ? oz[dz] + oy[dy] + ox[dx] : OOB_ELEM;
   }
   return true;
+}
+
+// LDS floats per unit of the backward query kernel (record, grad_attn, 16-byte-aligned stash
+// and keys); the block uses UPB times this.  Rounded to 4 x an odd number so that the units of
+// a wave start in different LDS banks.
+__host__ __device__ constexpr int bwd_query_lds_floats(int P, int LK) {
+  return (((((P + LK + 3) & ~3) + 5 * LK + ((LK & 3) ? 4 - (LK & 3) : 0)) / 4) | 1) * 4;
+}
+
+// Geometry of the backward value kernel: lane groups of LPU lanes, NBP of them (one per
+// neighbour bin, fewer when LPU is large) per voxel.
+template <int LPU> struct ValueGeom {
+  static constexpr int NBP = (kWave / LPU) >= 8 ? 8 : (kWave / LPU);   // parallel bins per voxel
+  static constexpr int VPW = kWave / (LPU * NBP);                      // voxels per wave
+  static constexpr int VPB = kWavesPerBlock * VPW;                     // voxels per block
+};
+
+// voxels per block of fda_bwd_value_kernel for a given LPU (host side)
+inline int value_voxels_per_block(int lpu) {
+  switch (lpu) {
+    case 1: return ValueGeom<1>::VPB;
+    case 2: return ValueGeom<2>::VPB;
+    case 4: return ValueGeom<4>::VPB;
+    case 8: return ValueGeom<8>::VPB;
+    case 16: return ValueGeom<16>::VPB;
+    default: return ValueGeom<32>::VPB;
+  }
+}
+
+// Sample numbering of the backward gather, head-major so that one block's samples are
+// contiguous: gs = ((b*G + g)*Q + q)*L*K + s.
+__device__ __forceinline__ uint32_t sample_index(int b, int g, int q, int s, int G, int Q, int LK) {
+  return (((uint32_t)b * G + g) * (uint32_t)Q + q) * (uint32_t)LK + s;
 }
 
 // Bins of the backward gather: per (b, g) and level, one bin per possible base corner

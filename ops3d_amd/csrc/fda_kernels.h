@@ -72,21 +72,23 @@ __global__ __launch_bounds__(kBlock) void fda_forward_kernel(const Args a) {
 #pragma unroll
   for (int c = 0; c < CPL; ++c) acc[c] = 0.f;
 
-  const int GD = a.G * a.D;
-  const uint32_t lane_elem = (uint32_t)(g * a.D + j * CPL);
-  const T *vb = static_cast<const T *>(a.value) + (int64_t)b * a.S * GD;
+  // value rows: [B,S,G,D] (stride G*D between voxels) or a head-major copy [B,G,S,D]
+  const int RST = a.vhm ? a.D : a.G * a.D;
+  const uint32_t lane_elem = (uint32_t)((a.vhm ? 0 : g * a.D) + j * CPL);
+  const T *vb = static_cast<const T *>(a.value) +
+                (a.vhm ? ((int64_t)b * a.G + g) * a.S * a.D : (int64_t)b * a.S * a.G * a.D);
   int s = 0;
   for (int l = 0; l < L; ++l) {
     const int Dl = (int)a.shapes[3 * l], Hl = (int)a.shapes[3 * l + 1], Wl = (int)a.shapes[3 * l + 2];
     const int64_t st = a.lsi[l];
-    const uint32_t nbytes = (uint32_t)((int64_t)Dl * Hl * Wl * GD * (int64_t)sizeof(T));
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb + st * GD, nbytes);
+    const uint32_t nbytes = (uint32_t)((int64_t)Dl * Hl * Wl * RST * (int64_t)sizeof(T));
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb + st * RST, nbytes);
 #pragma unroll 2
     for (int k = 0; k < K; ++k, ++s) {
       const float lx = rec[3 * s], ly = rec[3 * s + 1], lz = rec[3 * s + 2];
       const float at = rec[3 * LK + s];
       Sample sm;
-      if (live && sample_setup(lx, ly, lz, Wl, Hl, Dl, GD, sm)) {
+      if (live && sample_setup(lx, ly, lz, Wl, Hl, Dl, RST, sm)) {
         float v[8][CPL];
 #pragma unroll
         for (int c = 0; c < 8; ++c)
@@ -122,8 +124,13 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
   const int q = qb * UPB + ub;
   const bool live = q < a.Q;
   const int L = a.L, K = a.K, LK = L * K, P = a.P;
-  float *rec = lds + ub * (P + LK + 1);   // [0,P): record, later its gradient; [P,P+LK): grad_attn
+  // per unit: [0,P) record (later its gradient), [P,P+LK) grad_attn, then LK stash float4s
+  // and LK keys for the wave's coalesced write-out
+  const int RS = bwd_query_lds_floats(P, LK);
+  float *rec = lds + ub * RS;
   float *gat_s = rec + P;
+  float4 *st_s = reinterpret_cast<float4 *>(lds + ub * RS + ((P + LK + 3) & ~3));
+  uint32_t *key_s = reinterpret_cast<uint32_t *>(st_s + LK);
   const int64_t unit = ((int64_t)b * a.Q + (live ? q : 0)) * a.G + g;
 
   stage_record<T, LPU>(static_cast<const T *>(a.loc_attn) + unit * P, P, j, live, rec);
@@ -133,7 +140,8 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
 
   float tg[CPL];
   if (live) {
-    load_global_elems<T, CPL>(static_cast<const T *>(a.grad_out) + unit * a.D + j * CPL, tg);
+    const int64_t grow = a.ghm ? ((int64_t)b * a.G + g) * a.Q + q : unit;
+    load_global_elems<T, CPL>(static_cast<const T *>(a.grad_out) + grow * a.D + j * CPL, tg);
   } else {
 #pragma unroll
     for (int c = 0; c < CPL; ++c) tg[c] = 0.f;
@@ -143,22 +151,22 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
   for (int l = 0; l < L; ++l) bins_bg += level_bins(a.shapes, l);
   uint32_t bin_base = (uint32_t)(b * a.G + g) * bins_bg;
 
-  const int GD = a.G * a.D;
-  const uint32_t lane_elem = (uint32_t)(g * a.D + j * CPL);
-  const T *vb = static_cast<const T *>(a.value) + (int64_t)b * a.S * GD;
-  const int64_t gs0 = unit * LK;
+  const int RST = a.vhm ? a.D : a.G * a.D;
+  const uint32_t lane_elem = (uint32_t)((a.vhm ? 0 : g * a.D) + j * CPL);
+  const T *vb = static_cast<const T *>(a.value) +
+                (a.vhm ? ((int64_t)b * a.G + g) * a.S * a.D : (int64_t)b * a.S * a.G * a.D);
   int s = 0;
   for (int l = 0; l < L; ++l) {
     const int Dl = (int)a.shapes[3 * l], Hl = (int)a.shapes[3 * l + 1], Wl = (int)a.shapes[3 * l + 2];
     const int64_t st = a.lsi[l];
-    const int64_t nel = (int64_t)Dl * Hl * Wl * GD;
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb + st * GD, (uint32_t)(nel * (int64_t)sizeof(T)));
+    const int64_t nel = (int64_t)Dl * Hl * Wl * RST;
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb + st * RST, (uint32_t)(nel * (int64_t)sizeof(T)));
     for (int k = 0; k < K; ++k, ++s) {
       const float lx = rec[3 * s], ly = rec[3 * s + 1], lz = rec[3 * s + 2];
       const float at = rec[3 * LK + s];
       float gx = 0.f, gy = 0.f, gz = 0.f, ga = 0.f;
       Sample sm;
-      const bool in = live && sample_setup(lx, ly, lz, Wl, Hl, Dl, GD, sm);
+      const bool in = live && sample_setup(lx, ly, lz, Wl, Hl, Dl, RST, sm);
       if (in) {
         float U[8];
 #pragma unroll
@@ -202,21 +210,32 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
         rec[3 * s + 1] = gy * at * (float)Hl;
         rec[3 * s + 2] = gz * at * (float)Dl;
         gat_s[s] = ga;
-        if (live) {
-          const int64_t gsi = gs0 + s;
-          uint32_t key = a.key_invalid;
-          if (in) {
-            key = bin_base + (uint32_t)(((sm.z0 + 1) * (Hl + 1) + (sm.y0 + 1)) * (Wl + 1) + (sm.x0 + 1));
-            a.stash[gsi] = make_float4(sm.wx[1], sm.wy[1], sm.wz[1], at);
-          }
-          a.keys[gsi] = key;
-          a.vals[gsi] = (uint32_t)gsi;
-        }
+        key_s[s] = in ? bin_base + (uint32_t)(((sm.z0 + 1) * (Hl + 1) + (sm.y0 + 1)) * (Wl + 1) + (sm.x0 + 1))
+                      : a.key_invalid;
+        st_s[s] = make_float4(sm.wx[1], sm.wy[1], sm.wz[1], at);
       }
     }
     bin_base += level_bins(a.shapes, l);
   }
   wave_lds_sync();
+  {
+    // the wave's units are consecutive q of one (b, g): their samples are one contiguous range
+    const int q0 = qb * UPB + wave * UPW;
+    const int nlive = min(UPW, a.Q - q0);
+    if (nlive > 0) {
+      const uint32_t gs0 = sample_index(b, g, q0, 0, a.G, a.Q, LK);
+      const int ntot = nlive * LK;
+      for (int e = lane; e < ntot; e += kWave) {
+        const int uu = e / LK, ss = e - uu * LK;
+        const int ubx = wave * UPW + uu;
+        const float4 *stx = reinterpret_cast<const float4 *>(lds + ubx * RS + ((P + LK + 3) & ~3));
+        const uint32_t *kx = reinterpret_cast<const uint32_t *>(stx + LK);
+        a.keys[gs0 + e] = kx[ss];
+        a.vals[gs0 + e] = gs0 + e;
+        a.stash[gs0 + e] = stx[ss];
+      }
+    }
+  }
   // softmax backward over the unit's L*K attention weights
   float dot = 0.f;
   for (int t = j; t < LK; t += LPU) dot = fmaf(rec[3 * LK + t], gat_s[t], dot);
@@ -230,22 +249,38 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Backward phase 3, voxel-major: each unit owns one row grad_value[b, v, g, :] of level l and
-// sums, in registers, attn * w_corner * grad_out over every sample whose corner is v.  Those
-// samples are the ones whose base corner is v - (dz,dy,dx) for the 8 offsets, i.e. the
-// contents of 8 bins of the sorted sample list.  Every output row is written exactly once, in
-// T, in a deterministic order (stable sort of fixed-position keys): no zero-fill, no atomics.
-// Blocks are (b, g, level-voxel-block); heads are mapped to XCDs as in the query kernels.
+// Backward phase 3, voxel-major: one grad_value row grad_value[b, v, g, :] of level l is the
+// sum of attn * w_corner * grad_out over every sample with a corner at v, i.e. over the samples
+// of the 8 bins whose base corner is v - (dz,dy,dx).  NBP lane groups (one per bin, or per
+// 8/NBP bins when LPU is large) sum their bins in registers and are then reduced across the
+// wave with DPP / ds_swizzle; every row is written exactly once, in T, in a deterministic order
+// (stable sort of fixed-position keys): no zero-fill, no atomics.
+template <int LPU, int NBP>
+__device__ __forceinline__ float bin_group_sum(float v) {
+#pragma unroll
+  for (int m = LPU; m < LPU * NBP; m <<= 1) {
+    if (m == 1) v += xor_lane<1>(v);
+    else if (m == 2) v += xor_lane<2>(v);
+    else if (m == 4) v += xor_lane<4>(v);
+    else if (m == 8) v += xor_lane<8>(v);
+    else if (m == 16) v += xor_lane<16>(v);
+    else v += xor_lane<32>(v);
+  }
+  return v;
+}
+
 template <typename T, int CPL, int LPU>
 __global__ __launch_bounds__(kBlock) void fda_bwd_value_kernel(const Args a) {
-  constexpr int UPW = kWave / LPU, UPB = kWavesPerBlock * UPW;
+  using VG = ValueGeom<LPU>;
+  constexpr int NBP = VG::NBP, VPW = VG::VPW, VPB = VG::VPB;
   int b, g, vb;
   if (!map_tile(a, blockIdx.x, b, g, vb)) return;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   const int j = lane & (LPU - 1);
-  const int ub = wave * UPW + lane / LPU;
+  const int dp = (lane / LPU) % NBP;                  // which bin group
+  const int vw = lane / (LPU * NBP);                  // voxel within the wave
   // locate the level of voxel block vb
-  int l = 0, Dl = 0, Hl = 0, Wl = 0;
+  int Dl = 0, Hl = 0, Wl = 0;
   uint32_t bin_lvl = 0, bins_bg = 0;
   int64_t vstart = 0;
   bool found = false;
@@ -253,10 +288,10 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_value_kernel(const Args a) {
   for (int t = 0; t < a.L; ++t) {
     const int d = (int)a.shapes[3 * t], h = (int)a.shapes[3 * t + 1], w = (int)a.shapes[3 * t + 2];
     const int64_t n = (int64_t)d * h * w;
-    const int nvb = (int)((n + UPB - 1) / UPB);
+    const int nvb = (int)((n + VPB - 1) / VPB);
     if (!found) {
       if (rem < nvb) {
-        found = true; l = t; Dl = d; Hl = h; Wl = w; bin_lvl = bins_bg; vstart = a.lsi[t];
+        found = true; Dl = d; Hl = h; Wl = w; bin_lvl = bins_bg; vstart = a.lsi[t];
       } else {
         rem -= nvb;
       }
@@ -264,11 +299,11 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_value_kernel(const Args a) {
     bins_bg += level_bins(a.shapes, t);
   }
   if (!found) return;
-  (void)l;
   const int64_t nvox = (int64_t)Dl * Hl * Wl;
-  const int64_t v = (int64_t)rem * UPB + ub;
-  if (v >= nvox) return;
-  const int x = (int)(v % Wl), y = (int)((v / Wl) % Hl), z = (int)(v / ((int64_t)Wl * Hl));
+  const int64_t v = (int64_t)rem * VPB + wave * VPW + vw;
+  const bool live = v < nvox;   // dead lanes still take part in the cross-group reduction
+  const int64_t vv = live ? v : 0;
+  const int x = (int)(vv % Wl), y = (int)((vv / Wl) % Hl), z = (int)(vv / ((int64_t)Wl * Hl));
   const uint32_t bin_lb = (uint32_t)(b * a.G + g) * bins_bg + bin_lvl;
   const T *go = static_cast<const T *>(a.grad_out);
   const int D = a.D, GD = a.G * a.D;
@@ -276,26 +311,30 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_value_kernel(const Args a) {
   float acc[CPL];
 #pragma unroll
   for (int c = 0; c < CPL; ++c) acc[c] = 0.f;
+  if (live) {
 #pragma unroll 1
-  for (int d = 0; d < 8; ++d) {
-    const int dz = d >> 2, dy = (d >> 1) & 1, dx = d & 1;
-    const uint32_t bin = bin_lb + (uint32_t)(((z - dz + 1) * (Hl + 1) + (y - dy + 1)) * (Wl + 1) + (x - dx + 1));
-    const uint32_t i0 = a.bin_start[bin], i1 = a.bin_start[bin + 1];
-#pragma unroll 2
-    for (uint32_t i = i0; i < i1; ++i) {
-      const uint32_t gsi = a.sorted_vals[i];
-      const float4 st = a.stash[gsi];
-      const uint32_t u = (uint32_t)(((double)gsi + 0.5) * a.inv_lk);   // gsi / (L*K), exact
-      float tg[CPL];
-      load_global_elems<T, CPL>(go + (int64_t)u * D + j * CPL, tg);
-      const float wx = dx ? st.x : 1.f - st.x;
-      const float wy = dy ? st.y : 1.f - st.y;
-      const float wz = dz ? st.z : 1.f - st.z;
-      const float aw = st.w * ((wx * wy) * wz);
+    for (int d = dp; d < 8; d += NBP) {
+      const int dz = d >> 2, dy = (d >> 1) & 1, dx = d & 1;
+      const uint32_t bin = bin_lb + (uint32_t)(((z - dz + 1) * (Hl + 1) + (y - dy + 1)) * (Wl + 1) + (x - dx + 1));
+      const uint32_t i0 = a.bin_start[bin], i1 = a.bin_start[bin + 1];
+#pragma unroll 4
+      for (uint32_t i = i0; i < i1; ++i) {
+        const float4 st = a.sorted_stash[i];
+        const uint32_t row = a.sorted_row[i];
+        float tg[CPL];
+        load_global_elems<T, CPL>(go + (int64_t)row * D + j * CPL, tg);
+        const float wx = dx ? st.x : 1.f - st.x;
+        const float wy = dy ? st.y : 1.f - st.y;
+        const float wz = dz ? st.z : 1.f - st.z;
+        const float aw = st.w * ((wx * wy) * wz);
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) acc[c] = fmaf(aw, tg[c], acc[c]);
+        for (int c = 0; c < CPL; ++c) acc[c] = fmaf(aw, tg[c], acc[c]);
+      }
     }
   }
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) acc[c] = bin_group_sum<LPU, NBP>(acc[c]);
+  if (!live || dp != 0) return;
   const int64_t o = ((int64_t)b * a.S + vstart + v) * GD + g * D + j * CPL;
   if (a.accumulate) {   // caller-owned fp32 buffer: add to what it holds (sole owner, no atomics)
     float *dst = static_cast<float *>(a.out) + o;
@@ -309,8 +348,6 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_value_kernel(const Args a) {
   }
 }
 
-// ---------------------------------------------------------------------------------------------
-// Launch one (T, CPL) family, LPU chosen at run time.
 // which: 0 forward, 1 backward phase 1 (query-major), 2 backward phase 3 (voxel-major)
 template <typename T, int CPL, int LPU>
 hipError_t launch_one(int which, const Args &a, unsigned grid, size_t lds, hipStream_t st) {

@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_support_table(lib):
-    assert lib.ops3d_fda_abi_version() == 2
+    assert lib.ops3d_fda_abi_version() == 3
     F32, F16, BF16 = 0, 1, 2
     for d in (8, 16, 24, 32, 48, 64, 96, 128, 192, 256):
         assert lib.ops3d_fda_supported(BF16, d) == 1, d
@@ -54,6 +54,12 @@ def _has_device():
     import torch
 
     return torch.cuda.is_available()
+
+
+def test_forward_workspace_bytes(lib):
+    assert lib.ops3d_fda_forward_workspace_bytes(2, 1, 73728, 8, 32) == 73728 * 8 * 32 * 2
+    assert lib.ops3d_fda_forward_workspace_bytes(2, 1, 73728, 1, 32) == 0  # G == 1: already head-major
+    assert lib.ops3d_fda_forward_workspace_bytes(7, 1, 73728, 8, 32) == 0
 
 
 def test_workspace_bytes(lib):
@@ -72,8 +78,8 @@ def test_workspace_bytes(lib):
 def _fwd(lib, **kw):
     a = dict(dtype=2, B=1, S=576, G=8, D=32, L=2, Q=576, K=4, step=64)
     a.update(kw)
-    return lib.ops3d_fda_forward(None, None, None, None, None, a["dtype"], a["B"], a["S"], a["G"], a["D"],
-                                 a["L"], a["Q"], a["K"], a["step"], None)
+    return lib.ops3d_fda_forward(None, None, None, None, None, None, 0, a["dtype"], a["B"], a["S"], a["G"],
+                                 a["D"], a["L"], a["Q"], a["K"], a["step"], None)
 
 
 def test_argument_errors_before_device_work(lib):
