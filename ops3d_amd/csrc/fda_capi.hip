@@ -81,7 +81,8 @@ bool pick_config(int dtype, int D, int &cpl, int &lpu) {
     const int c = cands[i];
     if (D % c) continue;
     const int l = D / c;
-    if (is_pow2(l) && l <= 32) {
+    // (D * e) % 16: the backward stages whole grad_output rows through LDS in 16-byte pieces
+    if (is_pow2(l) && l <= 32 && (D * e) % 16 == 0) {
       cpl = c;
       lpu = l;
       return true;

@@ -355,18 +355,19 @@ __host__ __device__ constexpr int bwd_query_lds_floats(int P, int LK) {
 template <int LPU> struct ValueGeom {
   static constexpr int NBP = (kWave / LPU) >= 8 ? 8 : (kWave / LPU);   // parallel bins per voxel
   static constexpr int VPW = kWave / (LPU * NBP);                      // voxels per wave
-  static constexpr int VPB = kWavesPerBlock * VPW;                     // voxels per block
+  static constexpr int VPB = kWavesPerBlock * VPW;                     // voxels per block step
+  static constexpr int VIT = 8;                                        // steps per block
 };
 
 // voxels per block of fda_bwd_value_kernel for a given LPU (host side)
 inline int value_voxels_per_block(int lpu) {
   switch (lpu) {
-    case 1: return ValueGeom<1>::VPB;
-    case 2: return ValueGeom<2>::VPB;
-    case 4: return ValueGeom<4>::VPB;
-    case 8: return ValueGeom<8>::VPB;
-    case 16: return ValueGeom<16>::VPB;
-    default: return ValueGeom<32>::VPB;
+    case 1: return ValueGeom<1>::VPB * ValueGeom<1>::VIT;
+    case 2: return ValueGeom<2>::VPB * ValueGeom<2>::VIT;
+    case 4: return ValueGeom<4>::VPB * ValueGeom<4>::VIT;
+    case 8: return ValueGeom<8>::VPB * ValueGeom<8>::VIT;
+    case 16: return ValueGeom<16>::VPB * ValueGeom<16>::VIT;
+    default: return ValueGeom<32>::VPB * ValueGeom<32>::VIT;
   }
 }
 

@@ -272,26 +272,26 @@ __device__ __forceinline__ float bin_group_sum(float v) {
 template <typename T, int CPL, int LPU>
 __global__ __launch_bounds__(kBlock) void fda_bwd_value_kernel(const Args a) {
   using VG = ValueGeom<LPU>;
-  constexpr int NBP = VG::NBP, VPW = VG::VPW, VPB = VG::VPB;
+  constexpr int NBP = VG::NBP, VPW = VG::VPW, VPB = VG::VPB, VIT = VG::VIT;
   int b, g, vb;
   if (!map_tile(a, blockIdx.x, b, g, vb)) return;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   const int j = lane & (LPU - 1);
   const int dp = (lane / LPU) % NBP;                  // which bin group
   const int vw = lane / (LPU * NBP);                  // voxel within the wave
-  // locate the level of voxel block vb
+  // locate the level of voxel block vb (block-uniform, scalar)
   int Dl = 0, Hl = 0, Wl = 0;
   uint32_t bin_lvl = 0, bins_bg = 0;
-  int64_t vstart = 0;
+  uint32_t vstart = 0;
   bool found = false;
   int rem = vb;
   for (int t = 0; t < a.L; ++t) {
     const int d = (int)a.shapes[3 * t], h = (int)a.shapes[3 * t + 1], w = (int)a.shapes[3 * t + 2];
-    const int64_t n = (int64_t)d * h * w;
-    const int nvb = (int)((n + VPB - 1) / VPB);
+    const uint32_t n = (uint32_t)d * (uint32_t)h * (uint32_t)w;
+    const int nvb = (int)((n + VPB * VIT - 1) / (VPB * VIT));
     if (!found) {
       if (rem < nvb) {
-        found = true; Dl = d; Hl = h; Wl = w; bin_lvl = bins_bg; vstart = a.lsi[t];
+        found = true; Dl = d; Hl = h; Wl = w; bin_lvl = bins_bg; vstart = (uint32_t)a.lsi[t];
       } else {
         rem -= nvb;
       }
@@ -299,52 +299,59 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_value_kernel(const Args a) {
     bins_bg += level_bins(a.shapes, t);
   }
   if (!found) return;
-  const int64_t nvox = (int64_t)Dl * Hl * Wl;
-  const int64_t v = (int64_t)rem * VPB + wave * VPW + vw;
-  const bool live = v < nvox;   // dead lanes still take part in the cross-group reduction
-  const int64_t vv = live ? v : 0;
-  const int x = (int)(vv % Wl), y = (int)((vv / Wl) % Hl), z = (int)(vv / ((int64_t)Wl * Hl));
+  const uint32_t nvox = (uint32_t)Dl * (uint32_t)Hl * (uint32_t)Wl;
+  const uint32_t HW = (uint32_t)Hl * (uint32_t)Wl;
   const uint32_t bin_lb = (uint32_t)(b * a.G + g) * bins_bg + bin_lvl;
+  const uint32_t W1 = (uint32_t)Wl + 1, HW1 = ((uint32_t)Hl + 1) * W1;
   const T *go = static_cast<const T *>(a.grad_out);
   const int D = a.D, GD = a.G * a.D;
+  const int64_t obase = ((int64_t)b * a.S + vstart) * GD + g * D + j * CPL;
 
-  float acc[CPL];
+  for (int it = 0; it < VIT; ++it) {
+    const uint32_t v = (uint32_t)(rem * VIT + it) * VPB + wave * VPW + vw;
+    const bool live = v < nvox;   // dead lanes still take part in the cross-group reduction
+    float acc[CPL];
 #pragma unroll
-  for (int c = 0; c < CPL; ++c) acc[c] = 0.f;
-  if (live) {
+    for (int c = 0; c < CPL; ++c) acc[c] = 0.f;
+    if (live) {
+      const uint32_t z = v / HW, r2 = v - z * HW, y = r2 / (uint32_t)Wl, x = r2 - y * (uint32_t)Wl;
+      // bin of base corner (z-dz, y-dy, x-dx), shifted by +1 on every axis
+      const uint32_t bin_v = bin_lb + (z + 1) * HW1 + (y + 1) * W1 + (x + 1);
 #pragma unroll 1
-    for (int d = dp; d < 8; d += NBP) {
-      const int dz = d >> 2, dy = (d >> 1) & 1, dx = d & 1;
-      const uint32_t bin = bin_lb + (uint32_t)(((z - dz + 1) * (Hl + 1) + (y - dy + 1)) * (Wl + 1) + (x - dx + 1));
-      const uint32_t i0 = a.bin_start[bin], i1 = a.bin_start[bin + 1];
+      for (int d = dp; d < 8; d += NBP) {
+        const int dz = d >> 2, dy = (d >> 1) & 1, dx = d & 1;
+        const uint32_t bin = bin_v - (uint32_t)dz * HW1 - (uint32_t)dy * W1 - (uint32_t)dx;
+        const uint32_t i0 = a.bin_start[bin], i1 = a.bin_start[bin + 1];
 #pragma unroll 4
-      for (uint32_t i = i0; i < i1; ++i) {
-        const float4 st = a.sorted_stash[i];
-        const uint32_t row = a.sorted_row[i];
-        float tg[CPL];
-        load_global_elems<T, CPL>(go + (int64_t)row * D + j * CPL, tg);
-        const float wx = dx ? st.x : 1.f - st.x;
-        const float wy = dy ? st.y : 1.f - st.y;
-        const float wz = dz ? st.z : 1.f - st.z;
-        const float aw = st.w * ((wx * wy) * wz);
+        for (uint32_t i = i0; i < i1; ++i) {
+          const float4 st = a.sorted_stash[i];
+          const uint32_t row = a.sorted_row[i];
+          float tg[CPL];
+          load_global_elems<T, CPL>(go + (size_t)row * D + j * CPL, tg);
+          const float wx = dx ? st.x : 1.f - st.x;
+          const float wy = dy ? st.y : 1.f - st.y;
+          const float wz = dz ? st.z : 1.f - st.z;
+          const float aw = st.w * ((wx * wy) * wz);
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) acc[c] = fmaf(aw, tg[c], acc[c]);
+          for (int c = 0; c < CPL; ++c) acc[c] = fmaf(aw, tg[c], acc[c]);
+        }
       }
     }
-  }
 #pragma unroll
-  for (int c = 0; c < CPL; ++c) acc[c] = bin_group_sum<LPU, NBP>(acc[c]);
-  if (!live || dp != 0) return;
-  const int64_t o = ((int64_t)b * a.S + vstart + v) * GD + g * D + j * CPL;
-  if (a.accumulate) {   // caller-owned fp32 buffer: add to what it holds (sole owner, no atomics)
-    float *dst = static_cast<float *>(a.out) + o;
-    float old[CPL];
-    load_global_elems<float, CPL>(dst, old);
+    for (int c = 0; c < CPL; ++c) acc[c] = bin_group_sum<LPU, NBP>(acc[c]);
+    if (live && dp == 0) {
+      const int64_t o = obase + (int64_t)v * GD;
+      if (a.accumulate) {   // caller-owned fp32 buffer: add to what it holds (sole owner, no atomics)
+        float *dst = static_cast<float *>(a.out) + o;
+        float old[CPL];
+        load_global_elems<float, CPL>(dst, old);
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) acc[c] += old[c];
-    store_elems<float, CPL>(dst, acc);
-  } else {
-    store_elems<T, CPL>(static_cast<T *>(a.out) + o, acc);
+        for (int c = 0; c < CPL; ++c) acc[c] += old[c];
+        store_elems<float, CPL>(dst, acc);
+      } else {
+        store_elems<T, CPL>(static_cast<T *>(a.out) + o, acc);
+      }
+    }
   }
 }
 
