@@ -20,7 +20,8 @@ import os
 import torch  # imported first: its HIP runtime is the one libops3d_fda.so binds to
 
 _PKG_DIR = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_PKG_DIR, "libops3d_fda.so")
+# OPS3D_FDA_LIBRARY selects another build of the library (e.g. a tuning variant)
+LIB_PATH = os.environ.get("OPS3D_FDA_LIBRARY") or os.path.join(_PKG_DIR, "libops3d_fda.so")
 
 OPS3D_FDA_OK, OPS3D_FDA_EINVAL, OPS3D_FDA_ERUNTIME = 0, 1, 2
 _DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}

@@ -356,7 +356,10 @@ template <int LPU> struct ValueGeom {
   static constexpr int NBP = (kWave / LPU) >= 8 ? 8 : (kWave / LPU);   // parallel bins per voxel
   static constexpr int VPW = kWave / (LPU * NBP);                      // voxels per wave
   static constexpr int VPB = kWavesPerBlock * VPW;                     // voxels per block step
-  static constexpr int VIT = 8;                                        // steps per block
+#ifndef OPS3D_FDA_VALUE_VIT
+#define OPS3D_FDA_VALUE_VIT 8
+#endif
+  static constexpr int VIT = OPS3D_FDA_VALUE_VIT;                      // steps per block
 };
 
 // voxels per block of fda_bwd_value_kernel for a given LPU (host side)

@@ -19,6 +19,10 @@
 
 #include "fda_device.h"
 
+#ifndef OPS3D_FDA_VALUE_UNROLL
+#define OPS3D_FDA_VALUE_UNROLL 4
+#endif
+
 namespace ops3d_fda {
 
 template <typename T, int N>
@@ -322,7 +326,7 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_value_kernel(const Args a) {
         const int dz = d >> 2, dy = (d >> 1) & 1, dx = d & 1;
         const uint32_t bin = bin_v - (uint32_t)dz * HW1 - (uint32_t)dy * W1 - (uint32_t)dx;
         const uint32_t i0 = a.bin_start[bin], i1 = a.bin_start[bin + 1];
-#pragma unroll 4
+#pragma unroll OPS3D_FDA_VALUE_UNROLL
         for (uint32_t i = i0; i < i1; ++i) {
           const float4 st = a.sorted_stash[i];
           const uint32_t row = a.sorted_row[i];
