@@ -379,6 +379,8 @@ static int backward_impl(const void *value, const int64_t *spatial_shapes,
   const int64_t nval = (int64_t)batch * spatial_size * num_heads * channels;
   const bool work = (int64_t)batch * num_query > 0;
   if (nval == 0 && !work) return OPS3D_FDA_OK;
+  if ((int64_t)batch * num_query * num_heads * channels >= ((int64_t)1 << 32))
+    return fail(OPS3D_FDA_EINVAL, "grad_output too large for 32-bit element offsets (B*Q*G*D >= 2^32)");
   if (nval > 0 && !grad_value) return fail(OPS3D_FDA_EINVAL, "grad_value is NULL");
   if (!spatial_shapes || !level_start_index) return fail(OPS3D_FDA_EINVAL, "NULL pointer argument");
   if (work && (!sampling_loc_attn || !grad_output || !grad_sampling_loc_attn || (!value && spatial_size > 0)))

@@ -19,6 +19,12 @@
 
 #include "fda_device.h"
 
+#ifndef OPS3D_FDA_VALUE_REVERSE
+#define OPS3D_FDA_VALUE_REVERSE 1
+#endif
+#ifndef OPS3D_FDA_VALUE_BALANCED
+#define OPS3D_FDA_VALUE_BALANCED 1
+#endif
 #ifndef OPS3D_FDA_VALUE_UNROLL
 #define OPS3D_FDA_VALUE_UNROLL 4
 #endif
@@ -281,21 +287,25 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_value_kernel(const Args a) {
   if (!map_tile(a, blockIdx.x, b, g, vb)) return;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   const int j = lane & (LPU - 1);
-  const int dp = (lane / LPU) % NBP;                  // which bin group
-  const int vw = lane / (LPU * NBP);                  // voxel within the wave
-  // locate the level of voxel block vb (block-uniform, scalar)
+  const int dp = (lane / LPU) % NBP;                  // which lane group of the pair
+  const int vw = lane / (LPU * NBP);                  // pair within the wave
+  // A "pair" is two x-neighbour voxels (x0, x0+1) of one row; pairs per level D*H*ceil(W/2).
+  // Locate the level of pair block vb (block-uniform); coarse (last) levels first: their bins
+  // hold the most samples, so their blocks are the longest and must not start last.
   int Dl = 0, Hl = 0, Wl = 0;
   uint32_t bin_lvl = 0, bins_bg = 0;
   uint32_t vstart = 0;
   bool found = false;
   int rem = vb;
-  for (int t = 0; t < a.L; ++t) {
+  for (int tt = 0; tt < a.L; ++tt) {
+    const int t = OPS3D_FDA_VALUE_REVERSE ? a.L - 1 - tt : tt;
     const int d = (int)a.shapes[3 * t], h = (int)a.shapes[3 * t + 1], w = (int)a.shapes[3 * t + 2];
-    const uint32_t n = (uint32_t)d * (uint32_t)h * (uint32_t)w;
+    const uint32_t n = (uint32_t)d * (uint32_t)h * (((uint32_t)w + 1) >> 1);
     const int nvb = (int)((n + VPB * VIT - 1) / (VPB * VIT));
     if (!found) {
       if (rem < nvb) {
-        found = true; Dl = d; Hl = h; Wl = w; bin_lvl = bins_bg; vstart = (uint32_t)a.lsi[t];
+        found = true; Dl = d; Hl = h; Wl = w; vstart = (uint32_t)a.lsi[t];
+        for (int u = 0; u < t; ++u) bin_lvl += level_bins(a.shapes, u);
       } else {
         rem -= nvb;
       }
@@ -303,8 +313,9 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_value_kernel(const Args a) {
     bins_bg += level_bins(a.shapes, t);
   }
   if (!found) return;
-  const uint32_t nvox = (uint32_t)Dl * (uint32_t)Hl * (uint32_t)Wl;
-  const uint32_t HW = (uint32_t)Hl * (uint32_t)Wl;
+  const uint32_t Wp = ((uint32_t)Wl + 1) >> 1;          // pairs per row
+  const uint32_t npair = (uint32_t)Dl * (uint32_t)Hl * Wp;
+  const uint32_t HWp = (uint32_t)Hl * Wp;
   const uint32_t bin_lb = (uint32_t)(b * a.G + g) * bins_bg + bin_lvl;
   const uint32_t W1 = (uint32_t)Wl + 1, HW1 = ((uint32_t)Hl + 1) * W1;
   const T *go = static_cast<const T *>(a.grad_out);
@@ -313,47 +324,87 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_value_kernel(const Args a) {
 
   for (int it = 0; it < VIT; ++it) {
     const uint32_t v = (uint32_t)(rem * VIT + it) * VPB + wave * VPW + vw;
-    const bool live = v < nvox;   // dead lanes still take part in the cross-group reduction
-    float acc[CPL];
+    const bool live = v < npair;   // dead lanes still take part in the cross-group reduction
+    float acc0[CPL], acc1[CPL];      // voxels x0 and x0 + 1
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) acc[c] = 0.f;
+    for (int c = 0; c < CPL; ++c) acc0[c] = acc1[c] = 0.f;
+    uint32_t z = 0, y = 0, x0 = 0;
     if (live) {
-      const uint32_t z = v / HW, r2 = v - z * HW, y = r2 / (uint32_t)Wl, x = r2 - y * (uint32_t)Wl;
-      // bin of base corner (z-dz, y-dy, x-dx), shifted by +1 on every axis
-      const uint32_t bin_v = bin_lb + (z + 1) * HW1 + (y + 1) * W1 + (x + 1);
-#pragma unroll 1
-      for (int d = dp; d < 8; d += NBP) {
-        const int dz = d >> 2, dy = (d >> 1) & 1, dx = d & 1;
-        const uint32_t bin = bin_v - (uint32_t)dz * HW1 - (uint32_t)dy * W1 - (uint32_t)dx;
-        const uint32_t i0 = a.bin_start[bin], i1 = a.bin_start[bin + 1];
-#pragma unroll OPS3D_FDA_VALUE_UNROLL
-        for (uint32_t i = i0; i < i1; ++i) {
-          const float4 st = a.sorted_stash[i];
-          const uint32_t row = a.sorted_row[i];
-          float tg[CPL];
-          load_global_elems<T, CPL>(go + (size_t)row * D + j * CPL, tg);
-          const float wx = dx ? st.x : 1.f - st.x;
-          const float wy = dy ? st.y : 1.f - st.y;
-          const float wz = dz ? st.z : 1.f - st.z;
-          const float aw = st.w * ((wx * wy) * wz);
+      z = v / HWp;
+      const uint32_t r2 = v - z * HWp;
+      y = r2 / Wp;
+      x0 = (r2 - y * Wp) * 2;
+      // Samples with a corner on x0 or x0+1 in row (z, y): for each (dz, dy), the contiguous
+      // bins of base x0-1, x0, x0+1 (shifted by +1: x0, x0+1, x0+2).  Base x0-1 feeds x0 (dx=1),
+      // base x0 feeds x0 (dx=0) and x0+1 (dx=1), base x0+1 feeds x0+1 (dx=0).  The 4 ranges are
+      // concatenated and dealt round-robin to the pair's NBP lane groups (equal work whatever
+      // the bin sizes); each grad_out row is loaded and widened once for both voxels.
+      const uint32_t bin_p = bin_lb + (z + 1) * HW1 + (y + 1) * W1 + x0;   // shifted base x0-1
+      const bool two = x0 + 1 < (uint32_t)Wl;
+      uint32_t st_r[4], m1_r[4], m2_r[4], cum[4];
+      uint32_t n = 0;
 #pragma unroll
-          for (int c = 0; c < CPL; ++c) acc[c] = fmaf(aw, tg[c], acc[c]);
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t rb = bin_p - (uint32_t)(r >> 1) * HW1 - (uint32_t)(r & 1) * W1;   // (dz, dy) = (r>>1, r&1)
+        // a pair with one voxel (x0 = W-1) has no bin of base x0+1: bin_start[rb + 3] is past
+        // its row (at the end of the array: never written), so its range ends at s2
+        const uint32_t s0 = a.bin_start[rb], s1 = a.bin_start[rb + 1], s2 = a.bin_start[rb + 2];
+        const uint32_t s3 = two ? a.bin_start[rb + 3] : s2;
+        st_r[r] = s0;
+        m1_r[r] = s1;
+        m2_r[r] = s2;
+        n += s3 - s0;
+        cum[r] = n;
+      }
+#pragma unroll OPS3D_FDA_VALUE_UNROLL
+      for (uint32_t t = (uint32_t)dp; t < n; t += NBP) {
+        const int r = (t >= cum[0]) + (t >= cum[1]) + (t >= cum[2]);
+        const uint32_t base = r == 0 ? 0u : (r == 1 ? cum[0] : (r == 2 ? cum[1] : cum[2]));
+        const uint32_t s0 = r == 0 ? st_r[0] : (r == 1 ? st_r[1] : (r == 2 ? st_r[2] : st_r[3]));
+        const uint32_t m1 = r == 0 ? m1_r[0] : (r == 1 ? m1_r[1] : (r == 2 ? m1_r[2] : m1_r[3]));
+        const uint32_t m2 = r == 0 ? m2_r[0] : (r == 1 ? m2_r[1] : (r == 2 ? m2_r[2] : m2_r[3]));
+        const uint32_t i = s0 + (t - base);
+        const float4 st = a.sorted_stash[i];
+        const uint32_t row = a.sorted_row[i];
+        float tg[CPL];
+        load_global_elems<T, CPL>(go + (size_t)(row * (uint32_t)D) + j * CPL, tg);
+        const float wy = (r & 1) ? st.y : 1.f - st.y;
+        const float wz = (r >> 1) ? st.z : 1.f - st.z;
+        const float ayz = st.w;
+        // base x0-1: (x0, dx=1); base x0: (x0, dx=0), (x0+1, dx=1); base x0+1: (x0+1, dx=0)
+        const float wx0 = i < m1 ? st.x : (i < m2 ? 1.f - st.x : 0.f);
+        const float wx1 = i < m1 ? 0.f : (i < m2 ? st.x : 1.f - st.x);
+        const float aw0 = ayz * ((wx0 * wy) * wz);
+        const float aw1 = ayz * ((wx1 * wy) * wz);
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+          acc0[c] = fmaf(aw0, tg[c], acc0[c]);
+          acc1[c] = fmaf(aw1, tg[c], acc1[c]);
         }
       }
     }
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) acc[c] = bin_group_sum<LPU, NBP>(acc[c]);
-    if (live && dp == 0) {
-      const int64_t o = obase + (int64_t)v * GD;
-      if (a.accumulate) {   // caller-owned fp32 buffer: add to what it holds (sole owner, no atomics)
-        float *dst = static_cast<float *>(a.out) + o;
-        float old[CPL];
-        load_global_elems<float, CPL>(dst, old);
+    for (int c = 0; c < CPL; ++c) {
+      acc0[c] = bin_group_sum<LPU, NBP>(acc0[c]);
+      acc1[c] = bin_group_sum<LPU, NBP>(acc1[c]);
+    }
+    if (live && dp < 2) {   // lane group 0 stores x0, group 1 stores x0 + 1
+      const uint32_t x = x0 + (uint32_t)dp;
+      if (x < (uint32_t)Wl) {
+        const int64_t o = obase + (int64_t)((z * (uint32_t)Hl + y) * (uint32_t)Wl + x) * GD;
+        float res[CPL];
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) acc[c] += old[c];
-        store_elems<float, CPL>(dst, acc);
-      } else {
-        store_elems<T, CPL>(static_cast<T *>(a.out) + o, acc);
+        for (int c = 0; c < CPL; ++c) res[c] = dp == 0 ? acc0[c] : acc1[c];
+        if (a.accumulate) {   // caller-owned fp32 buffer: add to what it holds (sole owner, no atomics)
+          float *dst = static_cast<float *>(a.out) + o;
+          float old[CPL];
+          load_global_elems<float, CPL>(dst, old);
+#pragma unroll
+          for (int c = 0; c < CPL; ++c) res[c] += old[c];
+          store_elems<float, CPL>(dst, res);
+        } else {
+          store_elems<T, CPL>(static_cast<T *>(a.out) + o, res);
+        }
       }
     }
   }
