@@ -26,7 +26,7 @@
 #define OPS3D_FDA_VALUE_BALANCED 1
 #endif
 #ifndef OPS3D_FDA_VALUE_UNROLL
-#define OPS3D_FDA_VALUE_UNROLL 4
+#define OPS3D_FDA_VALUE_UNROLL 2
 #endif
 
 namespace ops3d_fda {
