@@ -16,7 +16,7 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_NAME = "libops3d_fda.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["fda_capi.hip", "fda_f32.hip", "fda_f16.hip", "fda_bf16.hip"]
+SOURCES = ["fda_capi.hip", "fda_binsort.hip", "fda_f32.hip", "fda_f16.hip", "fda_bf16.hip"]
 ARCH = "gfx950"
 
 # -packed-fp32-ops off: hipcc must not form v_pk_{add,mul,fma}_f32 on its own.

@@ -16,6 +16,9 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <stdlib.h>
+
+#include <algorithm>
 #include <string>
 
 #include <hipcub/hipcub.hpp>
@@ -27,6 +30,12 @@ namespace ops3d_fda {
 hipError_t launch_f32(int, int, int, const Args &, unsigned, size_t, hipStream_t);
 hipError_t launch_f16(int, int, int, const Args &, unsigned, size_t, hipStream_t);
 hipError_t launch_bf16(int, int, int, const Args &, unsigned, size_t, hipStream_t);
+bool binsort_supported(uint32_t n, int bits);
+size_t binsort_temp_bytes(uint32_t n, int bits);
+hipError_t binsort_pairs(uint32_t *keys_a, uint32_t *vals_a, uint32_t *keys_b, uint32_t *vals_b, uint32_t n,
+                         int bits, void *temp, size_t temp_bytes, const float4 *stash, float4 *sorted_stash,
+                         uint32_t *sorted_row, double inv_lk, uint32_t Q, uint32_t G, int ghm,
+                         const uint32_t **sorted_keys, hipStream_t st);
 }  // namespace ops3d_fda
 
 using namespace ops3d_fda;
@@ -184,6 +193,16 @@ struct BwdLayout {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Sort of the backward: the library's own bin sort (default) or hipCUB's radix sort followed by
+// a permute pass (OPS3D_FDA_SORT=cub), read once per process.
+bool use_binsort() {
+  static const bool on = [] {
+    const char *v = getenv("OPS3D_FDA_SORT");
+    return !(v && std::string(v) == "cub");
+  }();
+  return on;
+}
+
 int bwd_layout(int B, int S, int G, int D, int e, int L, int Q, int K, BwdLayout &ly) {
   ly = BwdLayout{};
   ly.n = (uint64_t)B * Q * G * L * K;
@@ -201,6 +220,7 @@ int bwd_layout(int B, int S, int G, int D, int e, int L, int Q, int K, BwdLayout
                                                       bits, (hipStream_t)0);
     if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "radix sort size query failed: %s", hipGetErrorString(e));
   }
+  if (ly.n > 0) temp = std::max(temp, binsort_temp_bytes((uint32_t)ly.n, bits));
   ly.temp_bytes = temp;
   size_t o = 0;
   const size_t n4 = align256(ly.n * 4);
@@ -274,19 +294,35 @@ hipError_t launch_head_major(const void *src, void *dst, int64_t B, int64_t N, i
 __global__ __launch_bounds__(256) void bin_start_kernel(const uint32_t *keys, uint32_t n, uint32_t *bin_start,
                                                         uint32_t nbins_bound, const int64_t *shapes, int L,
                                                         int BG) {
+  // bin_start[bb] = lower_bound(keys, bb) for bb in [0, last]: sorted element i starts every bin
+  // in (keys[i-1], keys[i]] (i = 0: [0, keys[0]]; i = n: (keys[n-1], last]).  Gaps of more than
+  // kSmallGap bins are filled by the whole wave.
+  constexpr uint64_t kSmallGap = 4;
   uint32_t per = 0;
   for (int l = 0; l < L; ++l) per += level_bins(shapes, l);
   const uint64_t real = (uint64_t)per * (uint64_t)BG;
   const uint64_t last = real < nbins_bound ? real : nbins_bound;
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-  for (uint64_t bb = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; bb <= last; bb += stride) {
-    uint32_t lo = 0, hi = n;
-    while (lo < hi) {
-      const uint32_t mid = (lo + hi) >> 1;
-      if (keys[mid] < (uint32_t)bb) lo = mid + 1;
-      else hi = mid;
+  const int lane = threadIdx.x & (kWave - 1);
+  for (uint64_t base = (uint64_t)blockIdx.x * blockDim.x; base <= n; base += stride) {
+    const uint64_t i = base + threadIdx.x;
+    uint64_t lo = 1, hi = 0;                          // empty
+    if (i <= n) {
+      lo = i == 0 ? 0 : (uint64_t)keys[i - 1] + 1;
+      hi = i == n ? last : ((uint64_t)keys[i] < last ? (uint64_t)keys[i] : last);
     }
-    bin_start[bb] = lo;
+    const bool big = lo <= hi && hi - lo >= kSmallGap;
+    if (lo <= hi && !big)
+      for (uint64_t bb = lo; bb <= hi; ++bb) bin_start[bb] = (uint32_t)i;
+    uint64_t m = __ballot(big);
+    while (m) {
+      const int src = __builtin_ctzll(m);
+      m &= m - 1;
+      const uint64_t blo = ((uint64_t)__shfl(( uint32_t)(lo >> 32), src) << 32) | __shfl((uint32_t)lo, src);
+      const uint64_t bhi = ((uint64_t)__shfl((uint32_t)(hi >> 32), src) << 32) | __shfl((uint32_t)hi, src);
+      const uint32_t bi = (uint32_t)__shfl((uint32_t)i, src);
+      for (uint64_t bb = blo + lane; bb <= bhi; bb += kWave) bin_start[bb] = bi;
+    }
   }
 }
 
@@ -403,6 +439,7 @@ static int backward_impl(const void *value, const int64_t *spatial_shapes,
   uint32_t *srow = reinterpret_cast<uint32_t *>(ws + ly.off_srow);
   uint32_t *bins = reinterpret_cast<uint32_t *>(ws + ly.off_bins);
   void *temp = ws + ly.off_temp;
+  const uint32_t *sorted_keys = keys_out;
 
   Args &a = geo.a;
   a.value = value;
@@ -437,29 +474,35 @@ static int backward_impl(const void *value, const int64_t *spatial_shapes,
       return fail(OPS3D_FDA_ERUNTIME, "backward query kernel launch failed: %s (grid=%u, lds=%zu)",
                   hipGetErrorString(e), geo.grid, geo.lds);
     prof_mark(2, st);
-    // phase 2: stable radix sort of (bin, sample) pairs
-    size_t tb = ly.temp_bytes;
-    e = hipcub::DeviceRadixSort::SortPairs(temp, tb, keys_in, keys_out, vals_in, vals_out, (int)ly.n, 0,
-                                           ly.key_bits, st);
-    if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "radix sort failed: %s", hipGetErrorString(e));
-    // stash and grad_output row of every sample in sorted order
-    a.sorted_vals = vals_out;
-    a.sorted_stash = sstash;
-    a.sorted_row = srow;
-    unsigned pblocks = (unsigned)((ly.n + 255) / 256);
-    if (pblocks > 16384) pblocks = 16384;
-    hipLaunchKernelGGL(fda_bwd_permute_kernel, dim3(pblocks), dim3(256), 0, st, a, (uint32_t)ly.n);
-    e = hipGetLastError();
-    if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "permute kernel launch failed: %s", hipGetErrorString(e));
+    // phase 2: stable sort of (bin, sample) pairs; stash and grad_output row in sorted order
+    if (use_binsort() && binsort_supported((uint32_t)ly.n, ly.key_bits)) {
+      e = binsort_pairs(keys_in, vals_in, keys_out, vals_out, (uint32_t)ly.n, ly.key_bits, temp, ly.temp_bytes,
+                        stash, sstash, srow, a.inv_lk, (uint32_t)num_query, (uint32_t)num_heads, a.ghm,
+                        &sorted_keys, st);
+      if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "bin sort failed: %s", hipGetErrorString(e));
+    } else {
+      size_t tb = ly.temp_bytes;
+      e = hipcub::DeviceRadixSort::SortPairs(temp, tb, keys_in, keys_out, vals_in, vals_out, (int)ly.n, 0,
+                                             ly.key_bits, st);
+      if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "radix sort failed: %s", hipGetErrorString(e));
+      a.sorted_vals = vals_out;
+      a.sorted_stash = sstash;
+      a.sorted_row = srow;
+      unsigned pblocks = (unsigned)((ly.n + 255) / 256);
+      if (pblocks > 16384) pblocks = 16384;
+      hipLaunchKernelGGL(fda_bwd_permute_kernel, dim3(pblocks), dim3(256), 0, st, a, (uint32_t)ly.n);
+      e = hipGetLastError();
+      if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "permute kernel launch failed: %s", hipGetErrorString(e));
+    }
   } else {
     prof_mark(2, st);
   }
   prof_mark(3, st);
   {
-    const uint64_t nb = ly.nbins_bound + 1;
+    const uint64_t nb = ly.n + 1;
     unsigned blocks = (unsigned)((nb + 255) / 256);
     if (blocks > 16384) blocks = 16384;
-    hipLaunchKernelGGL(bin_start_kernel, dim3(blocks), dim3(256), 0, st, keys_out, work ? (uint32_t)ly.n : 0u,
+    hipLaunchKernelGGL(bin_start_kernel, dim3(blocks), dim3(256), 0, st, sorted_keys, work ? (uint32_t)ly.n : 0u,
                        bins, (uint32_t)ly.nbins_bound, spatial_shapes, num_levels, batch * num_heads);
     e = hipGetLastError();
     if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "bin kernel launch failed: %s", hipGetErrorString(e));
@@ -471,7 +514,6 @@ static int backward_impl(const void *value, const int64_t *spatial_shapes,
     const int VPB = value_voxels_per_block(geo.lpu);
     const int nvb_bound = (int)(((int64_t)spatial_size + VPB - 1) / VPB) + num_levels;
     set_grid(g3.a, nvb_bound, g3.grid);
-    g3.a.sorted_vals = vals_out;
     g3.a.sorted_stash = sstash;
     g3.a.sorted_row = srow;
     g3.a.bin_start = bins;

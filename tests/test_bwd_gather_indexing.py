@@ -119,3 +119,42 @@ def test_gather_index_emulation_matches_oracle(shapes, B, Q, G, K):
     gv = emulate_grad_value(value.numpy(), shapes, sla.numpy(), go.numpy(), K)
     ref, _ = oracle.backward(value.numpy(), shapes, sla.numpy(), go.numpy(), K, coord_mode=1)
     np.testing.assert_allclose(gv, ref, rtol=1e-9, atol=1e-11)
+
+
+def emulate_bin_start_fill(skeys, last, small_gap=4, wave=64):
+    """The bin-offset kernel's boundary fill: element i starts every bin in (k[i-1], k[i]],
+    clamped to [0, last]; wide gaps are filled wave-cooperatively (same values)."""
+    n = len(skeys)
+    out = np.full(last + 1, -1, dtype=np.int64)
+    for i in range(n + 1):
+        lo = 0 if i == 0 else int(skeys[i - 1]) + 1
+        hi = last if i == n else min(int(skeys[i]), last)
+        if lo > hi:
+            continue
+        if hi - lo < small_gap:
+            out[lo:hi + 1] = i
+        else:
+            for lane in range(wave):
+                out[lo + lane:hi + 1:wave] = i
+    return out
+
+
+@pytest.mark.parametrize("case", ["random", "all_invalid", "empty", "dense", "sparse_tail"])
+def test_bin_start_fill_matches_lower_bound(case):
+    rng = np.random.default_rng(3)
+    last, invalid = 500, 800
+    if case == "random":
+        keys = rng.integers(0, last + 1, 300)
+        keys[rng.random(300) < 0.1] = invalid
+    elif case == "all_invalid":
+        keys = np.full(50, invalid)
+    elif case == "empty":
+        keys = np.zeros(0, dtype=np.int64)
+    elif case == "dense":
+        keys = rng.integers(0, 20, 400)
+    else:
+        keys = rng.integers(0, 7, 30)
+    skeys = np.sort(keys, kind="stable")
+    got = emulate_bin_start_fill(skeys, last)
+    want = np.searchsorted(skeys, np.arange(last + 1), side="left")
+    np.testing.assert_array_equal(got, want)

@@ -130,6 +130,12 @@ def test_out_of_volume_fp32(gpu_device):
     _check("oob fp32", inp, gpu_device, torch.float32)
 
 
+def test_all_samples_outside_volume(gpu_device):
+    """Every sample outside [-1, size): all keys invalid, grad_value all zero."""
+    inp = random_inputs([(6, 5, 7), (3, 2, 4)], 1, 200, 8, 32, 4, torch.float32, seed=6, lo=1.6, hi=2.5)
+    _check("all outside fp32", inp, gpu_device, torch.float32)
+
+
 # --- head widths, head counts (XCD mappings), dtypes ---------------------------------------
 @pytest.mark.parametrize("D", [8, 16, 24, 32, 48, 64, 96, 128])
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16])
