@@ -15,13 +15,9 @@
 //     ~0.5 lanes/clock per CU, far below what 8 corners x D channels per sample need).
 #include <stdarg.h>
 #include <stdio.h>
-
 #include <stdlib.h>
 
-#include <algorithm>
 #include <string>
-
-#include <hipcub/hipcub.hpp>
 
 #include "../../include/ops3d_fda.h"
 #include "fda_device.h"
@@ -45,7 +41,7 @@ namespace {
 thread_local std::string g_last_error;
 
 // backward phase timing (ops3d_fda_profile_*)
-// events 0..5: backward (copies | query kernel | sort+permute | bin offsets | value kernel)
+// events 0..5: backward (copies | query kernel | bin sort | bin offsets | value kernel)
 // events 6..8: forward (head-major copy | forward kernel)
 constexpr int kProfEvents = 9;
 bool g_prof_on = false;
@@ -180,7 +176,7 @@ void set_grid(Args &a, int ncol_per_b, unsigned &grid_out) {
 //   stash, sorted stash                 : N float4 each
 //   sorted grad_output rows             : N uint32
 //   bin_start                           : nbins_bound + 1 uint32
-//   sort temporary storage              : as hipcub reports
+//   sort temporary storage              : tile histograms, their scan and its temporary
 // nbins_bound = B*G*8*S bounds the real bin count sum_l (D+1)(H+1)(W+1) without reading the
 // device-resident level shapes on the host.
 struct BwdLayout {
@@ -193,15 +189,6 @@ struct BwdLayout {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Sort of the backward: the library's own bin sort (default) or hipCUB's radix sort followed by
-// a permute pass (OPS3D_FDA_SORT=cub), read once per process.
-bool use_binsort() {
-  static const bool on = [] {
-    const char *v = getenv("OPS3D_FDA_SORT");
-    return !(v && std::string(v) == "cub");
-  }();
-  return on;
-}
 
 int bwd_layout(int B, int S, int G, int D, int e, int L, int Q, int K, BwdLayout &ly) {
   ly = BwdLayout{};
@@ -215,12 +202,11 @@ int bwd_layout(int B, int S, int G, int D, int e, int L, int Q, int K, BwdLayout
   ly.key_bits = bits;
   size_t temp = 0;
   if (ly.n > 0) {
-    hipError_t e = hipcub::DeviceRadixSort::SortPairs(nullptr, temp, (uint32_t *)nullptr, (uint32_t *)nullptr,
-                                                      (uint32_t *)nullptr, (uint32_t *)nullptr, (int)ly.n, 0,
-                                                      bits, (hipStream_t)0);
-    if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "radix sort size query failed: %s", hipGetErrorString(e));
+    if (!binsort_supported((uint32_t)ly.n, bits))
+      return fail(OPS3D_FDA_EINVAL, "backward too large for the bin sort (N=%llu)", (unsigned long long)ly.n);
+    temp = binsort_temp_bytes((uint32_t)ly.n, bits);
+    if (temp == 0) return fail(OPS3D_FDA_ERUNTIME, "bin sort size query failed");
   }
-  if (ly.n > 0) temp = std::max(temp, binsort_temp_bytes((uint32_t)ly.n, bits));
   ly.temp_bytes = temp;
   size_t o = 0;
   const size_t n4 = align256(ly.n * 4);
@@ -238,20 +224,6 @@ int bwd_layout(int B, int S, int G, int D, int e, int L, int Q, int K, BwdLayout
   ly.off_ghm = o; o += G > 1 ? align256((size_t)B * Q * G * D * e) : 0;
   ly.total = o;
   return OPS3D_FDA_OK;
-}
-
-// After the sort: the stash and the grad_output row of every sorted sample, in sorted order,
-// so that the value kernel streams them instead of chasing sample -> stash -> row.
-__global__ __launch_bounds__(256) void fda_bwd_permute_kernel(const Args a, uint32_t n) {
-  const uint32_t stride = gridDim.x * blockDim.x;
-  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-    const uint32_t gsi = a.sorted_vals[i];
-    const uint32_t t = (uint32_t)(((double)gsi + 0.5) * a.inv_lk);   // gsi / (L*K), exact
-    const uint32_t bg = t / (uint32_t)a.Q, q = t - bg * (uint32_t)a.Q;
-    const uint32_t b = bg / (uint32_t)a.G, g = bg - b * (uint32_t)a.G;
-    const_cast<float4 *>(a.sorted_stash)[i] = a.stash[gsi];
-    const_cast<uint32_t *>(a.sorted_row)[i] = a.ghm ? t : (b * (uint32_t)a.Q + q) * (uint32_t)a.G + g;
-  }
 }
 
 // [B, N, G, R words] -> [B, G, N, R words]: the head-major copy of value / grad_output, so that
@@ -475,25 +447,10 @@ static int backward_impl(const void *value, const int64_t *spatial_shapes,
                   hipGetErrorString(e), geo.grid, geo.lds);
     prof_mark(2, st);
     // phase 2: stable sort of (bin, sample) pairs; stash and grad_output row in sorted order
-    if (use_binsort() && binsort_supported((uint32_t)ly.n, ly.key_bits)) {
-      e = binsort_pairs(keys_in, vals_in, keys_out, vals_out, (uint32_t)ly.n, ly.key_bits, temp, ly.temp_bytes,
-                        stash, sstash, srow, a.inv_lk, (uint32_t)num_query, (uint32_t)num_heads, a.ghm,
-                        &sorted_keys, st);
-      if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "bin sort failed: %s", hipGetErrorString(e));
-    } else {
-      size_t tb = ly.temp_bytes;
-      e = hipcub::DeviceRadixSort::SortPairs(temp, tb, keys_in, keys_out, vals_in, vals_out, (int)ly.n, 0,
-                                             ly.key_bits, st);
-      if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "radix sort failed: %s", hipGetErrorString(e));
-      a.sorted_vals = vals_out;
-      a.sorted_stash = sstash;
-      a.sorted_row = srow;
-      unsigned pblocks = (unsigned)((ly.n + 255) / 256);
-      if (pblocks > 16384) pblocks = 16384;
-      hipLaunchKernelGGL(fda_bwd_permute_kernel, dim3(pblocks), dim3(256), 0, st, a, (uint32_t)ly.n);
-      e = hipGetLastError();
-      if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "permute kernel launch failed: %s", hipGetErrorString(e));
-    }
+    e = binsort_pairs(keys_in, vals_in, keys_out, vals_out, (uint32_t)ly.n, ly.key_bits, temp, ly.temp_bytes,
+                      stash, sstash, srow, a.inv_lk, (uint32_t)num_query, (uint32_t)num_heads, a.ghm,
+                      &sorted_keys, st);
+    if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "bin sort failed: %s", hipGetErrorString(e));
   } else {
     prof_mark(2, st);
   }

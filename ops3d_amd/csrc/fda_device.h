@@ -46,7 +46,6 @@ struct Args {
   uint32_t *keys;             // [N] bin of each sample's base corner (key_invalid if skipped)
   uint32_t *vals;             // [N] sample index (iota), sort payload
   float4 *stash;              // [N] (fx, fy, fz, attn) of each sample
-  const uint32_t *sorted_vals;  // [N] sample indices sorted by bin
   const uint32_t *bin_start;    // [nbins_bound + 1] first sorted position of each bin
   const float4 *sorted_stash;   // [N] stash in sorted order
   const uint32_t *sorted_row;   // [N] grad_output row (b*Q + q)*G + g in sorted order
@@ -91,6 +90,10 @@ template <> struct Elem<float> {
   static constexpr int kPerWord = 1;
   static __device__ __forceinline__ void unpack(uint32_t w, float *f) { f[0] = __uint_as_float(w); }
   static __device__ __forceinline__ uint32_t pack(const float *f) { return __float_as_uint(f[0]); }
+  // c + sum over the word's elements of a[e] * b[e]
+  static __device__ __forceinline__ float dot(uint32_t a, uint32_t b, float c) {
+    return fmaf(__uint_as_float(a), __uint_as_float(b), c);
+  }
 };
 template <> struct Elem<__bf16> {
   static constexpr int kPerWord = 2;
@@ -104,6 +107,11 @@ template <> struct Elem<__bf16> {
     h.x = (__bf16)f[0];   // round to nearest even (v_cvt_pk_bf16_f32)
     h.y = (__bf16)f[1];
     return __builtin_bit_cast(uint32_t, h);
+  }
+  // v_dot2_f32_bf16: both bf16 products are exact in fp32, accumulated into c in fp32
+  static __device__ __forceinline__ float dot(uint32_t a, uint32_t b, float c) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a), __builtin_bit_cast(bf2, b), c, false);
   }
 };
 template <> struct Elem<_Float16> {
@@ -119,6 +127,10 @@ template <> struct Elem<_Float16> {
     h.x = (_Float16)f[0];
     h.y = (_Float16)f[1];
     return __builtin_bit_cast(uint32_t, h);
+  }
+  // v_dot2_f32_f16: both f16 products are exact in fp32, accumulated into c in fp32
+  static __device__ __forceinline__ float dot(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), c, false);
   }
 };
 
@@ -168,6 +180,19 @@ __device__ __forceinline__ void load_elems(__amdgpu_buffer_rsrc_t r, uint32_t of
   bload<NB>(r, off, w);
 #pragma unroll
   for (int i = 0; i < NB / 4; ++i) Elem<T>::unpack(w[i], f + i * Elem<T>::kPerWord);
+}
+
+// Dot product of N elements of T at byte offset `off` with N elements of T held as raw words
+// `bw` (N*sizeof(T)/4 words), accumulated in fp32.
+template <typename T, int N>
+__device__ __forceinline__ float dot_elems(__amdgpu_buffer_rsrc_t r, uint32_t off, const uint32_t *bw) {
+  constexpr int NB = N * (int)sizeof(T);
+  uint32_t w[NB / 4];
+  bload<NB>(r, off, w);
+  float u = 0.f;
+#pragma unroll
+  for (int i = 0; i < NB / 4; ++i) u = Elem<T>::dot(w[i], bw[i], u);
+  return u;
 }
 
 // Store N fp32 values as T to a plain global pointer (aligned to N*sizeof(T) or 16 bytes).
@@ -316,17 +341,18 @@ struct Sample {
 // axis, or NaN): such a sample contributes nothing, as with zero padding.
 __device__ __forceinline__ bool sample_setup(float lx, float ly, float lz, int Wl, int Hl, int Dl,
                                              int GD, Sample &sm) {
+  // Always fills sm: a sample outside [-1, size) gets zero weights and out-of-range offsets
+  // (its loads return zero), so callers may run the corner loop without a branch.
   const float x = pixel_coord(lx, (float)Wl);
   const float y = pixel_coord(ly, (float)Hl);
   const float z = pixel_coord(lz, (float)Dl);
-  if (!(x >= -1.f && y >= -1.f && z >= -1.f && x < (float)Wl && y < (float)Hl && z < (float)Dl))
-    return false;
-  const float x0f = floorf(x), y0f = floorf(y), z0f = floorf(z);
+  const bool in = x >= -1.f && y >= -1.f && z >= -1.f && x < (float)Wl && y < (float)Hl && z < (float)Dl;
+  const float x0f = in ? floorf(x) : 0.f, y0f = in ? floorf(y) : 0.f, z0f = in ? floorf(z) : 0.f;
   const int x0 = (int)x0f, y0 = (int)y0f, z0 = (int)z0f;
   sm.x0 = x0; sm.y0 = y0; sm.z0 = z0;
-  sm.wx[1] = x - x0f; sm.wx[0] = (x0f + 1.f) - x;
-  sm.wy[1] = y - y0f; sm.wy[0] = (y0f + 1.f) - y;
-  sm.wz[1] = z - z0f; sm.wz[0] = (z0f + 1.f) - z;
+  sm.wx[1] = in ? x - x0f : 0.f; sm.wx[0] = in ? (x0f + 1.f) - x : 0.f;
+  sm.wy[1] = in ? y - y0f : 0.f; sm.wy[0] = in ? (y0f + 1.f) - y : 0.f;
+  sm.wz[1] = in ? z - z0f : 0.f; sm.wz[0] = in ? (z0f + 1.f) - z : 0.f;
   const bool vx0 = x0 >= 0, vx1 = x0 + 1 < Wl;
   const bool vy0 = y0 >= 0, vy1 = y0 + 1 < Hl;
   const bool vz0 = z0 >= 0, vz1 = z0 + 1 < Dl;
@@ -337,10 +363,10 @@ __device__ __forceinline__ bool sample_setup(float lx, float ly, float lz, int W
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
     const int dz = c >> 2, dy = (c >> 1) & 1, dx = c & 1;
-    const bool ok = vz[dz] && vy[dy] && vx[dx];
+    const bool ok = in && vz[dz] && vy[dy] && vx[dx];
     sm.off[c] = ok ? oz[dz] + oy[dy] + ox[dx] : OOB_ELEM;
   }
-  return true;
+  return in;
 }
 
 // LDS floats per unit of the backward query kernel (record, grad_attn, 16-byte-aligned stash

@@ -25,11 +25,36 @@
 #ifndef OPS3D_FDA_VALUE_BALANCED
 #define OPS3D_FDA_VALUE_BALANCED 1
 #endif
+#ifndef OPS3D_FDA_FWD_BATCH
+#define OPS3D_FDA_FWD_BATCH 1
+#endif
 #ifndef OPS3D_FDA_VALUE_UNROLL
 #define OPS3D_FDA_VALUE_UNROLL 2
 #endif
 
 namespace ops3d_fda {
+
+// NW raw words from a plain global pointer (aligned to 16 bytes when NW % 4 == 0).
+template <int NW>
+__device__ __forceinline__ void load_global_words(const void *p, uint32_t *w) {
+  const uint32_t *q = static_cast<const uint32_t *>(p);
+  if constexpr (NW % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < NW / 4; ++i) {
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(q + 4 * i);
+      w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+    }
+  } else if constexpr (NW % 2 == 0) {
+#pragma unroll
+    for (int i = 0; i < NW / 2; ++i) {
+      const u32x2 v = *reinterpret_cast<const u32x2 *>(q + 2 * i);
+      w[2 * i] = v.x; w[2 * i + 1] = v.y;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NW; ++i) w[i] = q[i];
+  }
+}
 
 template <typename T, int N>
 __device__ __forceinline__ void load_global_elems(const T *p, float *f) {
@@ -93,28 +118,55 @@ __global__ __launch_bounds__(kBlock) void fda_forward_kernel(const Args a) {
     const int64_t st = a.lsi[l];
     const uint32_t nbytes = (uint32_t)((int64_t)Dl * Hl * Wl * RST * (int64_t)sizeof(T));
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb + st * RST, nbytes);
-#pragma unroll 2
-    for (int k = 0; k < K; ++k, ++s) {
-      const float lx = rec[3 * s], ly = rec[3 * s + 1], lz = rec[3 * s + 2];
-      const float at = rec[3 * LK + s];
-      Sample sm;
-      if (live && sample_setup(lx, ly, lz, Wl, Hl, Dl, RST, sm)) {
-        float v[8][CPL];
+    // FB samples per step: their 8*FB corner loads are issued before any is consumed
+    constexpr int FB = OPS3D_FDA_FWD_BATCH;
+    for (int k = 0; k < K; k += FB, s += FB) {
+      const int nk = K - k < FB ? K - k : FB;
+      float at[FB];
+      Sample sm[FB];
+#pragma unroll
+      for (int u = 0; u < FB; ++u) {
+        const int su = u < nk ? s + u : s;
+        // branch-free: a sample outside the volume (or of a dead unit) loads zeros, weighs zero
+        sample_setup(rec[3 * su], rec[3 * su + 1], rec[3 * su + 2], Wl, Hl, Dl, RST, sm[u]);
+        at[u] = u < nk ? rec[3 * LK + su] : 0.f;
+        if (!live || u >= nk) {
+#pragma unroll
+          for (int c = 0; c < 8; ++c) sm[u].off[c] = OOB_ELEM;
+        }
+      }
+      // raw words: widened to fp32 only where they are consumed (keeps the two samples'
+      // loads within the register budget)
+      constexpr int NW = CPL * (int)sizeof(T) / 4, EPW = Elem<T>::kPerWord;
+      uint32_t v[FB][8][NW];
+#pragma unroll
+      for (int u = 0; u < FB; ++u)
 #pragma unroll
         for (int c = 0; c < 8; ++c)
-          load_elems<T, CPL>(rv, (sm.off[c] + lane_elem) * (uint32_t)sizeof(T), v[c]);
+          bload<NW * 4>(rv, (sm[u].off[c] + lane_elem) * (uint32_t)sizeof(T), v[u][c]);
+#pragma unroll
+      for (int u = 0; u < FB; ++u) {
         float w[8];
 #pragma unroll
-        for (int c = 0; c < 8; ++c) w[c] = (sm.wx[c & 1] * sm.wy[(c >> 1) & 1]) * sm.wz[c >> 2];
+        for (int c = 0; c < 8; ++c) w[c] = (sm[u].wx[c & 1] * sm[u].wy[(c >> 1) & 1]) * sm[u].wz[c >> 2];
 #pragma unroll
-        for (int ch = 0; ch < CPL; ++ch) {
-          float t = v[0][ch] * w[0];
+        for (int i = 0; i < NW; ++i) {
+          float t[EPW], f[EPW];
+          Elem<T>::unpack(v[u][0][i], f);
 #pragma unroll
-          for (int c = 1; c < 8; ++c) t = fmaf(v[c][ch], w[c], t);
-          acc[ch] = fmaf(at, t, acc[ch]);
+          for (int e = 0; e < EPW; ++e) t[e] = f[e] * w[0];
+#pragma unroll
+          for (int c = 1; c < 8; ++c) {
+            Elem<T>::unpack(v[u][c][i], f);
+#pragma unroll
+            for (int e = 0; e < EPW; ++e) t[e] = fmaf(f[e], w[c], t[e]);
+          }
+#pragma unroll
+          for (int e = 0; e < EPW; ++e) acc[i * EPW + e] = fmaf(at[u], t[e], acc[i * EPW + e]);
         }
       }
     }
+    s += K - (K + FB - 1) / FB * FB;   // the steps above advanced s by K rounded up to FB
   }
   if (live) store_elems<T, CPL>(static_cast<T *>(a.out) + unit * a.D + j * CPL, acc);
 }
@@ -148,13 +200,15 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
   unit_softmax<LPU>(rec + 3 * LK, LK, j);
   wave_lds_sync();
 
-  float tg[CPL];
+  // the unit's grad_output channels as raw words (dot products run on the packed elements)
+  constexpr int NW = CPL * (int)sizeof(T) / 4;
+  uint32_t tgw[NW];
   if (live) {
     const int64_t grow = a.ghm ? ((int64_t)b * a.G + g) * a.Q + q : unit;
-    load_global_elems<T, CPL>(static_cast<const T *>(a.grad_out) + grow * a.D + j * CPL, tg);
+    load_global_words<NW>(static_cast<const T *>(a.grad_out) + grow * a.D + j * CPL, tgw);
   } else {
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) tg[c] = 0.f;
+    for (int c = 0; c < NW; ++c) tgw[c] = 0u;
   }
 
   uint32_t bins_bg = 0;
@@ -171,60 +225,71 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
     const int64_t st = a.lsi[l];
     const int64_t nel = (int64_t)Dl * Hl * Wl * RST;
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb + st * RST, (uint32_t)(nel * (int64_t)sizeof(T)));
-    for (int k = 0; k < K; ++k, ++s) {
-      const float lx = rec[3 * s], ly = rec[3 * s + 1], lz = rec[3 * s + 2];
-      const float at = rec[3 * LK + s];
-      float gx = 0.f, gy = 0.f, gz = 0.f, ga = 0.f;
-      Sample sm;
-      const bool in = live && sample_setup(lx, ly, lz, Wl, Hl, Dl, RST, sm);
-      if (in) {
-        float U[8];
+    // two samples per step: both records are read before either gradient is written back, so
+    // the 16 corner loads of the pair are in flight together
+    for (int k = 0; k < K; k += 2, s += 2) {
+      const int nk = k + 1 < K ? 2 : 1;
+      float at[2];
+      bool in[2];
+      Sample sm[2];
+      float U[2][8];
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          float v[CPL];
-          load_elems<T, CPL>(rv, (sm.off[c] + lane_elem) * (uint32_t)sizeof(T), v);
-          float u = v[0] * tg[0];
+      for (int u = 0; u < 2; ++u) {
+        const int su = u < nk ? s + u : s;
+        const float lx = rec[3 * su], ly = rec[3 * su + 1], lz = rec[3 * su + 2];
+        at[u] = rec[3 * LK + su];
+        // branch-free: a sample outside the volume (or of a dead unit) loads zeros, weighs zero
+        in[u] = sample_setup(lx, ly, lz, Wl, Hl, Dl, RST, sm[u]) && live && u < nk;
+        if (!live || u >= nk) {
 #pragma unroll
-          for (int ch = 1; ch < CPL; ++ch) u = fmaf(v[ch], tg[ch], u);
-          U[c] = u;
+          for (int c = 0; c < 8; ++c) sm[u].off[c] = OOB_ELEM;
         }
-        float w[8];
+      }
 #pragma unroll
-        for (int c = 0; c < 8; ++c) w[c] = (sm.wx[c & 1] * sm.wy[(c >> 1) & 1]) * sm.wz[c >> 2];
+      for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int c = 0; c < 8; ++c) ga = fmaf(w[c], U[c], ga);
+        for (int c = 0; c < 8; ++c)
+          U[u][c] = dot_elems<T, CPL>(rv, (sm[u].off[c] + lane_elem) * (uint32_t)sizeof(T), tgw);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const Sample &m = sm[u];
+        float gx = 0.f, gy = 0.f, gz = 0.f, ga = 0.f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) ga = fmaf((m.wx[c & 1] * m.wy[(c >> 1) & 1]) * m.wz[c >> 2], U[u][c], ga);
         // d w_c / dx = (dx ? +1 : -1) * wy * wz, and likewise for y, z
 #pragma unroll
         for (int zy = 0; zy < 4; ++zy) {
           const int dz = zy >> 1, dy = zy & 1;
-          gx = fmaf(sm.wy[dy] * sm.wz[dz], U[4 * dz + 2 * dy + 1] - U[4 * dz + 2 * dy], gx);
+          gx = fmaf(m.wy[dy] * m.wz[dz], U[u][4 * dz + 2 * dy + 1] - U[u][4 * dz + 2 * dy], gx);
         }
 #pragma unroll
         for (int zx = 0; zx < 4; ++zx) {
           const int dz = zx >> 1, dx = zx & 1;
-          gy = fmaf(sm.wx[dx] * sm.wz[dz], U[4 * dz + 2 + dx] - U[4 * dz + dx], gy);
+          gy = fmaf(m.wx[dx] * m.wz[dz], U[u][4 * dz + 2 + dx] - U[u][4 * dz + dx], gy);
         }
 #pragma unroll
         for (int yx = 0; yx < 4; ++yx) {
           const int dy = yx >> 1, dx = yx & 1;
-          gz = fmaf(sm.wx[dx] * sm.wy[dy], U[4 + 2 * dy + dx] - U[2 * dy + dx], gz);
+          gz = fmaf(m.wx[dx] * m.wy[dy], U[u][4 + 2 * dy + dx] - U[u][2 * dy + dx], gz);
+        }
+        gx = unit_sum<LPU>(gx);
+        gy = unit_sum<LPU>(gy);
+        gz = unit_sum<LPU>(gz);
+        ga = unit_sum<LPU>(ga);
+        if (j == 0 && u < nk) {
+          const int su = s + u;
+          // d(pixel)/d(loc) = size (grid_sample: size/2 per unit of grid, grid = 2*loc - 1)
+          rec[3 * su] = gx * at[u] * (float)Wl;
+          rec[3 * su + 1] = gy * at[u] * (float)Hl;
+          rec[3 * su + 2] = gz * at[u] * (float)Dl;
+          gat_s[su] = ga;
+          key_s[su] = in[u] ? bin_base + (uint32_t)(((m.z0 + 1) * (Hl + 1) + (m.y0 + 1)) * (Wl + 1) + (m.x0 + 1))
+                            : a.key_invalid;
+          st_s[su] = make_float4(m.wx[1], m.wy[1], m.wz[1], at[u]);
         }
       }
-      gx = unit_sum<LPU>(gx);
-      gy = unit_sum<LPU>(gy);
-      gz = unit_sum<LPU>(gz);
-      ga = unit_sum<LPU>(ga);
-      if (j == 0) {
-        // d(pixel)/d(loc) = size (grid_sample: size/2 per unit of grid, grid = 2*loc - 1)
-        rec[3 * s] = gx * at * (float)Wl;
-        rec[3 * s + 1] = gy * at * (float)Hl;
-        rec[3 * s + 2] = gz * at * (float)Dl;
-        gat_s[s] = ga;
-        key_s[s] = in ? bin_base + (uint32_t)(((sm.z0 + 1) * (Hl + 1) + (sm.y0 + 1)) * (Wl + 1) + (sm.x0 + 1))
-                      : a.key_invalid;
-        st_s[s] = make_float4(sm.wx[1], sm.wy[1], sm.wz[1], at);
-      }
     }
+    s += K - ((K + 1) & ~1);   // the steps above advanced s by K rounded up to even
     bin_base += level_bins(a.shapes, l);
   }
   wave_lds_sync();
@@ -336,50 +401,38 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_value_kernel(const Args a) {
       x0 = (r2 - y * Wp) * 2;
       // Samples with a corner on x0 or x0+1 in row (z, y): for each (dz, dy), the contiguous
       // bins of base x0-1, x0, x0+1 (shifted by +1: x0, x0+1, x0+2).  Base x0-1 feeds x0 (dx=1),
-      // base x0 feeds x0 (dx=0) and x0+1 (dx=1), base x0+1 feeds x0+1 (dx=0).  The 4 ranges are
-      // concatenated and dealt round-robin to the pair's NBP lane groups (equal work whatever
-      // the bin sizes); each grad_out row is loaded and widened once for both voxels.
+      // base x0 feeds x0 (dx=0) and x0+1 (dx=1), base x0+1 feeds x0+1 (dx=0); each grad_out
+      // row is loaded and widened once for both voxels.
       const uint32_t bin_p = bin_lb + (z + 1) * HW1 + (y + 1) * W1 + x0;   // shifted base x0-1
       const bool two = x0 + 1 < (uint32_t)Wl;
-      uint32_t st_r[4], m1_r[4], m2_r[4], cum[4];
-      uint32_t n = 0;
+      // One range per (dz, dy) (compile-time r, so wy / wz are fixed selections); the range's
+      // entries are dealt round-robin to the pair's NBP lane groups.
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const uint32_t rb = bin_p - (uint32_t)(r >> 1) * HW1 - (uint32_t)(r & 1) * W1;   // (dz, dy) = (r>>1, r&1)
         // a pair with one voxel (x0 = W-1) has no bin of base x0+1: bin_start[rb + 3] is past
         // its row (at the end of the array: never written), so its range ends at s2
-        const uint32_t s0 = a.bin_start[rb], s1 = a.bin_start[rb + 1], s2 = a.bin_start[rb + 2];
-        const uint32_t s3 = two ? a.bin_start[rb + 3] : s2;
-        st_r[r] = s0;
-        m1_r[r] = s1;
-        m2_r[r] = s2;
-        n += s3 - s0;
-        cum[r] = n;
-      }
+        const uint32_t s0 = a.bin_start[rb], m1 = a.bin_start[rb + 1], m2 = a.bin_start[rb + 2];
+        const uint32_t s3 = two ? a.bin_start[rb + 3] : m2;
 #pragma unroll OPS3D_FDA_VALUE_UNROLL
-      for (uint32_t t = (uint32_t)dp; t < n; t += NBP) {
-        const int r = (t >= cum[0]) + (t >= cum[1]) + (t >= cum[2]);
-        const uint32_t base = r == 0 ? 0u : (r == 1 ? cum[0] : (r == 2 ? cum[1] : cum[2]));
-        const uint32_t s0 = r == 0 ? st_r[0] : (r == 1 ? st_r[1] : (r == 2 ? st_r[2] : st_r[3]));
-        const uint32_t m1 = r == 0 ? m1_r[0] : (r == 1 ? m1_r[1] : (r == 2 ? m1_r[2] : m1_r[3]));
-        const uint32_t m2 = r == 0 ? m2_r[0] : (r == 1 ? m2_r[1] : (r == 2 ? m2_r[2] : m2_r[3]));
-        const uint32_t i = s0 + (t - base);
-        const float4 st = a.sorted_stash[i];
-        const uint32_t row = a.sorted_row[i];
-        float tg[CPL];
-        load_global_elems<T, CPL>(go + (size_t)(row * (uint32_t)D) + j * CPL, tg);
-        const float wy = (r & 1) ? st.y : 1.f - st.y;
-        const float wz = (r >> 1) ? st.z : 1.f - st.z;
-        const float ayz = st.w;
-        // base x0-1: (x0, dx=1); base x0: (x0, dx=0), (x0+1, dx=1); base x0+1: (x0+1, dx=0)
-        const float wx0 = i < m1 ? st.x : (i < m2 ? 1.f - st.x : 0.f);
-        const float wx1 = i < m1 ? 0.f : (i < m2 ? st.x : 1.f - st.x);
-        const float aw0 = ayz * ((wx0 * wy) * wz);
-        const float aw1 = ayz * ((wx1 * wy) * wz);
+        for (uint32_t i = s0 + (uint32_t)dp; i < s3; i += NBP) {
+          const float4 st = a.sorted_stash[i];
+          const uint32_t row = a.sorted_row[i];
+          float tg[CPL];
+          load_global_elems<T, CPL>(go + (size_t)(row * (uint32_t)D) + j * CPL, tg);
+          const float wy = (r & 1) ? st.y : 1.f - st.y;
+          const float wz = (r >> 1) ? st.z : 1.f - st.z;
+          const float ayz = st.w * (wy * wz);
+          // base x0-1: (x0, dx=1); base x0: (x0, dx=0), (x0+1, dx=1); base x0+1: (x0+1, dx=0)
+          const bool lft = i < m1, ctr = i < m2;
+          const float fx = st.x, gx = 1.f - st.x;
+          const float aw0 = ayz * (lft ? fx : (ctr ? gx : 0.f));
+          const float aw1 = ayz * (lft ? 0.f : (ctr ? fx : gx));
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-          acc0[c] = fmaf(aw0, tg[c], acc0[c]);
-          acc1[c] = fmaf(aw1, tg[c], acc1[c]);
+          for (int c = 0; c < CPL; ++c) {
+            acc0[c] = fmaf(aw0, tg[c], acc0[c]);
+            acc1[c] = fmaf(aw1, tg[c], acc1[c]);
+          }
         }
       }
     }

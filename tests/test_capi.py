@@ -103,7 +103,7 @@ def test_backward_workspace_check(lib):
     if _has_device():
         assert rc == 1 and b"workspace too small" in lib.ops3d_fda_last_error()
     else:
-        assert rc == 2 and b"radix sort" in lib.ops3d_fda_last_error()
+        assert rc == 2 and b"bin sort" in lib.ops3d_fda_last_error()
     # argument errors are still reported before anything else
     rc = lib.ops3d_fda_backward(p, p, p, p, p, p, p, None, 0, 2, 1, 576, 8, 32, 6, 576, 4, 64, None)
     assert rc == 1 and b"invalid number of scales" in lib.ops3d_fda_last_error()
