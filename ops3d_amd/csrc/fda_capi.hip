@@ -123,7 +123,8 @@ int common_checks(int dtype, int B, int S, int G, int D, int L, int Q, int K, in
     return fail(OPS3D_FDA_EINVAL, "value too large: S*G*D = %lld exceeds %lld elements per batch item",
                 (long long)S * G * D, (long long)kMaxLevelElems);
   const int LK = L * K, P = 4 * LK;
-  const int UPB = kWavesPerBlock * (kWave / geo.lpu);
+  const int ulanes = (!backward && fwd_pairs(geo.cpl, geo.lpu, elem_size(dtype))) ? 2 * geo.lpu : geo.lpu;
+  const int UPB = kWavesPerBlock * (kWave / ulanes);
   const size_t lds = (size_t)UPB * (size_t)(backward ? bwd_query_lds_floats(P, LK) : P + 1) * sizeof(float);
   if (lds > 160 * 1024)   // gfx950: 160 KB of LDS per workgroup
     return fail(OPS3D_FDA_EINVAL, "L*K=%d too large for D=%d (needs %zu bytes of LDS per block)", LK, D, lds);

@@ -337,22 +337,56 @@ struct Sample {
   int x0, y0, z0;    // base corner (may be -1)
 };
 
-// Returns false when every corner lies outside the volume (coordinate outside [-1, size) on some
-// axis, or NaN): such a sample contributes nothing, as with zero padding.
-__device__ __forceinline__ bool sample_setup(float lx, float ly, float lz, int Wl, int Hl, int Dl,
-                                             int GD, Sample &sm) {
-  // Always fills sm: a sample outside [-1, size) gets zero weights and out-of-range offsets
-  // (its loads return zero), so callers may run the corner loop without a branch.
+// Whether the forward runs the x-pair kernel: 4 lanes x 16 bytes per 64-byte row, 8 lanes per
+// query (host and device must agree: it sets the units per block).
+__host__ __device__ constexpr bool fwd_pairs(int cpl, int lpu, int esize) {
+  return lpu == 4 && cpl * esize == 16;
+}
+
+// Compile-time loop: f(IntConst<0>{}), ..., f(IntConst<N-1>{}).
+template <int V> struct IntConst { static constexpr int value = V; };
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  if constexpr (N > 0) {
+    static_for<N - 1>(f);
+    f(IntConst<N - 1>{});
+  }
+}
+
+// Compact per-sample set-up: base corner and the two linear weights per axis.  One lane of a
+// unit computes it and broadcasts it to the unit's other lanes (unit_bcast); each lane then
+// expands it into the 8 corner offsets and weights (sample_expand).
+struct SampleBase {
+  int x0, y0, z0;                 // base corner (-1 allowed); -2 on every axis when outside
+  float wx0, wx1, wy0, wy1, wz0, wz1;
+};
+
+// A coordinate outside [-1, size) on some axis (or NaN) leaves every corner outside the volume:
+// such a sample gets base corner (-2, -2, -2), so all its loads are out of range and read zero,
+// and zero weights, so it contributes nothing -- as with zero padding.  Returns whether the
+// sample is inside.
+__device__ __forceinline__ bool sample_base(float lx, float ly, float lz, int Wl, int Hl, int Dl,
+                                            SampleBase &sb) {
   const float x = pixel_coord(lx, (float)Wl);
   const float y = pixel_coord(ly, (float)Hl);
   const float z = pixel_coord(lz, (float)Dl);
   const bool in = x >= -1.f && y >= -1.f && z >= -1.f && x < (float)Wl && y < (float)Hl && z < (float)Dl;
-  const float x0f = in ? floorf(x) : 0.f, y0f = in ? floorf(y) : 0.f, z0f = in ? floorf(z) : 0.f;
-  const int x0 = (int)x0f, y0 = (int)y0f, z0 = (int)z0f;
+  const float x0f = floorf(x), y0f = floorf(y), z0f = floorf(z);
+  sb.x0 = in ? (int)x0f : -2; sb.y0 = in ? (int)y0f : -2; sb.z0 = in ? (int)z0f : -2;
+  sb.wx1 = in ? x - x0f : 0.f; sb.wx0 = in ? (x0f + 1.f) - x : 0.f;
+  sb.wy1 = in ? y - y0f : 0.f; sb.wy0 = in ? (y0f + 1.f) - y : 0.f;
+  sb.wz1 = in ? z - z0f : 0.f; sb.wz0 = in ? (z0f + 1.f) - z : 0.f;
+  return in;
+}
+
+// Corner offsets (element offsets voxel*GD inside the level, OOB_ELEM for a corner outside the
+// volume) and weights of a sample.
+__device__ __forceinline__ void sample_expand(const SampleBase &sb, int Wl, int Hl, int Dl, int GD, Sample &sm) {
+  const int x0 = sb.x0, y0 = sb.y0, z0 = sb.z0;
   sm.x0 = x0; sm.y0 = y0; sm.z0 = z0;
-  sm.wx[1] = in ? x - x0f : 0.f; sm.wx[0] = in ? (x0f + 1.f) - x : 0.f;
-  sm.wy[1] = in ? y - y0f : 0.f; sm.wy[0] = in ? (y0f + 1.f) - y : 0.f;
-  sm.wz[1] = in ? z - z0f : 0.f; sm.wz[0] = in ? (z0f + 1.f) - z : 0.f;
+  sm.wx[0] = sb.wx0; sm.wx[1] = sb.wx1;
+  sm.wy[0] = sb.wy0; sm.wy[1] = sb.wy1;
+  sm.wz[0] = sb.wz0; sm.wz[1] = sb.wz1;
   const bool vx0 = x0 >= 0, vx1 = x0 + 1 < Wl;
   const bool vy0 = y0 >= 0, vy1 = y0 + 1 < Hl;
   const bool vz0 = z0 >= 0, vz1 = z0 + 1 < Dl;
@@ -363,10 +397,74 @@ __device__ __forceinline__ bool sample_setup(float lx, float ly, float lz, int W
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
     const int dz = c >> 2, dy = (c >> 1) & 1, dx = c & 1;
-    const bool ok = in && vz[dz] && vy[dy] && vx[dx];
+    const bool ok = vz[dz] && vy[dy] && vx[dx];
     sm.off[c] = ok ? oz[dz] + oy[dy] + ox[dx] : OOB_ELEM;
   }
+}
+
+// Both steps in one lane.  Always fills sm; returns whether the sample is inside the volume.
+__device__ __forceinline__ bool sample_setup(float lx, float ly, float lz, int Wl, int Hl, int Dl,
+                                             int GD, Sample &sm) {
+  SampleBase sb;
+  const bool in = sample_base(lx, ly, lz, Wl, Hl, Dl, sb);
+  sample_expand(sb, Wl, Hl, Dl, GD, sm);
   return in;
+}
+
+// Value of lane u of this lane's unit (units are LPU consecutive lanes; u < min(LPU, 4)).
+template <int LPU, int U>
+__device__ __forceinline__ uint32_t unit_bcast(uint32_t v) {
+  if constexpr (LPU == 1) {
+    return v;
+  } else if constexpr (LPU == 2) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, U | (U << 2) | ((2 + U) << 4) | ((2 + U) << 6), 0xF, 0xF,
+                                              false);
+  } else if constexpr (LPU == 4) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, U * 0x55, 0xF, 0xF, false);
+  } else {
+    const int lane = (int)(threadIdx.x & (kWave - 1));
+    return (uint32_t)__shfl((int)v, (lane & ~(LPU - 1)) | U, kWave);
+  }
+}
+
+// The 8 corner offsets and 8 corner weights of lane U's sample.
+struct SampleCorners {
+  uint32_t off[8];
+  float w[8];
+};
+
+__device__ __forceinline__ void sample_corners(const Sample &sm, SampleCorners &sc) {
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    sc.off[c] = sm.off[c];
+    sc.w[c] = (sm.wx[c & 1] * sm.wy[(c >> 1) & 1]) * sm.wz[c >> 2];
+  }
+}
+
+template <int LPU, int U>
+__device__ __forceinline__ SampleCorners unit_bcast(const SampleCorners &sc) {
+  SampleCorners r;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    r.off[c] = unit_bcast<LPU, U>(sc.off[c]);
+    r.w[c] = __uint_as_float(unit_bcast<LPU, U>(__float_as_uint(sc.w[c])));
+  }
+  return r;
+}
+
+template <int LPU, int U>
+__device__ __forceinline__ SampleBase unit_bcast(const SampleBase &sb) {
+  SampleBase r;
+  r.x0 = (int)unit_bcast<LPU, U>((uint32_t)sb.x0);
+  r.y0 = (int)unit_bcast<LPU, U>((uint32_t)sb.y0);
+  r.z0 = (int)unit_bcast<LPU, U>((uint32_t)sb.z0);
+  r.wx0 = __uint_as_float(unit_bcast<LPU, U>(__float_as_uint(sb.wx0)));
+  r.wx1 = __uint_as_float(unit_bcast<LPU, U>(__float_as_uint(sb.wx1)));
+  r.wy0 = __uint_as_float(unit_bcast<LPU, U>(__float_as_uint(sb.wy0)));
+  r.wy1 = __uint_as_float(unit_bcast<LPU, U>(__float_as_uint(sb.wy1)));
+  r.wz0 = __uint_as_float(unit_bcast<LPU, U>(__float_as_uint(sb.wz0)));
+  r.wz1 = __uint_as_float(unit_bcast<LPU, U>(__float_as_uint(sb.wz1)));
+  return r;
 }
 
 // LDS floats per unit of the backward query kernel (record, grad_attn, 16-byte-aligned stash

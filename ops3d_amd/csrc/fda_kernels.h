@@ -25,9 +25,6 @@
 #ifndef OPS3D_FDA_VALUE_BALANCED
 #define OPS3D_FDA_VALUE_BALANCED 1
 #endif
-#ifndef OPS3D_FDA_FWD_BATCH
-#define OPS3D_FDA_FWD_BATCH 1
-#endif
 #ifndef OPS3D_FDA_VALUE_UNROLL
 #define OPS3D_FDA_VALUE_UNROLL 2
 #endif
@@ -112,61 +109,56 @@ __global__ __launch_bounds__(kBlock) void fda_forward_kernel(const Args a) {
   const uint32_t lane_elem = (uint32_t)((a.vhm ? 0 : g * a.D) + j * CPL);
   const T *vb = static_cast<const T *>(a.value) +
                 (a.vhm ? ((int64_t)b * a.G + g) * a.S * a.D : (int64_t)b * a.S * a.G * a.D);
-  int s = 0;
   for (int l = 0; l < L; ++l) {
     const int Dl = (int)a.shapes[3 * l], Hl = (int)a.shapes[3 * l + 1], Wl = (int)a.shapes[3 * l + 2];
     const int64_t st = a.lsi[l];
     const uint32_t nbytes = (uint32_t)((int64_t)Dl * Hl * Wl * RST * (int64_t)sizeof(T));
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb + st * RST, nbytes);
-    // FB samples per step: their 8*FB corner loads are issued before any is consumed
-    constexpr int FB = OPS3D_FDA_FWD_BATCH;
-    for (int k = 0; k < K; k += FB, s += FB) {
-      const int nk = K - k < FB ? K - k : FB;
-      float at[FB];
-      Sample sm[FB];
+    // NG samples per step: lane j < NG of each unit sets up sample k0 + j, then the unit
+    // processes them one after the other from broadcast set-ups
+    constexpr int NG = LPU < 4 ? LPU : 4;
+    for (int k0 = 0; k0 < K; k0 += NG) {
+      const int kj = k0 + (j < NG ? j : 0);
+      const int sj = l * K + (kj < K ? kj : K - 1);
+      Sample ms;
+      sample_setup(rec[3 * sj], rec[3 * sj + 1], rec[3 * sj + 2], Wl, Hl, Dl, RST, ms);
+      if (!live) {   // a dead unit loads zeros
 #pragma unroll
-      for (int u = 0; u < FB; ++u) {
-        const int su = u < nk ? s + u : s;
-        // branch-free: a sample outside the volume (or of a dead unit) loads zeros, weighs zero
-        sample_setup(rec[3 * su], rec[3 * su + 1], rec[3 * su + 2], Wl, Hl, Dl, RST, sm[u]);
-        at[u] = u < nk ? rec[3 * LK + su] : 0.f;
-        if (!live || u >= nk) {
-#pragma unroll
-          for (int c = 0; c < 8; ++c) sm[u].off[c] = OOB_ELEM;
-        }
+        for (int c = 0; c < 8; ++c) ms.off[c] = OOB_ELEM;
       }
-      // raw words: widened to fp32 only where they are consumed (keeps the two samples'
-      // loads within the register budget)
-      constexpr int NW = CPL * (int)sizeof(T) / 4, EPW = Elem<T>::kPerWord;
-      uint32_t v[FB][8][NW];
+      SampleCorners mine;
+      sample_corners(ms, mine);
+      const uint32_t at_mine = __float_as_uint(rec[3 * LK + sj]);
+      static_for<NG>([&](auto uc) {
+        constexpr int u = decltype(uc)::value;
+        if (k0 + u < K) {
+          const SampleCorners sm = unit_bcast<LPU, u>(mine);
+          const float at = __uint_as_float(unit_bcast<LPU, u>(at_mine));
+          // raw words: widened to fp32 only where they are consumed
+          constexpr int NW = CPL * (int)sizeof(T) / 4, EPW = Elem<T>::kPerWord;
+          uint32_t v[8][NW];
 #pragma unroll
-      for (int u = 0; u < FB; ++u)
+          for (int c = 0; c < 8; ++c)
+            bload<NW * 4>(rv, (sm.off[c] + lane_elem) * (uint32_t)sizeof(T), v[c]);
+          const float *w = sm.w;
 #pragma unroll
-        for (int c = 0; c < 8; ++c)
-          bload<NW * 4>(rv, (sm[u].off[c] + lane_elem) * (uint32_t)sizeof(T), v[u][c]);
+          for (int i = 0; i < NW; ++i) {
+            float t[EPW], f[EPW];
+            Elem<T>::unpack(v[0][i], f);
 #pragma unroll
-      for (int u = 0; u < FB; ++u) {
-        float w[8];
+            for (int e = 0; e < EPW; ++e) t[e] = f[e] * w[0];
 #pragma unroll
-        for (int c = 0; c < 8; ++c) w[c] = (sm[u].wx[c & 1] * sm[u].wy[(c >> 1) & 1]) * sm[u].wz[c >> 2];
+            for (int c = 1; c < 8; ++c) {
+              Elem<T>::unpack(v[c][i], f);
 #pragma unroll
-        for (int i = 0; i < NW; ++i) {
-          float t[EPW], f[EPW];
-          Elem<T>::unpack(v[u][0][i], f);
+              for (int e = 0; e < EPW; ++e) t[e] = fmaf(f[e], w[c], t[e]);
+            }
 #pragma unroll
-          for (int e = 0; e < EPW; ++e) t[e] = f[e] * w[0];
-#pragma unroll
-          for (int c = 1; c < 8; ++c) {
-            Elem<T>::unpack(v[u][c][i], f);
-#pragma unroll
-            for (int e = 0; e < EPW; ++e) t[e] = fmaf(f[e], w[c], t[e]);
+            for (int e = 0; e < EPW; ++e) acc[i * EPW + e] = fmaf(at, t[e], acc[i * EPW + e]);
           }
-#pragma unroll
-          for (int e = 0; e < EPW; ++e) acc[i * EPW + e] = fmaf(at[u], t[e], acc[i * EPW + e]);
         }
-      }
+      });
     }
-    s += K - (K + FB - 1) / FB * FB;   // the steps above advanced s by K rounded up to FB
   }
   if (live) store_elems<T, CPL>(static_cast<T *>(a.out) + unit * a.D + j * CPL, acc);
 }
@@ -174,6 +166,104 @@ __global__ __launch_bounds__(kBlock) void fda_forward_kernel(const Args a) {
 // ---------------------------------------------------------------------------------------------
 // Backward phase 1, query-major: gradients of the locations and logits of one unit, plus one
 // (bin, sample, stash) record per sample for the value-gradient gather of phase 3.  No atomics.
+// Forward for rows of 64 bytes (4 lanes x 16 bytes): the two x-neighbour rows of a corner pair
+// are adjacent in memory, so a unit of 8 lanes fetches the pair as one 128-byte span (lanes 0-3
+// row x0, lanes 4-7 row x0+1) -- 4 loads per sample instead of 8 and half the cache lines of
+// two 64-byte loads when x0 is even.  Gathers of random rows cost per distinct 128-byte line,
+// not per byte, so this halves the gather work per sample.  Each half accumulates its own x-row
+// over all samples; the halves are summed once at the end.
+template <typename T, int CPL>
+__global__ __launch_bounds__(kBlock) void fda_forward_pair_kernel(const Args a) {
+  extern __shared__ float lds[];
+  constexpr int LPU = 4, UL = 2 * LPU;
+  constexpr int UPW = kWave / UL, UPB = kWavesPerBlock * UPW;
+  static_assert(CPL * sizeof(T) == 16, "pair kernel: 16 bytes per lane, 64-byte rows");
+  int b, g, qb;
+  if (!map_tile(a, blockIdx.x, b, g, qb)) return;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int ju = lane & (UL - 1);        // lane within the unit
+  const int j = ju & (LPU - 1);          // channel chunk of the row
+  const int dxl = ju / LPU;              // x-row of the pair this lane loads
+  const int ub = wave * UPW + lane / UL;
+  const int q = qb * UPB + ub;
+  const bool live = q < a.Q;
+  const int L = a.L, K = a.K, LK = L * K, P = a.P;
+  float *rec = lds + ub * (P + 1);
+  const int64_t unit = ((int64_t)b * a.Q + (live ? q : 0)) * a.G + g;
+
+  stage_record<T, UL>(static_cast<const T *>(a.loc_attn) + unit * P, P, ju, live, rec);
+  wave_lds_sync();
+  unit_softmax<UL>(rec + 3 * LK, LK, ju);
+  wave_lds_sync();
+
+  float acc[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) acc[c] = 0.f;
+
+  const int RST = a.vhm ? a.D : a.G * a.D;
+  const uint32_t lane_elem = (uint32_t)((a.vhm ? 0 : g * a.D) + j * CPL);
+  const T *vb = static_cast<const T *>(a.value) +
+                (a.vhm ? ((int64_t)b * a.G + g) * a.S * a.D : (int64_t)b * a.S * a.G * a.D);
+  constexpr int NW = CPL * (int)sizeof(T) / 4, EPW = Elem<T>::kPerWord;
+  for (int l = 0; l < L; ++l) {
+    const int Dl = (int)a.shapes[3 * l], Hl = (int)a.shapes[3 * l + 1], Wl = (int)a.shapes[3 * l + 2];
+    const int64_t st = a.lsi[l];
+    const uint32_t nbytes = (uint32_t)((int64_t)Dl * Hl * Wl * RST * (int64_t)sizeof(T));
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb + st * RST, nbytes);
+    // 4 samples per step: lane (ju & 3) of each quad sets up sample k0 + (ju & 3) for its own
+    // x-row (4 corner offsets and weights); its quad receives them by DPP broadcast
+    for (int k0 = 0; k0 < K; k0 += 4) {
+      const int kj = k0 + (ju & 3);
+      const int sj = l * K + (kj < K ? kj : K - 1);
+      Sample ms;
+      sample_setup(rec[3 * sj], rec[3 * sj + 1], rec[3 * sj + 2], Wl, Hl, Dl, RST, ms);
+      uint32_t off4[4];
+      float w4[4];
+#pragma unroll
+      for (int c4 = 0; c4 < 4; ++c4) {   // c4 = (dz, dy); this lane's corner c = 2*c4 + dxl
+        off4[c4] = live ? (dxl ? ms.off[2 * c4 + 1] : ms.off[2 * c4]) : OOB_ELEM;
+        w4[c4] = (ms.wx[dxl] * ms.wy[c4 & 1]) * ms.wz[c4 >> 1];
+      }
+      const uint32_t at_mine = __float_as_uint(rec[3 * LK + sj]);
+      static_for<4>([&](auto uc) {
+        constexpr int u = decltype(uc)::value;
+        if (k0 + u < K) {
+          uint32_t off[4];
+          float w[4];
+#pragma unroll
+          for (int c4 = 0; c4 < 4; ++c4) {
+            off[c4] = unit_bcast<4, u>(off4[c4]);
+            w[c4] = __uint_as_float(unit_bcast<4, u>(__float_as_uint(w4[c4])));
+          }
+          const float at = __uint_as_float(unit_bcast<4, u>(at_mine));
+          uint32_t v[4][NW];
+#pragma unroll
+          for (int c4 = 0; c4 < 4; ++c4)
+            bload<NW * 4>(rv, (off[c4] + lane_elem) * (uint32_t)sizeof(T), v[c4]);
+#pragma unroll
+          for (int i = 0; i < NW; ++i) {
+            float t[EPW], f[EPW];
+            Elem<T>::unpack(v[0][i], f);
+#pragma unroll
+            for (int e = 0; e < EPW; ++e) t[e] = f[e] * w[0];
+#pragma unroll
+            for (int c4 = 1; c4 < 4; ++c4) {
+              Elem<T>::unpack(v[c4][i], f);
+#pragma unroll
+              for (int e = 0; e < EPW; ++e) t[e] = fmaf(f[e], w[c4], t[e]);
+            }
+#pragma unroll
+            for (int e = 0; e < EPW; ++e) acc[i * EPW + e] = fmaf(at, t[e], acc[i * EPW + e]);
+          }
+        }
+      });
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) acc[c] += xor_lane<LPU>(acc[c]);
+  if (live && dxl == 0) store_elems<T, CPL>(static_cast<T *>(a.out) + unit * a.D + j * CPL, acc);
+}
+
 template <typename T, int CPL, int LPU>
 __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
   extern __shared__ float lds[];
@@ -466,8 +556,12 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_value_kernel(const Args a) {
 // which: 0 forward, 1 backward phase 1 (query-major), 2 backward phase 3 (voxel-major)
 template <typename T, int CPL, int LPU>
 hipError_t launch_one(int which, const Args &a, unsigned grid, size_t lds, hipStream_t st) {
-  if (which == 0)
-    hipLaunchKernelGGL((fda_forward_kernel<T, CPL, LPU>), dim3(grid), dim3(kBlock), lds, st, a);
+  if (which == 0) {
+    if constexpr (fwd_pairs(CPL, LPU, (int)sizeof(T)))
+      hipLaunchKernelGGL((fda_forward_pair_kernel<T, CPL>), dim3(grid), dim3(kBlock), lds, st, a);
+    else
+      hipLaunchKernelGGL((fda_forward_kernel<T, CPL, LPU>), dim3(grid), dim3(kBlock), lds, st, a);
+  }
   else if (which == 1)
     hipLaunchKernelGGL((fda_bwd_query_kernel<T, CPL, LPU>), dim3(grid), dim3(kBlock), lds, st, a);
   else
