@@ -229,8 +229,8 @@ def summary_line(r):
     if bk:
         ph = r["bwd_kernel"]
         parts.append(f"bwd {bk * 1e3:7.1f} us [copy {ph['head_major_copies']['mean'] * 1e3:.1f} "
-                     f"q {ph['query_kernel']['mean'] * 1e3:.1f} sort {ph['sort']['mean'] * 1e3:.1f} "
-                     f"bins {ph['bin_offsets']['mean'] * 1e3:.1f} v {ph['value_kernel']['mean'] * 1e3:.1f}]")
+                     f"q {ph['query_kernel']['mean'] * 1e3:.1f} count {ph['tile_count']['mean'] * 1e3:.1f} "
+                     f"scatter {ph['tile_scatter']['mean'] * 1e3:.1f} tile {ph['tile_kernel']['mean'] * 1e3:.1f}]")
     parts.append(f"{samples / (s or f) / 1e6:.3g} Gsamples/s" if (s or f) else "")
     return " | ".join(parts)
 
@@ -309,16 +309,16 @@ def main():
     # per-kernel algorithmic bytes (each API tensor the kernel must touch, once):
     #   forward: read value + sampling_loc_attn, write output
     #   backward query kernel: read value + sampling_loc_attn + grad_output, write grad_sampling_loc_attn
-    #   backward value kernel: read grad_output, write grad_value
+    #   backward tile kernel: read grad_output, write grad_value
     kern = {
         "fda_forward_kernel": (r["fwd_kernel"]["forward_kernel"]["mean"], V + R + O),
         "fda_bwd_query_kernel": (ph["query_kernel"]["mean"], V + 2 * R + O),
-        "fda_bwd_value_kernel": (ph["value_kernel"]["mean"], O + V),
-        "radix_sort": (ph["sort"]["mean"], None),
+        "fda_bwd_tile_kernel": (ph["tile_kernel"]["mean"], O + V),
+        "tile_bucketing": (ph["tile_count"]["mean"] + ph["tile_scatter"]["mean"], None),
     }
     dominant = max(kern, key=lambda k: kern[k][0])
     kms, kbytes = kern[dominant]
-    if kbytes is None:  # the sort moves only internal keys; report the backward as a whole
+    if kbytes is None:  # the bucketing moves only internal entries; report the backward as a whole
         dominant, kms, kbytes = "backward (all phases)", ph["total"]["mean"], by["bwd"]
     achieved = kbytes / (kms * 1e-3) / 1e9
     kf, kb = r["fwd_kernel"]["total"]["mean"], ph["total"]["mean"]
@@ -350,7 +350,8 @@ def main():
         "kernels_us": {**{k: round(v[0] * 1e3, 2) for k, v in kern.items()},
                        "head_major_copy_fwd": round(r["fwd_kernel"]["head_major_copy"]["mean"] * 1e3, 2),
                        "head_major_copies_bwd": round(ph["head_major_copies"]["mean"] * 1e3, 2),
-                       "bin_offsets": round(ph["bin_offsets"]["mean"] * 1e3, 2),
+                       "tile_count_scan": round(ph["tile_count"]["mean"] * 1e3, 2),
+                       "tile_scatter": round(ph["tile_scatter"]["mean"] * 1e3, 2),
                        "forward_total": round(kf * 1e3, 2), "backward_total": round(kb * 1e3, 2)},
         "roofline": {
             "kernel": dominant,

@@ -16,7 +16,7 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_NAME = "libops3d_fda.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["fda_capi.hip", "fda_binsort.hip", "fda_f32.hip", "fda_f16.hip", "fda_bf16.hip"]
+SOURCES = ["fda_capi.hip", "fda_tiles.hip", "fda_f32.hip", "fda_f16.hip", "fda_bf16.hip"]
 ARCH = "gfx950"
 
 # -packed-fp32-ops off: hipcc must not form v_pk_{add,mul,fma}_f32 on its own.
@@ -53,8 +53,9 @@ def _run(cmd: list[str]) -> None:
         sys.stderr.write(err + "\n")
 
 
-def build(out_path: str = LIB_PATH, build_dir: str | None = None) -> str:
-    """Compile every source for gfx950 and link ``libops3d_fda.so``; return its path."""
+def build(out_path: str = LIB_PATH, build_dir: str | None = None, extra_flags: list[str] | None = None) -> str:
+    """Compile every source for gfx950 and link ``libops3d_fda.so``; return its path.
+    ``extra_flags`` (e.g. ``-DOPS3D_FDA_TILE_WPE=8``) builds a tuning variant."""
     hipcc = _hipcc()
     build_dir = build_dir or os.path.join(PKG_DIR, "_build")
     os.makedirs(build_dir, exist_ok=True)
@@ -63,7 +64,7 @@ def build(out_path: str = LIB_PATH, build_dir: str | None = None) -> str:
     for src in SOURCES:
         obj = os.path.join(build_dir, src.replace(".hip", ".o"))
         objs.append(obj)
-        cmds.append([hipcc, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append([hipcc, *HIP_FLAGS, *(extra_flags or []), "-c", os.path.join(CSRC, src), "-o", obj])
     with ThreadPoolExecutor(max_workers=min(len(cmds), os.cpu_count() or 1)) as ex:
         list(ex.map(_run, cmds))
     tmp = out_path + ".tmp"

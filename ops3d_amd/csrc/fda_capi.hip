@@ -10,9 +10,10 @@
 //     only validated (min(B, step) must divide B, as flash_deform_attn_cuda.cu:56-58);
 //   * outputs are written in full by the kernels, in the value dtype: no zero-fill of output,
 //     grad_offset or grad_value and no fp32 -> dtype cast passes;
-//   * grad_value is a gather, not a scatter: the backward sorts its samples by base corner
-//     and every grad_value row is summed by one owner (fp32 global atomics on gfx950 run at
-//     ~0.5 lanes/clock per CU, far below what 8 corners x D channels per sample need).
+//   * grad_value is a gather, not a scatter: the backward groups its samples by spatial tile and
+//     every grad_value row is summed in registers by the one thread group that owns its tile
+//     (fp32 global atomics on gfx950 run at ~0.5 lanes/clock per CU, LDS fp32 atomics at ~0.3,
+//     far below what 8 corners x D channels per sample need).
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -26,12 +27,10 @@ namespace ops3d_fda {
 hipError_t launch_f32(int, int, int, const Args &, unsigned, size_t, hipStream_t);
 hipError_t launch_f16(int, int, int, const Args &, unsigned, size_t, hipStream_t);
 hipError_t launch_bf16(int, int, int, const Args &, unsigned, size_t, hipStream_t);
-bool binsort_supported(uint32_t n, int bits);
-size_t binsort_temp_bytes(uint32_t n, int bits);
-hipError_t binsort_pairs(uint32_t *keys_a, uint32_t *vals_a, uint32_t *keys_b, uint32_t *vals_b, uint32_t n,
-                         int bits, void *temp, size_t temp_bytes, const float4 *stash, float4 *sorted_stash,
-                         uint32_t *sorted_row, double inv_lk, uint32_t Q, uint32_t G, int ghm,
-                         const uint32_t **sorted_keys, hipStream_t st);
+hipError_t launch_tile_bucketing(const uint32_t *keys, const uint32_t *words, uint32_t n, uint32_t per_head,
+                                 const int64_t *shapes, int L, int BG, int TX, int TY, int TZ, uint32_t *counts,
+                                 uint32_t *start, uint32_t *cursor, uint2 *entries, hipStream_t st,
+                                 void (*mark)(int, hipStream_t));
 }  // namespace ops3d_fda
 
 using namespace ops3d_fda;
@@ -41,7 +40,7 @@ namespace {
 thread_local std::string g_last_error;
 
 // backward phase timing (ops3d_fda_profile_*)
-// events 0..5: backward (copies | query kernel | bin sort | bin offsets | value kernel)
+// events 0..5: backward (copies | query kernel | tile count + scan | tile scatter | tile kernel)
 // events 6..8: forward (head-major copy | forward kernel)
 constexpr int kProfEvents = 9;
 bool g_prof_on = false;
@@ -161,70 +160,64 @@ hipError_t launch(int dtype, int which, const Geometry &g, hipStream_t st) {
   }
 }
 
-// XCD-aware grid over (b, g, column) for `ncol_per_b` columns per batch item (see map_tile).
-void set_grid(Args &a, int ncol_per_b, unsigned &grid_out) {
-  a.nqb = ncol_per_b;
-  a.ncol = a.B * ncol_per_b;
-  int64_t grid;
-  if (a.xcd_mode == 0) grid = (int64_t)a.G * a.ncol;
-  else if (a.xcd_mode == 1) grid = 8 * (((int64_t)a.ncol + a.xpg - 1) / a.xpg);
-  else grid = (int64_t)a.G * a.ncol;
-  grid_out = (unsigned)grid;
-}
-
-// Workspace of the backward gather (all offsets 256-byte aligned):
-//   keys_in, keys_out, vals_in, vals_out : N uint32 each, N = B*Q*G*L*K samples
-//   stash, sorted stash                 : N float4 each
-//   sorted grad_output rows             : N uint32
-//   bin_start                           : nbins_bound + 1 uint32
-//   sort temporary storage              : tile histograms, their scan and its temporary
-// nbins_bound = B*G*8*S bounds the real bin count sum_l (D+1)(H+1)(W+1) without reading the
-// device-resident level shapes on the host.
+// Workspace of the backward (all offsets 256-byte aligned):
+//   keys, words    : N uint32 each, N = B*Q*G*L*K samples (home tile, tile-local word)
+//   stash          : N float4 (fx, fy, fz, attn)
+//   entries        : 8N uint2 (a sample is listed in at most 8 tiles)
+//   counts, start, cursor : B*G*S + 1 uint32 each (a tile holds at least one voxel, so a head
+//                    has at most S tiles)
+//   head-major copies of value and grad_output (G > 1)
 struct BwdLayout {
-  uint64_t n, nbins_bound;
-  int key_bits;
-  size_t off_keys_in, off_keys_out, off_vals_in, off_vals_out, off_stash, off_sstash, off_srow, off_bins,
-      off_temp, off_vhm, off_ghm;
-  size_t temp_bytes, total;
+  uint64_t n, ntiles_bound;
+  size_t off_keys, off_words, off_stash, off_entries, off_counts, off_start, off_cursor, off_vhm, off_ghm;
+  size_t total;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-
 int bwd_layout(int B, int S, int G, int D, int e, int L, int Q, int K, BwdLayout &ly) {
   ly = BwdLayout{};
   ly.n = (uint64_t)B * Q * G * L * K;
-  ly.nbins_bound = (uint64_t)B * G * 8 * (uint64_t)S;
-  if (ly.n >= 0xffffffffull || ly.nbins_bound >= 0xfffffff0ull)
-    return fail(OPS3D_FDA_EINVAL, "backward too large for 32-bit sample/bin indices (N=%llu, bins<=%llu)",
-                (unsigned long long)ly.n, (unsigned long long)ly.nbins_bound);
-  int bits = 1;
-  while (bits < 32 && (ly.nbins_bound >> bits) != 0) ++bits;
-  ly.key_bits = bits;
-  size_t temp = 0;
-  if (ly.n > 0) {
-    if (!binsort_supported((uint32_t)ly.n, bits))
-      return fail(OPS3D_FDA_EINVAL, "backward too large for the bin sort (N=%llu)", (unsigned long long)ly.n);
-    temp = binsort_temp_bytes((uint32_t)ly.n, bits);
-    if (temp == 0) return fail(OPS3D_FDA_ERUNTIME, "bin sort size query failed");
-  }
-  ly.temp_bytes = temp;
+  ly.ntiles_bound = (uint64_t)B * G * (uint64_t)S;
+  if (ly.n >= 0x1fffffffull || ly.ntiles_bound >= 0xfffffff0ull)
+    return fail(OPS3D_FDA_EINVAL, "backward too large for 32-bit sample/tile indices (N=%llu, tiles<=%llu)",
+                (unsigned long long)ly.n, (unsigned long long)ly.ntiles_bound);
   size_t o = 0;
   const size_t n4 = align256(ly.n * 4);
-  ly.off_keys_in = o; o += n4;
-  ly.off_keys_out = o; o += n4;
-  ly.off_vals_in = o; o += n4;
-  ly.off_vals_out = o; o += n4;
+  const size_t t4 = align256((ly.ntiles_bound + 1) * 4);
+  ly.off_keys = o; o += n4;
+  ly.off_words = o; o += n4;
   ly.off_stash = o; o += align256(ly.n * 16);
-  ly.off_sstash = o; o += align256(ly.n * 16);
-  ly.off_srow = o; o += n4;
-  ly.off_bins = o; o += align256((ly.nbins_bound + 1) * 4);
-  ly.off_temp = o; o += align256(temp);
-  // head-major copies of value and grad_output (G > 1)
+  ly.off_entries = o; o += align256(ly.n * 8 * 8);
+  ly.off_counts = o; o += t4;
+  ly.off_start = o; o += t4;
+  ly.off_cursor = o; o += t4;
   ly.off_vhm = o; o += G > 1 ? align256((size_t)B * S * G * D * e) : 0;
   ly.off_ghm = o; o += G > 1 ? align256((size_t)B * Q * G * D * e) : 0;
   ly.total = o;
   return OPS3D_FDA_OK;
+}
+
+// Entries per LDS chunk of the tile kernel: as many as fit next to the bin arrays in the
+// block's share of the CU's 160 KB of LDS (1024 threads: one block per CU; 512: two; 256:
+// three), so that one block stages its next chunk while the others compute.
+int tile_chunk(int D, int e, int lpu) {
+  const int rb = D * e;
+  const int nt = tile_threads(lpu);
+  const size_t bins = tile_kernel_lds_bytes(0, rb, lpu);
+  const size_t budget = (nt >= 1024 ? 150 : (nt >= 512 ? 76 : 50)) * (size_t)1024;
+  if (budget <= bins) return 0;
+  int ch = (int)((budget - bins) / (size_t)(rb + 24));
+  ch = ch > kTileKPT * nt ? kTileKPT * nt : ch;
+  ch &= ~63;
+  return ch;
+}
+
+int device_cus() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
+  return n;
 }
 
 // [B, N, G, R words] -> [B, G, N, R words]: the head-major copy of value / grad_output, so that
@@ -260,43 +253,6 @@ hipError_t launch_head_major(const void *src, void *dst, int64_t B, int64_t N, i
   hipLaunchKernelGGL(head_major_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
                      static_cast<const uint32_t *>(src), static_cast<uint32_t *>(dst), B, N, G, R);
   return hipGetLastError();
-}
-
-// bin_start[b] = first position of key >= b in the sorted keys, for b in [0, nbins_real],
-// nbins_real = B*G*sum_l (D+1)(H+1)(W+1) read from the device-resident level shapes.
-__global__ __launch_bounds__(256) void bin_start_kernel(const uint32_t *keys, uint32_t n, uint32_t *bin_start,
-                                                        uint32_t nbins_bound, const int64_t *shapes, int L,
-                                                        int BG) {
-  // bin_start[bb] = lower_bound(keys, bb) for bb in [0, last]: sorted element i starts every bin
-  // in (keys[i-1], keys[i]] (i = 0: [0, keys[0]]; i = n: (keys[n-1], last]).  Gaps of more than
-  // kSmallGap bins are filled by the whole wave.
-  constexpr uint64_t kSmallGap = 4;
-  uint32_t per = 0;
-  for (int l = 0; l < L; ++l) per += level_bins(shapes, l);
-  const uint64_t real = (uint64_t)per * (uint64_t)BG;
-  const uint64_t last = real < nbins_bound ? real : nbins_bound;
-  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-  const int lane = threadIdx.x & (kWave - 1);
-  for (uint64_t base = (uint64_t)blockIdx.x * blockDim.x; base <= n; base += stride) {
-    const uint64_t i = base + threadIdx.x;
-    uint64_t lo = 1, hi = 0;                          // empty
-    if (i <= n) {
-      lo = i == 0 ? 0 : (uint64_t)keys[i - 1] + 1;
-      hi = i == n ? last : ((uint64_t)keys[i] < last ? (uint64_t)keys[i] : last);
-    }
-    const bool big = lo <= hi && hi - lo >= kSmallGap;
-    if (lo <= hi && !big)
-      for (uint64_t bb = lo; bb <= hi; ++bb) bin_start[bb] = (uint32_t)i;
-    uint64_t m = __ballot(big);
-    while (m) {
-      const int src = __builtin_ctzll(m);
-      m &= m - 1;
-      const uint64_t blo = ((uint64_t)__shfl(( uint32_t)(lo >> 32), src) << 32) | __shfl((uint32_t)lo, src);
-      const uint64_t bhi = ((uint64_t)__shfl((uint32_t)(hi >> 32), src) << 32) | __shfl((uint32_t)hi, src);
-      const uint32_t bi = (uint32_t)__shfl((uint32_t)i, src);
-      for (uint64_t bb = blo + lane; bb <= bhi; bb += kWave) bin_start[bb] = bi;
-    }
-  }
 }
 
 }  // namespace
@@ -403,16 +359,13 @@ static int backward_impl(const void *value, const int64_t *spatial_shapes,
     return fail(OPS3D_FDA_EINVAL, "workspace must be 256-byte aligned");
 
   char *ws = static_cast<char *>(workspace);
-  uint32_t *keys_in = reinterpret_cast<uint32_t *>(ws + ly.off_keys_in);
-  uint32_t *keys_out = reinterpret_cast<uint32_t *>(ws + ly.off_keys_out);
-  uint32_t *vals_in = reinterpret_cast<uint32_t *>(ws + ly.off_vals_in);
-  uint32_t *vals_out = reinterpret_cast<uint32_t *>(ws + ly.off_vals_out);
+  uint32_t *keys = reinterpret_cast<uint32_t *>(ws + ly.off_keys);
+  uint32_t *words = reinterpret_cast<uint32_t *>(ws + ly.off_words);
   float4 *stash = reinterpret_cast<float4 *>(ws + ly.off_stash);
-  float4 *sstash = reinterpret_cast<float4 *>(ws + ly.off_sstash);
-  uint32_t *srow = reinterpret_cast<uint32_t *>(ws + ly.off_srow);
-  uint32_t *bins = reinterpret_cast<uint32_t *>(ws + ly.off_bins);
-  void *temp = ws + ly.off_temp;
-  const uint32_t *sorted_keys = keys_out;
+  uint2 *entries = reinterpret_cast<uint2 *>(ws + ly.off_entries);
+  uint32_t *counts = reinterpret_cast<uint32_t *>(ws + ly.off_counts);
+  uint32_t *tstart = reinterpret_cast<uint32_t *>(ws + ly.off_start);
+  uint32_t *cursor = reinterpret_cast<uint32_t *>(ws + ly.off_cursor);
 
   Args &a = geo.a;
   a.value = value;
@@ -421,10 +374,14 @@ static int backward_impl(const void *value, const int64_t *spatial_shapes,
   a.loc_attn = sampling_loc_attn;
   a.grad_out = grad_output;
   a.grad_loc_attn = grad_sampling_loc_attn;
-  a.keys = keys_in;
-  a.vals = vals_in;
+  a.keys = keys;
+  a.vals = words;
   a.stash = stash;
-  a.key_invalid = (uint32_t)ly.nbins_bound;
+  a.tile_counts = counts;
+  a.tile_start = tstart;
+  a.tile_cursor = cursor;
+  a.entries = entries;
+  tile_dims(tile_lanes(geo.lpu, geo.cpl * elem_size(dtype)), a.TX, a.TY, a.TZ);
   a.inv_lk = 1.0 / (double)(num_levels * num_point);
   hipError_t e;
   prof_mark(0, st);
@@ -441,47 +398,57 @@ static int backward_impl(const void *value, const int64_t *spatial_shapes,
   }
   prof_mark(1, st);
   if (work) {
-    // phase 1: location / logit gradients, per-sample bin keys and stash
+    // phase 1: location / logit gradients, per-sample home tile, tile-local corner and stash
     e = launch(dtype, 1, geo, st);
     if (e != hipSuccess)
       return fail(OPS3D_FDA_ERUNTIME, "backward query kernel launch failed: %s (grid=%u, lds=%zu)",
                   hipGetErrorString(e), geo.grid, geo.lds);
-    prof_mark(2, st);
-    // phase 2: stable sort of (bin, sample) pairs; stash and grad_output row in sorted order
-    e = binsort_pairs(keys_in, vals_in, keys_out, vals_out, (uint32_t)ly.n, ly.key_bits, temp, ly.temp_bytes,
-                      stash, sstash, srow, a.inv_lk, (uint32_t)num_query, (uint32_t)num_heads, a.ghm,
-                      &sorted_keys, st);
-    if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "bin sort failed: %s", hipGetErrorString(e));
-  } else {
-    prof_mark(2, st);
   }
-  prof_mark(3, st);
-  {
-    const uint64_t nb = ly.n + 1;
-    unsigned blocks = (unsigned)((nb + 255) / 256);
-    if (blocks > 16384) blocks = 16384;
-    hipLaunchKernelGGL(bin_start_kernel, dim3(blocks), dim3(256), 0, st, sorted_keys, work ? (uint32_t)ly.n : 0u,
-                       bins, (uint32_t)ly.nbins_bound, spatial_shapes, num_levels, batch * num_heads);
-    e = hipGetLastError();
-    if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "bin kernel launch failed: %s", hipGetErrorString(e));
-  }
+  prof_mark(2, st);
+  // phase 2: entries grouped by tile (counters are cleared even without samples: the tile
+  // kernel reads the tile ranges of every tile)
+  e = launch_tile_bucketing(keys, words, work ? (uint32_t)ly.n : 0u,
+                            (uint32_t)num_query * (uint32_t)(num_levels * num_point), spatial_shapes, num_levels,
+                            batch * num_heads, a.TX, a.TY, a.TZ, counts, tstart, cursor, entries, st,
+                            g_prof_on ? prof_mark : nullptr);
+  if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "tile bucketing failed: %s", hipGetErrorString(e));
   prof_mark(4, st);
   if (nval > 0) {
-    // phase 3: one owner per grad_value row, gathered from 8 bins, written once
+    // phase 3: one owner per grad_value row (per tile, in registers), written once
     Geometry g3 = geo;
-    const int VPB = value_voxels_per_block(geo.lpu);
-    const int nvb_bound = (int)(((int64_t)spatial_size + VPB - 1) / VPB) + num_levels;
-    set_grid(g3.a, nvb_bound, g3.grid);
-    g3.a.sorted_stash = sstash;
-    g3.a.sorted_row = srow;
-    g3.a.bin_start = bins;
     g3.a.out = grad_value;
     g3.a.accumulate = out_f32_accumulate ? 1 : 0;
-    g3.lds = 0;
+    g3.a.tile_affinity = num_heads % 8 == 0;
+    g3.a.chunk = tile_chunk(channels, elem_size(dtype), tile_lanes(geo.lpu, geo.cpl * elem_size(dtype)));
+    g3.lds = tile_kernel_lds_bytes(g3.a.chunk, channels * elem_size(dtype),
+                                   tile_lanes(geo.lpu, geo.cpl * elem_size(dtype)));
+    g3.grid = (unsigned)device_cus();   // times the resident blocks per CU (launch_one)
+    if (g3.a.tile_affinity) g3.grid = (g3.grid + 7) & ~7u;
+    if (g3.a.chunk < 64 || g3.lds > 160 * 1024)
+      return fail(OPS3D_FDA_EINVAL, "channels per head D=%d too large for the backward tile kernel", channels);
+#if OPS3D_FDA_TILE_TIMING
+    static unsigned long long *dbg = nullptr;
+    if (!dbg && hipMalloc(&dbg, 6 * sizeof(unsigned long long)) != hipSuccess) dbg = nullptr;
+    if (dbg) (void)hipMemsetAsync(dbg, 0, 6 * sizeof(unsigned long long), st);
+    g3.a.dbg = dbg;
+#endif
     e = launch(dtype, 2, g3, st);
     if (e != hipSuccess)
-      return fail(OPS3D_FDA_ERUNTIME, "backward value kernel launch failed: %s (grid=%u)", hipGetErrorString(e),
-                  g3.grid);
+      return fail(OPS3D_FDA_ERUNTIME, "backward tile kernel launch failed: %s (grid=%u, lds=%zu)",
+                  hipGetErrorString(e), g3.grid, g3.lds);
+#if OPS3D_FDA_TILE_TIMING
+    if (dbg) {
+      unsigned long long h[6];
+      if (hipMemcpyAsync(h, dbg, sizeof(h), hipMemcpyDeviceToHost, st) == hipSuccess &&
+          hipStreamSynchronize(st) == hipSuccess) {
+        unsigned long long tot = 0;
+        for (int i = 0; i < 6; ++i) tot += h[i];
+        fprintf(stderr, "[tile timing] clear %.1f%% stage %.1f%% rows+scan %.1f%% sort %.1f%% owners %.1f%% tile %.1f%% (%.3g Mcyc/block)\n",
+                100.0 * h[0] / tot, 100.0 * h[1] / tot, 100.0 * h[2] / tot, 100.0 * h[3] / tot, 100.0 * h[4] / tot,
+                100.0 * h[5] / tot, tot / 1e6 / g3.grid);
+      }
+    }
+#endif
   }
   prof_mark(5, st);
   if (g_prof_on) g_prof_recorded[0] = true;

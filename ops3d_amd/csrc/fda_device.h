@@ -42,18 +42,22 @@ struct Args {
   void *out;                  // [B,Q,G*D] T          (forward)
   float *grad_value;          // [B,S,G,D] fp32 acc   (backward)
   void *grad_loc_attn;        // [B,Q,G,P] T          (backward)
-  // backward, gather formulation of grad_value
-  uint32_t *keys;             // [N] bin of each sample's base corner (key_invalid if skipped)
-  uint32_t *vals;             // [N] sample index (iota), sort payload
+  // backward, tile formulation of grad_value
+  uint32_t *keys;             // [N] home tile of each sample's base corner (kKeyInvalid if outside)
+  uint32_t *vals;             // [N] tile-local base corner word of each sample (tile_word)
   float4 *stash;              // [N] (fx, fy, fz, attn) of each sample
-  const uint32_t *bin_start;    // [nbins_bound + 1] first sorted position of each bin
-  const float4 *sorted_stash;   // [N] stash in sorted order
-  const uint32_t *sorted_row;   // [N] grad_output row (b*Q + q)*G + g in sorted order
-  uint32_t key_invalid;       // = nbins_bound, sorts after every real bin
-  int accumulate;             // phase 3: add into grad_value instead of overwriting
+  uint32_t *tile_counts;      // [B*G*T_h] entries per tile
+  uint32_t *tile_start;       // [B*G*T_h + 1] first entry of each tile (exclusive scan)
+  uint32_t *tile_cursor;      // [B*G*T_h] fill cursor of each tile
+  uint2 *entries;             // [<= 8N] (sample, tile-local base corner word), grouped by tile
+  int TX, TY, TZ;             // nominal tile dimensions (voxels), clipped per level
+  int chunk;                  // entries per LDS chunk of the tile kernel
+  int tile_affinity;          // tiles of head g run on XCD g % 8 (G % 8 == 0)
+  int accumulate;             // add into an fp32 grad_value instead of overwriting
   int vhm;                    // value is head-major [B,G,S,D] (a transposed copy)
   int ghm;                    // grad_out is head-major [B,G,Q,D] (a transposed copy)
   double inv_lk;              // 1.0 / (L*K), for sample -> unit
+  unsigned long long *dbg;    // tile kernel phase cycles (OPS3D_FDA_TILE_TIMING builds only)
   int B, S, G, D, L, K, Q, P;
   int nqb;                    // query blocks per batch = ceil(Q / UPB)
   int ncol;                   // B * nqb
@@ -467,49 +471,97 @@ __device__ __forceinline__ SampleBase unit_bcast(const SampleBase &sb) {
   return r;
 }
 
-// LDS floats per unit of the backward query kernel (record, grad_attn, 16-byte-aligned stash
-// and keys); the block uses UPB times this.  Rounded to 4 x an odd number so that the units of
+// LDS floats per unit of the backward query kernel (record, grad_attn, 16-byte-aligned stash,
+// tile keys and tile-local words); the block uses UPB times this.  Rounded to 4 x an odd number so that the units of
 // a wave start in different LDS banks.
 __host__ __device__ constexpr int bwd_query_lds_floats(int P, int LK) {
-  return (((((P + LK + 3) & ~3) + 5 * LK + ((LK & 3) ? 4 - (LK & 3) : 0)) / 4) | 1) * 4;
+  return ((((((P + LK + 3) & ~3) + 6 * LK) + 3) / 4) | 1) * 4;
 }
 
-// Geometry of the backward value kernel: lane groups of LPU lanes, NBP of them (one per
-// neighbour bin, fewer when LPU is large) per voxel.
-template <int LPU> struct ValueGeom {
-  static constexpr int NBP = (kWave / LPU) >= 8 ? 8 : (kWave / LPU);   // parallel bins per voxel
-  static constexpr int VPW = kWave / (LPU * NBP);                      // voxels per wave
-  static constexpr int VPB = kWavesPerBlock * VPW;                     // voxels per block step
-#ifndef OPS3D_FDA_VALUE_VIT
-#define OPS3D_FDA_VALUE_VIT 8
-#endif
-  static constexpr int VIT = OPS3D_FDA_VALUE_VIT;                      // steps per block
-};
-
-// voxels per block of fda_bwd_value_kernel for a given LPU (host side)
-inline int value_voxels_per_block(int lpu) {
-  switch (lpu) {
-    case 1: return ValueGeom<1>::VPB * ValueGeom<1>::VIT;
-    case 2: return ValueGeom<2>::VPB * ValueGeom<2>::VIT;
-    case 4: return ValueGeom<4>::VPB * ValueGeom<4>::VIT;
-    case 8: return ValueGeom<8>::VPB * ValueGeom<8>::VIT;
-    case 16: return ValueGeom<16>::VPB * ValueGeom<16>::VIT;
-    default: return ValueGeom<32>::VPB * ValueGeom<32>::VIT;
-  }
-}
-
-// Sample numbering of the backward gather, head-major so that one block's samples are
+// Sample numbering of the backward, head-major so that one block's samples are
 // contiguous: gs = ((b*G + g)*Q + q)*L*K + s.
 __device__ __forceinline__ uint32_t sample_index(int b, int g, int q, int s, int G, int Q, int LK) {
   return (((uint32_t)b * G + g) * (uint32_t)Q + q) * (uint32_t)LK + s;
 }
 
-// Bins of the backward gather: per (b, g) and level, one bin per possible base corner
-// (x0, y0, z0) in [-1, W) x [-1, H) x [-1, D), i.e. (W+1)(H+1)(D+1) bins (0 for an empty
-// level), <= 8 * D*H*W.  Returns the bins of one (b, g) and the offset of level `lvl`.
-__device__ __forceinline__ uint32_t level_bins(const int64_t *shapes, int l) {
-  const uint32_t d = (uint32_t)shapes[3 * l], h = (uint32_t)shapes[3 * l + 1], w = (uint32_t)shapes[3 * l + 2];
-  return (d == 0 || h == 0 || w == 0) ? 0u : (d + 1) * (h + 1) * (w + 1);
+// ---------------------------------------------------------------------------------------------
+// Tiles of the backward's value gradient.  Each level of each (b, g) is cut into tiles of
+// TX x TY x TZ voxels (clipped to the level: a level smaller than the tile is one tile); the
+// tile kernel owns one tile at a time and sums every grad_value row of it in registers.  A
+// sample is listed in its HOME tile, the tile containing corner (max(x0,0), max(y0,0),
+// max(z0,0)), and additionally in the next tile along each axis on which its base corner is the
+// home tile's last voxel (its upper corner then lies in that tile): 1 to 8 entries per sample.
+// Threads of a tile-kernel block for `lpu` lanes per x-pair: 64 * lpu, at least 256 and at
+// most 1024, so tiles hold 128 voxels (512/lpu for lpu < 4, 64 for lpu = 32).
+__host__ __device__ constexpr int tile_threads(int lpu) {
+  return lpu <= 4 ? 256 : (lpu >= 16 ? 1024 : 64 * lpu);
+}
+constexpr int kTileKPT = 2;          // entries per thread and chunk (chunk <= 2 * threads)
+constexpr uint32_t kKeyInvalid = 0xffffffffu;
+
+// Lanes per x-pair of voxels in the tile kernel (lane_bytes = CPL * sizeof(T) of the query
+// kernels).  The same as the query kernels' LPU: fewer lanes per pair would spread each entry
+// visit's fixed cost over more channels, but put more pairs -- each with its own entry count --
+// into a wave, whose loops run as long as its busiest pair's (measured slower on gfx950).
+__host__ __device__ constexpr int tile_lanes(int lpu, int lane_bytes) { return (void)lane_bytes, lpu; }
+
+// Nominal tile dimensions for the tile kernel: its tile_threads(lpu) threads own x-pairs of
+// voxels, lpu lanes each, so a tile has 2 * tile_threads(lpu) / lpu voxels, as cubic as powers
+// of two allow (x even).
+__host__ __device__ constexpr void tile_dims(int lpu, int &tx, int &ty, int &tz) {
+  int v = 2 * tile_threads(lpu) / lpu, lg = 0;
+  while ((1 << lg) < v) ++lg;
+  // split lg bits over (x, y, z): x gets the extra bit first, then y
+  const int bz = lg / 3, by = (lg - bz) / 2, bx = lg - bz - by;
+  tx = 1 << bx;
+  ty = 1 << by;
+  tz = 1 << bz;
+}
+
+// LDS bytes of fda_bwd_tile_kernel for `chunk` entries of row_bytes each, `lpu` tile lanes
+// per x-pair (host side).
+inline size_t tile_kernel_lds_bytes(int chunk, int row_bytes, int lpu) {
+  int tx, ty, tz;
+  tile_dims(lpu, tx, ty, tz);
+  const size_t nb = (size_t)(tx + 1) * (ty + 1) * (tz + 1);
+  return (size_t)chunk * (16 + (size_t)row_bytes + 8) + (2 * nb + 1) * 4 + 4;
+}
+
+struct LevelTiles {
+  int n[3];       // level size (D, H, W)
+  int t[3];       // tile size  (tz, ty, tx), clipped to the level
+  int nt[3];      // tiles per axis
+  int sh[3];      // log2 of the nominal tile size: tile index of a voxel = coordinate >> sh
+                  // (t is the nominal size, a power of two, or the level is one tile wide)
+  uint32_t count; // tiles of the level (0 for an empty level)
+};
+
+__device__ __forceinline__ LevelTiles level_tiles(const int64_t *shapes, int l, int TX, int TY, int TZ) {
+  LevelTiles lt;
+  const int T[3] = {TZ, TY, TX};
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    const int n = (int)shapes[3 * l + a];
+    lt.n[a] = n;
+    lt.t[a] = n < T[a] ? (n > 0 ? n : 1) : T[a];
+    lt.nt[a] = n > 0 ? (n + lt.t[a] - 1) / lt.t[a] : 0;
+    lt.sh[a] = 31 - __builtin_clz((unsigned)T[a]);
+  }
+  lt.count = (uint32_t)lt.nt[0] * (uint32_t)lt.nt[1] * (uint32_t)lt.nt[2];
+  return lt;
+}
+
+__device__ __forceinline__ uint32_t tiles_per_head(const int64_t *shapes, int L, int TX, int TY, int TZ) {
+  uint32_t t = 0;
+  for (int l = 0; l < L; ++l) t += level_tiles(shapes, l, TX, TY, TZ).count;
+  return t;
+}
+
+// Tile-local word of an entry: base corner relative to the tile origin, each coordinate in
+// [-1, t) stored +1 in 5 bits (x bits 0-4, y 5-9, z 10-14); in a sample's home word also the
+// "next tile" flags (x bit 15, y 16, z 17) and the level (bits 18-20).
+__device__ __forceinline__ uint32_t tile_word(int lx, int ly, int lz) {
+  return (uint32_t)(lx + 1) | ((uint32_t)(ly + 1) << 5) | ((uint32_t)(lz + 1) << 10);
 }
 
 }  // namespace ops3d_fda

@@ -4,14 +4,16 @@
 //   out[b,q,g,:] = sum_{l,k} softmax(logits[b,q,g,:])[l,k] *
 //                  trilinear(value_l[b,:,g,:], pixel(loc[b,q,g,l,k]))
 // Backward (replaces backward_kernel_warp_primitive, flash_deform_col2im_cuda.cuh:248-429, and
-// ms_deform_attn_col2im_trilinear, common.h:141-353), in two kernels around a sort:
+// ms_deform_attn_col2im_trilinear, common.h:141-353), in two kernels around a bucketing of the
+// samples by spatial tile:
 //   phase 1 (query-major)  grad_loc  = attn * size * sum_c grad_out[c] * d(interp_c)/d(pixel)
 //                          grad_attn = sum_c grad_out[c] * interp_c, then softmax backward
 //                          grad_logit_i = a_i * (grad_attn_i - sum_j a_j grad_attn_j)
-//                          + per sample: key = bin of its base corner, stash (fx,fy,fz,attn)
-//   phase 2                stable radix sort of (key, sample) pairs
-//   phase 3 (voxel-major)  grad_value[v] = sum over samples s with a corner at v of
-//                          attn_s * w_corner(s) * grad_out[unit(s)]     (register sums, no atomics)
+//                          + per sample: its home tile, tile-local base corner, stash
+//                          (fx,fy,fz,attn)
+//   phase 2 (fda_tiles.hip) entries (sample, tile-local corner) grouped by tile
+//   phase 3 (tile-major)   grad_value[v] = sum over entries s of v's tile with a corner at v of
+//                          attn_s * w_corner(s) * grad_out[unit(s)]   (register sums, no atomics)
 // The per-sample location/attention partials are formed from U_i = sum_c grad_out[c] * V_i[c]
 // (one dot product per corner) so the channel loop costs one FMA per corner and channel, and
 // are summed over the unit's LPU lanes with DPP / ds_swizzle reductions.
@@ -19,14 +21,11 @@
 
 #include "fda_device.h"
 
-#ifndef OPS3D_FDA_VALUE_REVERSE
-#define OPS3D_FDA_VALUE_REVERSE 1
+#ifndef OPS3D_FDA_TILE_TIMING
+#define OPS3D_FDA_TILE_TIMING 0   // 1: per-phase cycle counts of the tile kernel into Args::dbg
 #endif
-#ifndef OPS3D_FDA_VALUE_BALANCED
-#define OPS3D_FDA_VALUE_BALANCED 1
-#endif
-#ifndef OPS3D_FDA_VALUE_UNROLL
-#define OPS3D_FDA_VALUE_UNROLL 2
+#ifndef OPS3D_FDA_TILE_WPE
+#define OPS3D_FDA_TILE_WPE 4    // minimum waves per SIMD the tile kernel is compiled for
 #endif
 
 namespace ops3d_fda {
@@ -276,13 +275,14 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
   const int q = qb * UPB + ub;
   const bool live = q < a.Q;
   const int L = a.L, K = a.K, LK = L * K, P = a.P;
-  // per unit: [0,P) record (later its gradient), [P,P+LK) grad_attn, then LK stash float4s
-  // and LK keys for the wave's coalesced write-out
+  // per unit: [0,P) record (later its gradient), [P,P+LK) grad_attn, then LK stash float4s,
+  // LK tile keys and LK tile-local words for the wave's coalesced write-out
   const int RS = bwd_query_lds_floats(P, LK);
   float *rec = lds + ub * RS;
   float *gat_s = rec + P;
   float4 *st_s = reinterpret_cast<float4 *>(lds + ub * RS + ((P + LK + 3) & ~3));
   uint32_t *key_s = reinterpret_cast<uint32_t *>(st_s + LK);
+  uint32_t *word_s = key_s + LK;
   const int64_t unit = ((int64_t)b * a.Q + (live ? q : 0)) * a.G + g;
 
   stage_record<T, LPU>(static_cast<const T *>(a.loc_attn) + unit * P, P, j, live, rec);
@@ -301,9 +301,8 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
     for (int c = 0; c < NW; ++c) tgw[c] = 0u;
   }
 
-  uint32_t bins_bg = 0;
-  for (int l = 0; l < L; ++l) bins_bg += level_bins(a.shapes, l);
-  uint32_t bin_base = (uint32_t)(b * a.G + g) * bins_bg;
+  // tile ids of this (b, g): bg * T_h + (tiles of the earlier levels) + tile within the level
+  uint32_t tile_base = (uint32_t)(b * a.G + g) * tiles_per_head(a.shapes, L, a.TX, a.TY, a.TZ);
 
   const int RST = a.vhm ? a.D : a.G * a.D;
   const uint32_t lane_elem = (uint32_t)((a.vhm ? 0 : g * a.D) + j * CPL);
@@ -315,6 +314,7 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
     const int64_t st = a.lsi[l];
     const int64_t nel = (int64_t)Dl * Hl * Wl * RST;
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb + st * RST, (uint32_t)(nel * (int64_t)sizeof(T)));
+    const LevelTiles lt = level_tiles(a.shapes, l, a.TX, a.TY, a.TZ);
     // two samples per step: both records are read before either gradient is written back, so
     // the 16 corner loads of the pair are in flight together
     for (int k = 0; k < K; k += 2, s += 2) {
@@ -373,14 +373,21 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
           rec[3 * su + 1] = gy * at[u] * (float)Hl;
           rec[3 * su + 2] = gz * at[u] * (float)Dl;
           gat_s[su] = ga;
-          key_s[su] = in[u] ? bin_base + (uint32_t)(((m.z0 + 1) * (Hl + 1) + (m.y0 + 1)) * (Wl + 1) + (m.x0 + 1))
-                            : a.key_invalid;
+          // home tile: the tile holding corner (max(x0,0), max(y0,0), max(z0,0)); the sample
+          // is also listed in the next tile along an axis where x0 is the tile's last voxel
+          const int hz = max(m.z0, 0) >> lt.sh[0], hy = max(m.y0, 0) >> lt.sh[1], hx = max(m.x0, 0) >> lt.sh[2];
+          const int lz = m.z0 - hz * lt.t[0], ly = m.y0 - hy * lt.t[1], lx = m.x0 - hx * lt.t[2];
+          const uint32_t ex = lx == lt.t[2] - 1 && (hx + 1) * lt.t[2] < Wl;
+          const uint32_t ey = ly == lt.t[1] - 1 && (hy + 1) * lt.t[1] < Hl;
+          const uint32_t ez = lz == lt.t[0] - 1 && (hz + 1) * lt.t[0] < Dl;
+          key_s[su] = in[u] ? tile_base + (uint32_t)((hz * lt.nt[1] + hy) * lt.nt[2] + hx) : kKeyInvalid;
+          word_s[su] = tile_word(lx, ly, lz) | (ex << 15) | (ey << 16) | (ez << 17) | ((uint32_t)l << 18);
           st_s[su] = make_float4(m.wx[1], m.wy[1], m.wz[1], at[u]);
         }
       }
     }
     s += K - ((K + 1) & ~1);   // the steps above advanced s by K rounded up to even
-    bin_base += level_bins(a.shapes, l);
+    tile_base += lt.count;
   }
   wave_lds_sync();
   {
@@ -396,7 +403,7 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
         const float4 *stx = reinterpret_cast<const float4 *>(lds + ubx * RS + ((P + LK + 3) & ~3));
         const uint32_t *kx = reinterpret_cast<const uint32_t *>(stx + LK);
         a.keys[gs0 + e] = kx[ss];
-        a.vals[gs0 + e] = gs0 + e;
+        a.vals[gs0 + e] = kx[LK + ss];
         a.stash[gs0 + e] = stx[ss];
       }
     }
@@ -414,146 +421,266 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Backward phase 3, voxel-major: one grad_value row grad_value[b, v, g, :] of level l is the
-// sum of attn * w_corner * grad_out over every sample with a corner at v, i.e. over the samples
-// of the 8 bins whose base corner is v - (dz,dy,dx).  NBP lane groups (one per bin, or per
-// 8/NBP bins when LPU is large) sum their bins in registers and are then reduced across the
-// wave with DPP / ds_swizzle; every row is written exactly once, in T, in a deterministic order
-// (stable sort of fixed-position keys): no zero-fill, no atomics.
-template <int LPU, int NBP>
-__device__ __forceinline__ float bin_group_sum(float v) {
+// Backward phase 3, tile-major: grad_value of one tile = for every voxel v of the tile, the sum of
+// attn * w_corner * grad_out over the tile's entries (samples) with a corner at v.  A block of
+// tile_threads(LPU) threads owns the tile: LPU lanes own an x-pair of voxels (x0, x0+1) and CPL channels,
+// and keep their sums in registers.  The tile's entries are processed in chunks:
+//   1. stage each entry's stash (fx, fy, fz, attn) and grad_output row in LDS, and count the
+//      entries of each local bin (base corner in [-1,tx) x [-1,ty) x [-1,tz), LDS atomics),
+//   2. exclusive scan of the bin counts,
+//   3. counting-sort the chunk by bin (LDS atomics),
+//   4. each owner walks the entries of the bins with a corner on its voxels -- for each (dz, dy)
+//      the three contiguous bins of base x0-1, x0, x0+1 -- reading only LDS.
+// Every grad_value row of the tile is written once, in T (or added to an fp32 buffer): no
+// zero-fill, no global atomics.  Tiles are scheduled coarse levels first (their tiles hold the
+// most entries), and with G % 8 == 0 the tiles of head g run on XCD g % 8, whose L2 then holds
+// that head's grad_output rows.
+
+// Exclusive scan across the NT threads of a block; tmp holds NT/64 words.
+template <int NT>
+__device__ __forceinline__ uint32_t block_exclusive_scan_tile(uint32_t x, uint32_t *tmp) {
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+  uint32_t inc = x;
 #pragma unroll
-  for (int m = LPU; m < LPU * NBP; m <<= 1) {
-    if (m == 1) v += xor_lane<1>(v);
-    else if (m == 2) v += xor_lane<2>(v);
-    else if (m == 4) v += xor_lane<4>(v);
-    else if (m == 8) v += xor_lane<8>(v);
-    else if (m == 16) v += xor_lane<16>(v);
-    else v += xor_lane<32>(v);
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint32_t y = __shfl_up(inc, o, kWave);
+    if (lane >= o) inc += y;
   }
-  return v;
+  if (lane == kWave - 1) tmp[w] = inc;
+  __syncthreads();
+  uint32_t wofs = 0;
+  for (int ww = 0; ww < w; ++ww) wofs += tmp[ww];
+  __syncthreads();
+  return wofs + inc - x;
 }
 
 template <typename T, int CPL, int LPU>
-__global__ __launch_bounds__(kBlock) void fda_bwd_value_kernel(const Args a) {
-  using VG = ValueGeom<LPU>;
-  constexpr int NBP = VG::NBP, VPW = VG::VPW, VPB = VG::VPB, VIT = VG::VIT;
-  int b, g, vb;
-  if (!map_tile(a, blockIdx.x, b, g, vb)) return;
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  const int j = lane & (LPU - 1);
-  const int dp = (lane / LPU) % NBP;                  // which lane group of the pair
-  const int vw = lane / (LPU * NBP);                  // pair within the wave
-  // A "pair" is two x-neighbour voxels (x0, x0+1) of one row; pairs per level D*H*ceil(W/2).
-  // Locate the level of pair block vb (block-uniform); coarse (last) levels first: their bins
-  // hold the most samples, so their blocks are the longest and must not start last.
-  int Dl = 0, Hl = 0, Wl = 0;
-  uint32_t bin_lvl = 0, bins_bg = 0;
-  uint32_t vstart = 0;
-  bool found = false;
-  int rem = vb;
-  for (int tt = 0; tt < a.L; ++tt) {
-    const int t = OPS3D_FDA_VALUE_REVERSE ? a.L - 1 - tt : tt;
-    const int d = (int)a.shapes[3 * t], h = (int)a.shapes[3 * t + 1], w = (int)a.shapes[3 * t + 2];
-    const uint32_t n = (uint32_t)d * (uint32_t)h * (((uint32_t)w + 1) >> 1);
-    const int nvb = (int)((n + VPB * VIT - 1) / (VPB * VIT));
-    if (!found) {
-      if (rem < nvb) {
-        found = true; Dl = d; Hl = h; Wl = w; vstart = (uint32_t)a.lsi[t];
-        for (int u = 0; u < t; ++u) bin_lvl += level_bins(a.shapes, u);
-      } else {
-        rem -= nvb;
-      }
-    }
-    bins_bg += level_bins(a.shapes, t);
-  }
-  if (!found) return;
-  const uint32_t Wp = ((uint32_t)Wl + 1) >> 1;          // pairs per row
-  const uint32_t npair = (uint32_t)Dl * (uint32_t)Hl * Wp;
-  const uint32_t HWp = (uint32_t)Hl * Wp;
-  const uint32_t bin_lb = (uint32_t)(b * a.G + g) * bins_bg + bin_lvl;
-  const uint32_t W1 = (uint32_t)Wl + 1, HW1 = ((uint32_t)Hl + 1) * W1;
-  const T *go = static_cast<const T *>(a.grad_out);
-  const int D = a.D, GD = a.G * a.D;
-  const int64_t obase = ((int64_t)b * a.S + vstart) * GD + g * D + j * CPL;
+__global__ __launch_bounds__(tile_threads(LPU)) __attribute__((amdgpu_waves_per_eu(OPS3D_FDA_TILE_WPE)))
+void fda_bwd_tile_kernel(const Args a) {
+  constexpr int NT = tile_threads(LPU);
+  extern __shared__ __align__(16) unsigned char tsm[];
+  __shared__ uint32_t scan_tmp[NT / kWave];
+  constexpr int EB = CPL * (int)sizeof(T);      // bytes of a lane's channels
+  constexpr int NW = EB / 4;
+  const int tid = threadIdx.x;
+  const int D = a.D, G = a.G, L = a.L;
+  constexpr int RB = CPL * LPU * (int)sizeof(T);   // bytes of a grad_output row (D = CPL*LPU)
+  const int CH = a.chunk;                          // <= kTileKPT * NT
+  const int NBX = (a.TX + 1) * (a.TY + 1) * (a.TZ + 1);
+  float4 *st_l = reinterpret_cast<float4 *>(tsm);
+  unsigned char *row_l = tsm + (size_t)CH * 16;
+  uint32_t *start_l = reinterpret_cast<uint32_t *>(row_l + (size_t)CH * RB);   // [NBX + 1]
+  uint32_t *cur_l = start_l + NBX + 1;                                        // [NBX]
+  uint16_t *lbin_l = reinterpret_cast<uint16_t *>(cur_l + NBX);               // [CH]
+  uint16_t *sorted_l = lbin_l + CH;                                          // [CH]
+  uint32_t *rowi_l = reinterpret_cast<uint32_t *>(sorted_l + CH + (CH & 1));  // [CH]
 
-  for (int it = 0; it < VIT; ++it) {
-    const uint32_t v = (uint32_t)(rem * VIT + it) * VPB + wave * VPW + vw;
-    const bool live = v < npair;   // dead lanes still take part in the cross-group reduction
-    float acc0[CPL], acc1[CPL];      // voxels x0 and x0 + 1
+  // owner: x-pair p of the nominal tile, channel chunk j
+  const int p = tid / LPU, j = tid & (LPU - 1);
+  const int hxn = a.TX / 2;
+  const int px = p % hxn, py = (p / hxn) % a.TY, pz = p / (hxn * a.TY);
+
+  const uint32_t T_h = tiles_per_head(a.shapes, L, a.TX, a.TY, a.TZ);
+  int xcd = 0, bi = blockIdx.x, nbx = gridDim.x, hpx = G;   // heads served by this block's group
+  if (a.tile_affinity) {
+    xcd = blockIdx.x & 7;
+    bi = blockIdx.x >> 3;
+    nbx = ((int)gridDim.x - xcd + 7) >> 3;
+    hpx = G / 8;
+  }
+  const uint32_t nbg = (uint32_t)a.B * (uint32_t)hpx;
+  const uint32_t total = nbg * T_h;
+  const T *go = static_cast<const T *>(a.grad_out);
+
+#if OPS3D_FDA_TILE_TIMING
+  unsigned long long t_acc[6] = {0, 0, 0, 0, 0, 0}, t_prev = clock64();
+#define TILE_MARK(i)                                        \
+  do {                                                      \
+    const unsigned long long t_now = clock64();             \
+    t_acc[i] += t_now - t_prev;                             \
+    t_prev = t_now;                                         \
+  } while (0)
+#else
+#define TILE_MARK(i) ((void)0)
+#endif
+  for (uint32_t k = (uint32_t)bi; k < total; k += (uint32_t)nbx) {
+    // k -> (level, head, tile), coarse (last) levels first
+    uint32_t rem = k, lbase = 0;
+    int l = L - 1;
+    for (; l > 0; --l) {
+      const uint32_t nl = nbg * level_tiles(a.shapes, l, a.TX, a.TY, a.TZ).count;
+      if (rem < nl) break;
+      rem -= nl;
+    }
+    for (int u = 0; u < l; ++u) lbase += level_tiles(a.shapes, u, a.TX, a.TY, a.TZ).count;
+    const LevelTiles lt = level_tiles(a.shapes, l, a.TX, a.TY, a.TZ);
+    const uint32_t bgi = rem / lt.count, t = rem - bgi * lt.count;
+    const int b = (int)(bgi / (uint32_t)hpx);
+    const int g = a.tile_affinity ? xcd + 8 * (int)(bgi % (uint32_t)hpx) : (int)(bgi % (uint32_t)hpx);
+    const int itx = (int)(t % (uint32_t)lt.nt[2]);
+    const int ity = (int)((t / (uint32_t)lt.nt[2]) % (uint32_t)lt.nt[1]);
+    const int itz = (int)(t / ((uint32_t)lt.nt[2] * (uint32_t)lt.nt[1]));
+    const int tz = lt.t[0], ty = lt.t[1], tx = lt.t[2];
+    const int Dl = lt.n[0], Hl = lt.n[1], Wl = lt.n[2];
+    const int z = itz * tz + pz, y = ity * ty + py, x0 = itx * tx + 2 * px;
+    const bool live = 2 * px < tx && py < ty && pz < tz && z < Dl && y < Hl && x0 < Wl;
+    const bool two = 2 * px + 1 < tx && x0 + 1 < Wl;
+    const uint32_t gid = (uint32_t)(b * G + g) * T_h + lbase + t;
+    const uint32_t e0 = a.tile_start[gid], e1 = a.tile_start[gid + 1];
+    const int TXp = tx + 1, TYp = ty + 1;
+    const int nb = TXp * TYp * (tz + 1);
+
+    float acc0[CPL], acc1[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; ++c) acc0[c] = acc1[c] = 0.f;
-    uint32_t z = 0, y = 0, x0 = 0;
-    if (live) {
-      z = v / HWp;
-      const uint32_t r2 = v - z * HWp;
-      y = r2 / Wp;
-      x0 = (r2 - y * Wp) * 2;
-      // Samples with a corner on x0 or x0+1 in row (z, y): for each (dz, dy), the contiguous
-      // bins of base x0-1, x0, x0+1 (shifted by +1: x0, x0+1, x0+2).  Base x0-1 feeds x0 (dx=1),
-      // base x0 feeds x0 (dx=0) and x0+1 (dx=1), base x0+1 feeds x0+1 (dx=0); each grad_out
-      // row is loaded and widened once for both voxels.
-      const uint32_t bin_p = bin_lb + (z + 1) * HW1 + (y + 1) * W1 + x0;   // shifted base x0-1
-      const bool two = x0 + 1 < (uint32_t)Wl;
-      // One range per (dz, dy) (compile-time r, so wy / wz are fixed selections); the range's
-      // entries are dealt round-robin to the pair's NBP lane groups.
+
+    for (uint32_t c0 = e0; c0 < e1; c0 += (uint32_t)CH) {
+      const int n = (int)min((uint32_t)CH, e1 - c0);
+      for (int i = tid; i < nb; i += NT) cur_l[i] = 0u;
+      __syncthreads();
+      TILE_MARK(0);
+      // 1a. entries: local bin, stash, grad_output row index; bin counts.  All global loads of
+      // the thread's entries are issued before any is used.
+      {
+        uint2 en[kTileKPT];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const uint32_t rb = bin_p - (uint32_t)(r >> 1) * HW1 - (uint32_t)(r & 1) * W1;   // (dz, dy) = (r>>1, r&1)
-        // a pair with one voxel (x0 = W-1) has no bin of base x0+1: bin_start[rb + 3] is past
-        // its row (at the end of the array: never written), so its range ends at s2
-        const uint32_t s0 = a.bin_start[rb], m1 = a.bin_start[rb + 1], m2 = a.bin_start[rb + 2];
-        const uint32_t s3 = two ? a.bin_start[rb + 3] : m2;
-#pragma unroll OPS3D_FDA_VALUE_UNROLL
-        for (uint32_t i = s0 + (uint32_t)dp; i < s3; i += NBP) {
-          const float4 st = a.sorted_stash[i];
-          const uint32_t row = a.sorted_row[i];
-          float tg[CPL];
-          load_global_elems<T, CPL>(go + (size_t)(row * (uint32_t)D) + j * CPL, tg);
-          const float wy = (r & 1) ? st.y : 1.f - st.y;
-          const float wz = (r >> 1) ? st.z : 1.f - st.z;
-          const float ayz = st.w * (wy * wz);
-          // base x0-1: (x0, dx=1); base x0: (x0, dx=0), (x0+1, dx=1); base x0+1: (x0+1, dx=0)
-          const bool lft = i < m1, ctr = i < m2;
-          const float fx = st.x, gx = 1.f - st.x;
-          const float aw0 = ayz * (lft ? fx : (ctr ? gx : 0.f));
-          const float aw1 = ayz * (lft ? 0.f : (ctr ? fx : gx));
+        for (int k = 0; k < kTileKPT; ++k) {
+          const int e = tid + k * NT;
+          en[k] = a.entries[c0 + (e < n ? e : 0)];
+        }
+        float4 st[kTileKPT];   // unconditional loads (entry 0 stands in for absent ones): no scratch
 #pragma unroll
-          for (int c = 0; c < CPL; ++c) {
-            acc0[c] = fmaf(aw0, tg[c], acc0[c]);
-            acc1[c] = fmaf(aw1, tg[c], acc1[c]);
+        for (int k = 0; k < kTileKPT; ++k) st[k] = a.stash[en[k].x];
+#pragma unroll
+        for (int k = 0; k < kTileKPT; ++k) {
+          const int e = tid + k * NT;
+          if (e < n) {
+            const uint32_t w = en[k].y;
+            const uint32_t lb = ((w >> 10) & 31u) * (uint32_t)TYp * (uint32_t)TXp +
+                                ((w >> 5) & 31u) * (uint32_t)TXp + (w & 31u);
+            lbin_l[e] = (uint16_t)lb;
+            st_l[e] = st[k];
+            rowi_l[e] = (uint32_t)(((double)en[k].x + 0.5) * a.inv_lk);   // sample / (L*K), exact
+            atomicAdd(&cur_l[lb], 1u);
           }
         }
       }
-    }
+      __syncthreads();
+      TILE_MARK(1);
+      // 1b. grad_output rows into LDS, 16-byte pieces spread over all threads (loads first)
+      {
+        constexpr int PPR = RB / 16;                 // pieces per row
+        const int np = n * PPR;
+        for (int i0 = 0; i0 < np; i0 += 4 * NT) {
+          u32x4 v[4];
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      acc0[c] = bin_group_sum<LPU, NBP>(acc0[c]);
-      acc1[c] = bin_group_sum<LPU, NBP>(acc1[c]);
+          for (int k = 0; k < 4; ++k) {
+            const int i = min(i0 + k * NT + tid, np - 1);
+            const int e = i / PPR, q = i - e * PPR;
+            v[k] = reinterpret_cast<const u32x4 *>(go + (size_t)rowi_l[e] * (uint32_t)D)[q];
+          }
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const int i = i0 + k * NT + tid;
+            if (i < np) reinterpret_cast<u32x4 *>(row_l)[i] = v[k];
+          }
+        }
+      }
+      // 2. bin starts: thread tid scans bins [tid*per, (tid+1)*per)
+      {
+        const int per = (nb + NT - 1) / NT;
+        const int b0 = tid * per;
+        uint32_t sum = 0;
+        for (int i = 0; i < per; ++i)
+          if (b0 + i < nb) sum += cur_l[b0 + i];
+        uint32_t run = block_exclusive_scan_tile<NT>(sum, scan_tmp);
+        for (int i = 0; i < per; ++i)
+          if (b0 + i < nb) {
+            const uint32_t c = cur_l[b0 + i];
+            start_l[b0 + i] = run;
+            cur_l[b0 + i] = run;
+            run += c;
+          }
+        if (tid == NT - 1) start_l[nb] = (uint32_t)n;
+      }
+      __syncthreads();
+      TILE_MARK(2);
+      // 3. counting sort by bin
+      for (int e = tid; e < n; e += NT) {
+        const uint32_t pos = atomicAdd(&cur_l[lbin_l[e]], 1u);
+        sorted_l[pos] = (uint16_t)e;
+      }
+      __syncthreads();
+      TILE_MARK(3);
+      // 4. owners gather from LDS
+      if (live) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int dz = r >> 1, dy = r & 1;
+          // bins of base (x0-1, x0, x0+1) at (y-dy, z-dz): local +1-shifted x index 2*px
+          const int rb = ((pz - dz + 1) * TYp + (py - dy + 1)) * TXp + 2 * px;
+          const uint32_t s0 = start_l[rb], m1 = start_l[rb + 1], m2 = start_l[rb + 2];
+          const uint32_t s3 = two ? start_l[rb + 3] : m2;
+#pragma unroll 2
+          for (uint32_t i = s0; i < s3; ++i) {
+            const int slot = sorted_l[i];
+            const float4 st = st_l[slot];
+            uint32_t wv[NW];
+            const uint32_t *rw = reinterpret_cast<const uint32_t *>(row_l + (size_t)slot * RB + j * EB);
+#pragma unroll
+            for (int q = 0; q < NW; ++q) wv[q] = rw[q];
+            float tg[CPL];
+#pragma unroll
+            for (int q = 0; q < NW; ++q) Elem<T>::unpack(wv[q], tg + q * Elem<T>::kPerWord);
+            const float wy = dy ? st.y : 1.f - st.y;
+            const float wz = dz ? st.z : 1.f - st.z;
+            const float ayz = st.w * (wy * wz);
+            // base x0-1: (x0, dx=1); base x0: (x0, dx=0), (x0+1, dx=1); base x0+1: (x0+1, dx=0)
+            const bool lft = i < m1, ctr = i < m2;
+            const float fx = st.x, gx = 1.f - st.x;
+            const float aw0 = ayz * (lft ? fx : (ctr ? gx : 0.f));
+            const float aw1 = ayz * (lft ? 0.f : (ctr ? fx : gx));
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+              acc0[c] = fmaf(aw0, tg[c], acc0[c]);
+              acc1[c] = fmaf(aw1, tg[c], acc1[c]);
+            }
+          }
+        }
+      }
+      __syncthreads();
+      TILE_MARK(4);
     }
-    if (live && dp < 2) {   // lane group 0 stores x0, group 1 stores x0 + 1
-      const uint32_t x = x0 + (uint32_t)dp;
-      if (x < (uint32_t)Wl) {
-        const int64_t o = obase + (int64_t)((z * (uint32_t)Hl + y) * (uint32_t)Wl + x) * GD;
+    if (live) {
+      const int64_t vox = a.lsi[l] + ((int64_t)z * Hl + y) * Wl + x0;
+      const int64_t o = (((int64_t)b * a.S + vox) * G + g) * D + j * CPL;
+      for (int h = 0; h < (two ? 2 : 1); ++h) {
         float res[CPL];
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) res[c] = dp == 0 ? acc0[c] : acc1[c];
+        for (int c = 0; c < CPL; ++c) res[c] = h ? acc1[c] : acc0[c];
+        const int64_t oh = o + (int64_t)h * G * D;
         if (a.accumulate) {   // caller-owned fp32 buffer: add to what it holds (sole owner, no atomics)
-          float *dst = static_cast<float *>(a.out) + o;
+          float *dst = static_cast<float *>(a.out) + oh;
           float old[CPL];
           load_global_elems<float, CPL>(dst, old);
 #pragma unroll
           for (int c = 0; c < CPL; ++c) res[c] += old[c];
           store_elems<float, CPL>(dst, res);
         } else {
-          store_elems<T, CPL>(static_cast<T *>(a.out) + o, res);
+          store_elems<T, CPL>(static_cast<T *>(a.out) + oh, res);
         }
       }
     }
+    TILE_MARK(5);
   }
+#if OPS3D_FDA_TILE_TIMING
+  if (tid == 0 && a.dbg)
+    for (int i = 0; i < 6; ++i) atomicAdd(a.dbg + i, t_acc[i]);
+#endif
+#undef TILE_MARK
 }
 
-// which: 0 forward, 1 backward phase 1 (query-major), 2 backward phase 3 (voxel-major)
+// which: 0 forward, 1 backward phase 1 (query-major), 2 backward phase 3 (tile-major)
 template <typename T, int CPL, int LPU>
 hipError_t launch_one(int which, const Args &a, unsigned grid, size_t lds, hipStream_t st) {
   if (which == 0) {
@@ -564,8 +691,18 @@ hipError_t launch_one(int which, const Args &a, unsigned grid, size_t lds, hipSt
   }
   else if (which == 1)
     hipLaunchKernelGGL((fda_bwd_query_kernel<T, CPL, LPU>), dim3(grid), dim3(kBlock), lds, st, a);
-  else
-    hipLaunchKernelGGL((fda_bwd_value_kernel<T, CPL, LPU>), dim3(grid), dim3(kBlock), 0, st, a);
+  else {
+    // persistent: `grid` (the CU count, a multiple of 8 with XCD affinity) times the blocks that
+    // fit on a CU at once
+    // tile lanes per x-pair: half of LPU, twice the channels per lane
+    constexpr int TL = tile_lanes(LPU, CPL * (int)sizeof(T)), TC = CPL * LPU / TL;
+    int occ = 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fda_bwd_tile_kernel<T, TC, TL>, tile_threads(TL), lds) !=
+            hipSuccess || occ < 1)
+      occ = 1;
+    hipLaunchKernelGGL((fda_bwd_tile_kernel<T, TC, TL>), dim3(grid * (unsigned)occ), dim3(tile_threads(TL)), lds, st,
+                       a);
+  }
   return hipGetLastError();
 }
 

@@ -1,0 +1,209 @@
+// Phase 2 of the backward: group the samples' entries by spatial tile, gfx950.
+//
+// Every sample inside the volume has a home tile (key) and a tile-local word (fda_device.h,
+// tile_word); it is listed in its home tile and in the next tile along each axis whose flag is
+// set, 1 to 8 entries.  Three kernels and a scan:
+//   tile_clear:   zero the per-tile counters,
+//   tile_count:   per block, a contiguous range of one head's samples (about 64 blocks per
+//                 head); an LDS histogram over all of the head's tiles, flushed with one global
+//                 atomic per touched tile (a head with more than kWin tiles counts straight
+//                 into global atomics: correct, slower),
+//   tile_scan:    one block: exclusive scan of the counters -> tile_start, tile_cursor,
+//   tile_scatter: the same histogram again, then one global atomic per touched tile reserves
+//                 the block's range of that tile, and LDS atomics rank the entries inside it.
+// The order of entries inside a tile depends on the order in which blocks reserve; the tile
+// kernel's sums are fp32 and so depend on that order at the rounding level.
+#include "fda_device.h"
+
+namespace ops3d_fda {
+
+constexpr int kBucketThreads = 1024;
+constexpr int kWin = 16384;                           // LDS histogram window (tiles of one head)
+constexpr int kBlocksPerHead = 64;
+
+struct BucketArgs {
+  const uint32_t *keys;        // [N] home tile id or kKeyInvalid
+  const uint32_t *words;       // [N] home tile-local word (+ next-tile flags, level)
+  uint32_t n;                  // samples
+  uint32_t per_head;           // samples per (b, g) = Q * L * K
+  uint32_t chunk;              // samples per block (a block never spans two heads)
+  uint32_t blocks_per_head;
+  const int64_t *shapes;
+  int L, BG, TX, TY, TZ;
+  uint32_t *counts;            // [BG * T_h]
+  uint32_t *cursor;            // [BG * T_h]
+  uint2 *entries;              // [<= 8N]
+};
+
+struct LevelGrid {
+  uint32_t sy, sz;             // tile-id strides of the level's tile grid (y: ntx, z: ntx*nty)
+};
+
+__device__ __forceinline__ void level_grids(const BucketArgs &a, LevelGrid *lg) {
+  for (int l = 0; l < a.L; ++l) {
+    const LevelTiles lt = level_tiles(a.shapes, l, a.TX, a.TY, a.TZ);
+    lg[l].sy = (uint32_t)lt.nt[2];
+    lg[l].sz = (uint32_t)lt.nt[2] * (uint32_t)lt.nt[1];
+  }
+}
+
+// Calls f(tile id, tile-local word) for each entry of sample (key, word).
+template <typename F>
+__device__ __forceinline__ void for_each_entry(uint32_t key, uint32_t word, const LevelGrid *lg, F &&f) {
+  const uint32_t ex = (word >> 15) & 1u, ey = (word >> 16) & 1u, ez = (word >> 17) & 1u;
+  const LevelGrid g = lg[word >> 18];
+  const uint32_t base = word & 0x7fffu;
+  for (uint32_t dz = 0; dz <= ez; ++dz)
+    for (uint32_t dy = 0; dy <= ey; ++dy)
+      for (uint32_t dx = 0; dx <= ex; ++dx) {
+        // in the next tile along an axis the base corner is at local -1 (stored as 0)
+        uint32_t w = base;
+        if (dx) w &= ~0x1fu;
+        if (dy) w &= ~(0x1fu << 5);
+        if (dz) w &= ~(0x1fu << 10);
+        f(key + dx + dy * g.sy + dz * g.sz, w);
+      }
+}
+
+__global__ __launch_bounds__(1024) void tile_clear_kernel(uint32_t *counts, const int64_t *shapes, int L, int BG,
+                                                         int TX, int TY, int TZ) {
+  const uint32_t total = (uint32_t)BG * tiles_per_head(shapes, L, TX, TY, TZ);
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) counts[i] = 0u;
+}
+
+// Block -> its head and sample range [s0, s1).
+__device__ __forceinline__ void block_range(const BucketArgs &a, uint32_t &bg, uint32_t &s0, uint32_t &s1) {
+  bg = blockIdx.x / a.blocks_per_head;
+  const uint32_t c = blockIdx.x - bg * a.blocks_per_head;
+  const uint32_t h0 = bg * a.per_head;
+  s0 = h0 + min(c * a.chunk, a.per_head);
+  s1 = h0 + min((c + 1) * a.chunk, a.per_head);
+}
+
+__global__ __launch_bounds__(kBucketThreads) void tile_count_kernel(const BucketArgs a) {
+  extern __shared__ uint32_t win[];   // [kWin]
+  __shared__ LevelGrid lg[5];
+  const uint32_t T_h = tiles_per_head(a.shapes, a.L, a.TX, a.TY, a.TZ);
+  const uint32_t nw = min(T_h, (uint32_t)kWin);
+  if (threadIdx.x == 0) level_grids(a, lg);
+  for (uint32_t i = threadIdx.x; i < nw; i += kBucketThreads) win[i] = 0u;
+  __syncthreads();
+  uint32_t bg, s0, s1;
+  block_range(a, bg, s0, s1);
+  const uint32_t w0 = bg * T_h;
+#pragma unroll 2
+  for (uint32_t s = s0 + threadIdx.x; s < s1; s += kBucketThreads) {
+    const uint32_t key = a.keys[s];
+    if (key == kKeyInvalid) continue;
+    for_each_entry(key, a.words[s], lg, [&](uint32_t id, uint32_t) {
+      if (id - w0 < nw) atomicAdd(&win[id - w0], 1u);
+      else atomicAdd(&a.counts[id], 1u);
+    });
+  }
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < nw; i += kBucketThreads)
+    if (win[i]) atomicAdd(&a.counts[w0 + i], win[i]);
+}
+
+__global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const BucketArgs a) {
+  extern __shared__ uint32_t win[];   // [kWin] counts, then the block's first position in each tile
+  uint32_t *rk = win + kWin;          // [kWin] rank counters
+  __shared__ LevelGrid lg[5];
+  const uint32_t T_h = tiles_per_head(a.shapes, a.L, a.TX, a.TY, a.TZ);
+  const uint32_t nw = min(T_h, (uint32_t)kWin);
+  if (threadIdx.x == 0) level_grids(a, lg);
+  for (uint32_t i = threadIdx.x; i < nw; i += kBucketThreads) {
+    win[i] = 0u;
+    rk[i] = 0u;
+  }
+  __syncthreads();
+  uint32_t bg, s0, s1;
+  block_range(a, bg, s0, s1);
+  const uint32_t w0 = bg * T_h;
+  // pass A: counts of the window's tiles
+#pragma unroll 2
+  for (uint32_t s = s0 + threadIdx.x; s < s1; s += kBucketThreads) {
+    const uint32_t key = a.keys[s];
+    if (key == kKeyInvalid) continue;
+    for_each_entry(key, a.words[s], lg, [&](uint32_t id, uint32_t) {
+      if (id - w0 < nw) atomicAdd(&win[id - w0], 1u);
+    });
+  }
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < nw; i += kBucketThreads)
+    if (win[i]) win[i] = atomicAdd(&a.cursor[w0 + i], win[i]);
+  __syncthreads();
+  // pass B: place the entries
+#pragma unroll 2
+  for (uint32_t s = s0 + threadIdx.x; s < s1; s += kBucketThreads) {
+    const uint32_t key = a.keys[s];
+    if (key == kKeyInvalid) continue;
+    for_each_entry(key, a.words[s], lg, [&](uint32_t id, uint32_t w) {
+      uint32_t pos;
+      if (id - w0 < nw) pos = win[id - w0] + atomicAdd(&rk[id - w0], 1u);
+      else pos = atomicAdd(&a.cursor[id], 1u);
+      a.entries[pos] = make_uint2(s, w);
+    });
+  }
+}
+
+// One block of 1024 threads: tile_start = exclusive scan of counts (and its total at the end),
+// cursor = tile_start.
+__global__ __launch_bounds__(1024) void tile_scan_kernel(const uint32_t *counts, uint32_t *start, uint32_t *cursor,
+                                                        const int64_t *shapes, int L, int BG, int TX, int TY,
+                                                        int TZ) {
+  __shared__ uint32_t tmp[16];
+  const uint32_t total = (uint32_t)BG * tiles_per_head(shapes, L, TX, TY, TZ);
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+  uint32_t carry = 0;
+  for (uint32_t base = 0; base < total; base += 1024) {
+    const uint32_t i = base + threadIdx.x;
+    const uint32_t x = i < total ? counts[i] : 0u;
+    uint32_t inc = x;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const uint32_t y = __shfl_up(inc, o, kWave);
+      if (lane >= o) inc += y;
+    }
+    if (lane == kWave - 1) tmp[w] = inc;
+    __syncthreads();
+    uint32_t wofs = 0, all = 0;
+    for (int ww = 0; ww < 16; ++ww) {
+      if (ww < w) wofs += tmp[ww];
+      all += tmp[ww];
+    }
+    __syncthreads();
+    if (i < total) {
+      const uint32_t v = carry + wofs + inc - x;
+      start[i] = v;
+      cursor[i] = v;
+    }
+    carry += all;
+  }
+  if (threadIdx.x == 0) start[total] = carry;
+}
+
+hipError_t launch_tile_bucketing(const uint32_t *keys, const uint32_t *words, uint32_t n, uint32_t per_head,
+                                 const int64_t *shapes, int L, int BG, int TX, int TY, int TZ, uint32_t *counts,
+                                 uint32_t *start, uint32_t *cursor, uint2 *entries, hipStream_t st,
+                                 void (*mark)(int, hipStream_t)) {
+  hipLaunchKernelGGL(tile_clear_kernel, dim3(64), dim3(1024), 0, st, counts, shapes, L, BG, TX, TY, TZ);
+  BucketArgs a{};
+  a.keys = keys; a.words = words; a.n = n; a.per_head = per_head; a.shapes = shapes;
+  a.L = L; a.BG = BG; a.TX = TX; a.TY = TY; a.TZ = TZ;
+  a.counts = counts; a.cursor = cursor; a.entries = entries;
+  // about kBlocksPerHead blocks per head, each a whole number of kBucketThreads-sample steps
+  a.blocks_per_head = kBlocksPerHead;
+  a.chunk = (per_head + kBlocksPerHead - 1) / kBlocksPerHead;
+  a.chunk = (a.chunk + kBucketThreads - 1) / kBucketThreads * kBucketThreads;
+  if (a.chunk == 0) a.chunk = kBucketThreads;
+  a.blocks_per_head = (per_head + a.chunk - 1) / a.chunk;
+  const unsigned blocks = n > 0 ? (unsigned)BG * a.blocks_per_head : 0u;
+  if (blocks > 0) hipLaunchKernelGGL(tile_count_kernel, dim3(blocks), dim3(kBucketThreads), kWin * 4, st, a);
+  hipLaunchKernelGGL(tile_scan_kernel, dim3(1), dim3(1024), 0, st, counts, start, cursor, shapes, L, BG, TX, TY, TZ);
+  if (mark) mark(3, st);
+  if (blocks > 0) hipLaunchKernelGGL(tile_scatter_kernel, dim3(blocks), dim3(kBucketThreads), kWin * 8, st, a);
+  return hipGetLastError();
+}
+
+}  // namespace ops3d_fda

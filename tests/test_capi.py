@@ -50,12 +50,6 @@ def test_abi_version_and_support_table(lib):
     assert lib.ops3d_fda_supported(9, 32) == 0
 
 
-def _has_device():
-    import torch
-
-    return torch.cuda.is_available()
-
-
 def test_forward_workspace_bytes(lib):
     assert lib.ops3d_fda_forward_workspace_bytes(2, 1, 73728, 8, 32) == 73728 * 8 * 32 * 2
     assert lib.ops3d_fda_forward_workspace_bytes(2, 1, 73728, 1, 32) == 0  # G == 1: already head-major
@@ -63,16 +57,18 @@ def test_forward_workspace_bytes(lib):
 
 
 def test_workspace_bytes(lib):
-    n = 73728 * 8 * 8  # c4 samples
-    ws = lib.ops3d_fda_backward_workspace_bytes(2, 1, 73728, 8, 32, 2, 73728, 4)
-    if not _has_device():
-        # the radix sort sizes its temporary storage for the device it will run on
-        assert ws == 0
-        return
-    # 4 index arrays + stash + bin starts (<= 8*B*G*S + 1) + sort temporary storage
-    assert ws >= n * (4 * 4 + 16) + (8 * 8 * 73728 + 1) * 4
-    assert ws < n * (4 * 4 + 16) * 3
-    assert lib.ops3d_fda_backward_workspace_bytes(9, 1, 73728, 8, 32, 2, 73728, 4) == 0
+    B, S, G, D, L, Q, K = 1, 73728, 8, 32, 2, 73728, 4   # c4
+    n = B * Q * G * L * K
+
+    def al(x):
+        return (x + 255) // 256 * 256
+
+    # keys, words, stash, <= 8 entries per sample, 3 tile arrays of B*G*S+1 words, head-major
+    # copies of value and grad_output
+    want = (2 * al(4 * n) + al(16 * n) + al(64 * n) + 3 * al(4 * (B * G * S + 1)) + al(B * S * G * D * 2)
+            + al(B * Q * G * D * 2))
+    assert lib.ops3d_fda_backward_workspace_bytes(2, B, S, G, D, L, Q, K) == want
+    assert lib.ops3d_fda_backward_workspace_bytes(9, B, S, G, D, L, Q, K) == 0
 
 
 def _fwd(lib, **kw):
@@ -100,10 +96,7 @@ def test_argument_errors_before_device_work(lib):
 def test_backward_workspace_check(lib):
     p = ctypes.c_void_p(256)
     rc = lib.ops3d_fda_backward(p, p, p, p, p, p, p, None, 0, 2, 1, 576, 8, 32, 2, 576, 4, 64, None)
-    if _has_device():
-        assert rc == 1 and b"workspace too small" in lib.ops3d_fda_last_error()
-    else:
-        assert rc == 2 and b"bin sort" in lib.ops3d_fda_last_error()
+    assert rc == 1 and b"workspace too small" in lib.ops3d_fda_last_error()
     # argument errors are still reported before anything else
     rc = lib.ops3d_fda_backward(p, p, p, p, p, p, p, None, 0, 2, 1, 576, 8, 32, 6, 576, 4, 64, None)
     assert rc == 1 and b"invalid number of scales" in lib.ops3d_fda_last_error()

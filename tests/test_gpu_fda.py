@@ -193,13 +193,19 @@ def test_im2col_step_invariance_and_determinism(gpu_device):
         assert torch.equal(o, outs[0])
 
 
-def test_backward_deterministic(gpu_device):
-    """grad_value is a sorted gather: bitwise identical across runs (the reference's atomic
-    scatter is not)."""
+def test_backward_repeatable(gpu_device):
+    """grad_sampling_loc_attn is bitwise identical across runs.  grad_value rows are fp32 sums
+    whose order follows the order in which blocks fill a tile's entry list, so runs may differ
+    by fp32 rounding of the sums (relative to the sum of the terms' magnitudes, ~1 here), seen
+    after the bf16 rounding as one bf16 ulp, or a few ulps of a row that nearly cancels."""
     inp = random_inputs([(8, 8, 8), (4, 4, 4)], 2, 500, 8, 32, 4, torch.bfloat16, seed=11)
     a = run_gpu(inp, gpu_device)
     b = run_gpu(inp, gpu_device)
-    assert torch.equal(a[1], b[1]) and torch.equal(a[2], b[2])
+    assert torch.equal(a[2], b[2])
+    ga, gb = a[1].float(), b[1].float()
+    tol = torch.maximum(ga.abs(), gb.abs()) * 2.0 ** -7 + 1e-5   # >= one bf16 ulp of either
+    d = (ga - gb).abs()
+    assert (d <= tol).all(), f"max diff {d.max().item():.3e} at |g| {ga.flatten()[d.argmax()].item():.3e}"
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
