@@ -205,7 +205,10 @@ int tile_chunk(int D, int e, int lpu) {
   const int rb = D * e;
   const int nt = tile_threads(lpu);
   const size_t bins = tile_kernel_lds_bytes(0, rb, lpu);
-  const size_t budget = (nt >= 1024 ? 150 : (nt >= 512 ? 76 : 50)) * (size_t)1024;
+#ifndef OPS3D_FDA_TILE_LDS_KB_256
+#define OPS3D_FDA_TILE_LDS_KB_256 50
+#endif
+  const size_t budget = (nt >= 1024 ? 150 : (nt >= 512 ? 76 : OPS3D_FDA_TILE_LDS_KB_256)) * (size_t)1024;
   if (budget <= bins) return 0;
   int ch = (int)((budget - bins) / (size_t)(rb + 24));
   ch = ch > kTileKPT * nt ? kTileKPT * nt : ch;

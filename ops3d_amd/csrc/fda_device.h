@@ -472,10 +472,10 @@ __device__ __forceinline__ SampleBase unit_bcast(const SampleBase &sb) {
 }
 
 // LDS floats per unit of the backward query kernel (record, grad_attn, 16-byte-aligned stash,
-// tile keys and tile-local words); the block uses UPB times this.  Rounded to 4 x an odd number so that the units of
+// base corner x, y, z); the block uses UPB times this.  Rounded to 4 x an odd number so that the units of
 // a wave start in different LDS banks.
 __host__ __device__ constexpr int bwd_query_lds_floats(int P, int LK) {
-  return ((((((P + LK + 3) & ~3) + 6 * LK) + 3) / 4) | 1) * 4;
+  return ((((((P + LK + 3) & ~3) + 7 * LK) + 3) / 4) | 1) * 4;
 }
 
 // Sample numbering of the backward, head-major so that one block's samples are

@@ -275,15 +275,27 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
   const int q = qb * UPB + ub;
   const bool live = q < a.Q;
   const int L = a.L, K = a.K, LK = L * K, P = a.P;
-  // per unit: [0,P) record (later its gradient), [P,P+LK) grad_attn, then LK stash float4s,
-  // LK tile keys and LK tile-local words for the wave's coalesced write-out
+  // per unit: [0,P) record (later its gradient), [P,P+LK) grad_attn, then LK stash float4s and
+  // the LK base corners (x0+1 or kKeyInvalid, y0+1, z0+1) for the wave's coalesced write-out
   const int RS = bwd_query_lds_floats(P, LK);
   float *rec = lds + ub * RS;
   float *gat_s = rec + P;
   float4 *st_s = reinterpret_cast<float4 *>(lds + ub * RS + ((P + LK + 3) & ~3));
-  uint32_t *key_s = reinterpret_cast<uint32_t *>(st_s + LK);
-  uint32_t *word_s = key_s + LK;
+  uint32_t *cx_s = reinterpret_cast<uint32_t *>(st_s + LK);
+  uint32_t *cy_s = cx_s + LK, *cz_s = cy_s + LK;
   const int64_t unit = ((int64_t)b * a.Q + (live ? q : 0)) * a.G + g;
+  // per level: tile geometry and the id of the level's first tile of this (b, g)
+  __shared__ LevelTiles lvt[5];
+  __shared__ uint32_t lvbase[5];
+  if (threadIdx.x == 0) {
+    uint32_t t = (uint32_t)(b * a.G + g) * tiles_per_head(a.shapes, L, a.TX, a.TY, a.TZ);
+    for (int l = 0; l < L; ++l) {
+      lvt[l] = level_tiles(a.shapes, l, a.TX, a.TY, a.TZ);
+      lvbase[l] = t;
+      t += lvt[l].count;
+    }
+  }
+  __syncthreads();
 
   stage_record<T, LPU>(static_cast<const T *>(a.loc_attn) + unit * P, P, j, live, rec);
   wave_lds_sync();
@@ -301,9 +313,6 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
     for (int c = 0; c < NW; ++c) tgw[c] = 0u;
   }
 
-  // tile ids of this (b, g): bg * T_h + (tiles of the earlier levels) + tile within the level
-  uint32_t tile_base = (uint32_t)(b * a.G + g) * tiles_per_head(a.shapes, L, a.TX, a.TY, a.TZ);
-
   const int RST = a.vhm ? a.D : a.G * a.D;
   const uint32_t lane_elem = (uint32_t)((a.vhm ? 0 : g * a.D) + j * CPL);
   const T *vb = static_cast<const T *>(a.value) +
@@ -314,7 +323,6 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
     const int64_t st = a.lsi[l];
     const int64_t nel = (int64_t)Dl * Hl * Wl * RST;
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb + st * RST, (uint32_t)(nel * (int64_t)sizeof(T)));
-    const LevelTiles lt = level_tiles(a.shapes, l, a.TX, a.TY, a.TZ);
     // two samples per step: both records are read before either gradient is written back, so
     // the 16 corner loads of the pair are in flight together
     for (int k = 0; k < K; k += 2, s += 2) {
@@ -373,21 +381,14 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
           rec[3 * su + 1] = gy * at[u] * (float)Hl;
           rec[3 * su + 2] = gz * at[u] * (float)Dl;
           gat_s[su] = ga;
-          // home tile: the tile holding corner (max(x0,0), max(y0,0), max(z0,0)); the sample
-          // is also listed in the next tile along an axis where x0 is the tile's last voxel
-          const int hz = max(m.z0, 0) >> lt.sh[0], hy = max(m.y0, 0) >> lt.sh[1], hx = max(m.x0, 0) >> lt.sh[2];
-          const int lz = m.z0 - hz * lt.t[0], ly = m.y0 - hy * lt.t[1], lx = m.x0 - hx * lt.t[2];
-          const uint32_t ex = lx == lt.t[2] - 1 && (hx + 1) * lt.t[2] < Wl;
-          const uint32_t ey = ly == lt.t[1] - 1 && (hy + 1) * lt.t[1] < Hl;
-          const uint32_t ez = lz == lt.t[0] - 1 && (hz + 1) * lt.t[0] < Dl;
-          key_s[su] = in[u] ? tile_base + (uint32_t)((hz * lt.nt[1] + hy) * lt.nt[2] + hx) : kKeyInvalid;
-          word_s[su] = tile_word(lx, ly, lz) | (ex << 15) | (ey << 16) | (ez << 17) | ((uint32_t)l << 18);
+          cx_s[su] = in[u] ? (uint32_t)(m.x0 + 1) : kKeyInvalid;
+          cy_s[su] = (uint32_t)(m.y0 + 1);
+          cz_s[su] = (uint32_t)(m.z0 + 1);
           st_s[su] = make_float4(m.wx[1], m.wy[1], m.wz[1], at[u]);
         }
       }
     }
     s += K - ((K + 1) & ~1);   // the steps above advanced s by K rounded up to even
-    tile_base += lt.count;
   }
   wave_lds_sync();
   {
@@ -402,8 +403,20 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
         const int ubx = wave * UPW + uu;
         const float4 *stx = reinterpret_cast<const float4 *>(lds + ubx * RS + ((P + LK + 3) & ~3));
         const uint32_t *kx = reinterpret_cast<const uint32_t *>(stx + LK);
-        a.keys[gs0 + e] = kx[ss];
-        a.vals[gs0 + e] = kx[LK + ss];
+        // home tile: the tile holding corner (max(x0,0), max(y0,0), max(z0,0)); the sample is
+        // also listed in the next tile along an axis where its base corner is the tile's last
+        // voxel (flags in the tile-local word)
+        const int l = ss / K;
+        const LevelTiles &lt = lvt[l];
+        const uint32_t bx = kx[ss];
+        const int x0 = (int)bx - 1, y0 = (int)kx[LK + ss] - 1, z0 = (int)kx[2 * LK + ss] - 1;
+        const int hz = max(z0, 0) >> lt.sh[0], hy = max(y0, 0) >> lt.sh[1], hx = max(x0, 0) >> lt.sh[2];
+        const int lz = z0 - hz * lt.t[0], ly = y0 - hy * lt.t[1], lx = x0 - hx * lt.t[2];
+        const uint32_t ex = lx == lt.t[2] - 1 && (hx + 1) * lt.t[2] < lt.n[2];
+        const uint32_t ey = ly == lt.t[1] - 1 && (hy + 1) * lt.t[1] < lt.n[1];
+        const uint32_t ez = lz == lt.t[0] - 1 && (hz + 1) * lt.t[0] < lt.n[0];
+        a.keys[gs0 + e] = bx == kKeyInvalid ? kKeyInvalid : lvbase[l] + (uint32_t)((hz * lt.nt[1] + hy) * lt.nt[2] + hx);
+        a.vals[gs0 + e] = tile_word(lx, ly, lz) | (ex << 15) | (ey << 16) | (ez << 17) | ((uint32_t)l << 18);
         a.stash[gs0 + e] = stx[ss];
       }
     }
