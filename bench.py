@@ -134,7 +134,9 @@ class Bench:
         _C.profile_enable(True)
         try:
             fwd = run(lambda: _C.flash_deform_attn_forward(v, self.st, self.lsi, s, 64, self.w.K), "forward")
-            bwd = run(lambda: _C.flash_deform_attn_backward(v, self.st, self.lsi, s, self.go, 64, self.w.K),
+            # as in FlashDeformAttnFunction: the backward reuses the forward's head-major value
+            _, vhm = _C.forward_keep_head_major(v, self.st, self.lsi, s, 64, self.w.K)
+            bwd = run(lambda: _C.backward_with_head_major(v, vhm, self.st, self.lsi, s, self.go, 64, self.w.K),
                       "backward")
         finally:
             _C.profile_enable(False)

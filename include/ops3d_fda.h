@@ -108,6 +108,22 @@ OPS3D_FDA_API int ops3d_fda_backward(const void *value, const int64_t *spatial_s
                        void *stream);
 
 /*
+ * Backward with the head-major copy of value the forward already made.  Same as
+ * ops3d_fda_backward, plus value_head_major: NULL, or the [B,G,S,D] copy of value that
+ * ops3d_fda_forward left in its workspace (its first B*S*G*D elements) for the same value, so
+ * the backward does not make it again.  Ignored when G == 1.  No counterpart in the reference
+ * (its backward re-reads value, flash_deform_attn_cuda.cu:93-179); for autograd functions that
+ * keep the forward workspace until the backward.
+ */
+OPS3D_FDA_API int ops3d_fda_backward_ex(const void *value, const void *value_head_major,
+                       const int64_t *spatial_shapes, const int64_t *level_start_index,
+                       const void *sampling_loc_attn, const void *grad_output, void *grad_value,
+                       void *grad_sampling_loc_attn, void *workspace, size_t workspace_bytes,
+                       int dtype, int batch, int spatial_size, int num_heads, int channels,
+                       int num_levels, int num_query, int num_point, int im2col_step,
+                       void *stream);
+
+/*
  * Backward that ADDS the value gradient into a caller-owned fp32 buffer grad_value_f32
  * ([B,S,G,D] fp32, not cleared) instead of writing it in `dtype`; grad_sampling_loc_attn is
  * written in full in `dtype`.  Same workspace as ops3d_fda_backward.  No counterpart in the

@@ -36,6 +36,7 @@ EXPORTED_SYMBOLS = (
     "ops3d_fda_forward",
     "ops3d_fda_backward_workspace_bytes",
     "ops3d_fda_backward",
+    "ops3d_fda_backward_ex",
     "ops3d_fda_backward_accumulate_f32",
     "ops3d_fda_profile_enable",
     "ops3d_fda_profile_read",
@@ -57,6 +58,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ops3d_fda_backward_workspace_bytes.argtypes = [_i] * 8
     lib.ops3d_fda_backward.restype = _i
     lib.ops3d_fda_backward.argtypes = [_vp] * 8 + [_sz] + [_i] * 9 + [_vp]
+    lib.ops3d_fda_backward_ex.restype = _i
+    lib.ops3d_fda_backward_ex.argtypes = [_vp] * 9 + [_sz] + [_i] * 9 + [_vp]
     lib.ops3d_fda_profile_enable.restype = _i
     lib.ops3d_fda_profile_enable.argtypes = [_i]
     lib.ops3d_fda_profile_read.restype = _i
@@ -145,6 +148,12 @@ class _NativeFDA:
     ):
         """Forward; ``d_stride``, ``block_thread`` and ``use_reg`` are accepted and ignored
         (the gfx950 launch geometry is chosen by the library).  Returns [B, Q, G*D]."""
+        return self.forward_keep_head_major(value, spatial_shapes, level_start_index, sampling_loc_attn,
+                                            im2col_step, K)[0]
+
+    def forward_keep_head_major(self, value, spatial_shapes, level_start_index, sampling_loc_attn, im2col_step, K):
+        """Forward that also returns its workspace, which holds the head-major copy of value
+        (None when G == 1), for backward_with_head_major."""
         B, S, G, D, L, Q = self._common(value, spatial_shapes, level_start_index, sampling_loc_attn, K, {})
         out = torch.empty((B, Q, G * D), dtype=value.dtype, device=value.device)
         code = _DTYPE_CODE[value.dtype]
@@ -158,27 +167,39 @@ class _NativeFDA:
             )
         if rc != OPS3D_FDA_OK:
             self._raise(rc, "flash_deform_attn_forward failed")
-        return out
+        return out, ws
 
     def flash_deform_attn_backward(
         self, value, spatial_shapes, level_start_index, sampling_loc_attn, grad_output,
         im2col_step, K, d_stride=1, block_thread=0,
     ):
         """Backward; returns [grad_value, grad_sampling_loc_attn] in value's dtype."""
+        return self.backward_with_head_major(value, None, spatial_shapes, level_start_index, sampling_loc_attn,
+                                             grad_output, im2col_step, K)
+
+    def backward_with_head_major(
+        self, value, value_head_major, spatial_shapes, level_start_index, sampling_loc_attn, grad_output,
+        im2col_step, K,
+    ):
+        """Backward reusing ``value_head_major``, the workspace forward_keep_head_major returned
+        for this value (or None)."""
         B, S, G, D, L, Q = self._common(
             value, spatial_shapes, level_start_index, sampling_loc_attn, K, {"grad_output": grad_output}
         )
         if grad_output.numel() != B * Q * G * D:
             raise ValueError(f"grad_output must have B*Q*G*D = {B * Q * G * D} elements, got {grad_output.numel()}")
+        if value_head_major is not None and (value_head_major.device != value.device
+                                             or value_head_major.numel() < value.numel() * value.element_size()):
+            raise ValueError("value_head_major is not a forward workspace of this value")
         code = _DTYPE_CODE[value.dtype]
         grad_value = torch.empty_like(value)
         grad_sla = torch.empty_like(sampling_loc_attn)
         ws, ws_bytes = self._workspace(code, B, S, G, D, L, Q, K, value.device)
         stream = torch.cuda.current_stream(value.device).cuda_stream
         with torch.cuda.device(value.device):
-            rc = self._lib.ops3d_fda_backward(
-                _ptr(value), _ptr(spatial_shapes), _ptr(level_start_index), _ptr(sampling_loc_attn),
-                _ptr(grad_output), _ptr(grad_value), _ptr(grad_sla), _ptr(ws), ws_bytes,
+            rc = self._lib.ops3d_fda_backward_ex(
+                _ptr(value), _ptr(value_head_major), _ptr(spatial_shapes), _ptr(level_start_index),
+                _ptr(sampling_loc_attn), _ptr(grad_output), _ptr(grad_value), _ptr(grad_sla), _ptr(ws), ws_bytes,
                 code, B, S, G, D, L, Q, int(K), int(im2col_step), stream,
             )
         if rc != OPS3D_FDA_OK:

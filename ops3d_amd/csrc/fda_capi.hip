@@ -29,8 +29,9 @@ hipError_t launch_f16(int, int, int, const Args &, unsigned, size_t, hipStream_t
 hipError_t launch_bf16(int, int, int, const Args &, unsigned, size_t, hipStream_t);
 hipError_t launch_tile_bucketing(const uint32_t *keys, const uint32_t *words, uint32_t n, uint32_t per_head,
                                  const int64_t *shapes, int L, int BG, int TX, int TY, int TZ, uint32_t *counts,
-                                 uint32_t *start, uint32_t *cursor, uint2 *entries, hipStream_t st,
-                                 void (*mark)(int, hipStream_t));
+                                 uint32_t *start, uint32_t *cursor, uint32_t *mat, uint32_t tcap, uint2 *entries,
+                                 hipStream_t st, void (*mark)(int, hipStream_t));
+size_t tile_matrix_words(uint32_t BG, uint32_t tcap);
 }  // namespace ops3d_fda
 
 using namespace ops3d_fda;
@@ -166,10 +167,13 @@ hipError_t launch(int dtype, int which, const Geometry &g, hipStream_t st) {
 //   entries        : 8N uint2 (a sample is listed in at most 8 tiles)
 //   counts, start, cursor : B*G*S + 1 uint32 each (a tile holds at least one voxel, so a head
 //                    has at most S tiles)
+//   bucketing matrix: B*G x 64 blocks x tcap uint32, tcap = S/16 + 64 tiles per head (volumes
+//                    cut into more tiles are bucketed with global atomics instead)
 //   head-major copies of value and grad_output (G > 1)
 struct BwdLayout {
   uint64_t n, ntiles_bound;
-  size_t off_keys, off_words, off_stash, off_entries, off_counts, off_start, off_cursor, off_vhm, off_ghm;
+  uint32_t tcap;
+  size_t off_keys, off_words, off_stash, off_entries, off_counts, off_start, off_cursor, off_mat, off_vhm, off_ghm;
   size_t total;
 };
 
@@ -192,6 +196,8 @@ int bwd_layout(int B, int S, int G, int D, int e, int L, int Q, int K, BwdLayout
   ly.off_counts = o; o += t4;
   ly.off_start = o; o += t4;
   ly.off_cursor = o; o += t4;
+  ly.tcap = (uint32_t)(S / 16 + 64);
+  ly.off_mat = o; o += align256(tile_matrix_words((uint32_t)(B * G), ly.tcap) * 4);
   ly.off_vhm = o; o += G > 1 ? align256((size_t)B * S * G * D * e) : 0;
   ly.off_ghm = o; o += G > 1 ? align256((size_t)B * Q * G * D * e) : 0;
   ly.total = o;
@@ -330,7 +336,7 @@ size_t ops3d_fda_backward_workspace_bytes(int dtype, int batch, int spatial_size
   return ly.total;
 }
 
-static int backward_impl(const void *value, const int64_t *spatial_shapes,
+static int backward_impl(const void *value, const void *value_head_major, const int64_t *spatial_shapes,
                          const int64_t *level_start_index, const void *sampling_loc_attn,
                          const void *grad_output, void *grad_value, bool out_f32_accumulate,
                          void *grad_sampling_loc_attn, void *workspace, size_t workspace_bytes,
@@ -389,15 +395,17 @@ static int backward_impl(const void *value, const int64_t *spatial_shapes,
   hipError_t e;
   prof_mark(0, st);
   if (work && num_heads > 1) {
-    // head-major copies: one head's value rows / grad_output rows become contiguous
-    e = launch_head_major(value, ws + ly.off_vhm, batch, spatial_size, num_heads, channels, elem_size(dtype), st);
-    if (e == hipSuccess)
-      e = launch_head_major(grad_output, ws + ly.off_ghm, batch, num_query, num_heads, channels, elem_size(dtype), st);
-    if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "head-major copy failed: %s", hipGetErrorString(e));
-    a.value = ws + ly.off_vhm;
+    // head-major value (one head's rows contiguous): the caller's copy, or made here; the query
+    // kernel writes the head-major copy of grad_output as it reads it
+    if (value_head_major) {
+      a.value = value_head_major;
+    } else {
+      e = launch_head_major(value, ws + ly.off_vhm, batch, spatial_size, num_heads, channels, elem_size(dtype), st);
+      if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "head-major copy failed: %s", hipGetErrorString(e));
+      a.value = ws + ly.off_vhm;
+    }
     a.vhm = 1;
-    a.grad_out = ws + ly.off_ghm;
-    a.ghm = 1;
+    a.gout_hm = ws + ly.off_ghm;
   }
   prof_mark(1, st);
   if (work) {
@@ -412,7 +420,8 @@ static int backward_impl(const void *value, const int64_t *spatial_shapes,
   // kernel reads the tile ranges of every tile)
   e = launch_tile_bucketing(keys, words, work ? (uint32_t)ly.n : 0u,
                             (uint32_t)num_query * (uint32_t)(num_levels * num_point), spatial_shapes, num_levels,
-                            batch * num_heads, a.TX, a.TY, a.TZ, counts, tstart, cursor, entries, st,
+                            batch * num_heads, a.TX, a.TY, a.TZ, counts, tstart, cursor,
+                            reinterpret_cast<uint32_t *>(ws + ly.off_mat), ly.tcap, entries, st,
                             g_prof_on ? prof_mark : nullptr);
   if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "tile bucketing failed: %s", hipGetErrorString(e));
   prof_mark(4, st);
@@ -487,9 +496,24 @@ int ops3d_fda_backward(const void *value, const int64_t *spatial_shapes,
                        int num_levels, int num_query, int num_point, int im2col_step,
                        void *stream) {
   g_last_error.clear();
-  return backward_impl(value, spatial_shapes, level_start_index, sampling_loc_attn, grad_output, grad_value,
-                       false, grad_sampling_loc_attn, workspace, workspace_bytes, dtype, batch, spatial_size,
+  return backward_impl(value, nullptr, spatial_shapes, level_start_index, sampling_loc_attn, grad_output,
+                       grad_value, false, grad_sampling_loc_attn, workspace, workspace_bytes, dtype, batch, spatial_size,
                        num_heads, channels, num_levels, num_query, num_point, im2col_step,
+                       static_cast<hipStream_t>(stream));
+}
+
+int ops3d_fda_backward_ex(const void *value, const void *value_head_major, const int64_t *spatial_shapes,
+                          const int64_t *level_start_index, const void *sampling_loc_attn,
+                          const void *grad_output, void *grad_value, void *grad_sampling_loc_attn,
+                          void *workspace, size_t workspace_bytes, int dtype, int batch, int spatial_size,
+                          int num_heads, int channels, int num_levels, int num_query, int num_point,
+                          int im2col_step, void *stream) {
+  g_last_error.clear();
+  if (value_head_major && misaligned(value_head_major))
+    return fail(OPS3D_FDA_EINVAL, "value_head_major must be 4-byte aligned");
+  return backward_impl(value, value_head_major, spatial_shapes, level_start_index, sampling_loc_attn, grad_output,
+                       grad_value, false, grad_sampling_loc_attn, workspace, workspace_bytes, dtype, batch,
+                       spatial_size, num_heads, channels, num_levels, num_query, num_point, im2col_step,
                        static_cast<hipStream_t>(stream));
 }
 
@@ -501,7 +525,7 @@ int ops3d_fda_backward_accumulate_f32(const void *value, const int64_t *spatial_
                                       int spatial_size, int num_heads, int channels, int num_levels,
                                       int num_query, int num_point, int im2col_step, void *stream) {
   g_last_error.clear();
-  return backward_impl(value, spatial_shapes, level_start_index, sampling_loc_attn, grad_output,
+  return backward_impl(value, nullptr, spatial_shapes, level_start_index, sampling_loc_attn, grad_output,
                        grad_value_f32, true, grad_sampling_loc_attn, workspace, workspace_bytes, dtype, batch,
                        spatial_size, num_heads, channels, num_levels, num_query, num_point, im2col_step,
                        static_cast<hipStream_t>(stream));

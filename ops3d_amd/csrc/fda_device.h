@@ -55,7 +55,8 @@ struct Args {
   int tile_affinity;          // tiles of head g run on XCD g % 8 (G % 8 == 0)
   int accumulate;             // add into an fp32 grad_value instead of overwriting
   int vhm;                    // value is head-major [B,G,S,D] (a transposed copy)
-  int ghm;                    // grad_out is head-major [B,G,Q,D] (a transposed copy)
+  void *gout_hm;              // head-major copy [B,G,Q,D] of grad_out (G > 1): written by the
+                              // query kernel, read by the tile kernel
   double inv_lk;              // 1.0 / (L*K), for sample -> unit
   unsigned long long *dbg;    // tile kernel phase cycles (OPS3D_FDA_TILE_TIMING builds only)
   int B, S, G, D, L, K, Q, P;

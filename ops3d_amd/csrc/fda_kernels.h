@@ -306,8 +306,13 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
   constexpr int NW = CPL * (int)sizeof(T) / 4;
   uint32_t tgw[NW];
   if (live) {
-    const int64_t grow = a.ghm ? ((int64_t)b * a.G + g) * a.Q + q : unit;
-    load_global_words<NW>(static_cast<const T *>(a.grad_out) + grow * a.D + j * CPL, tgw);
+    load_global_words<NW>(static_cast<const T *>(a.grad_out) + unit * a.D + j * CPL, tgw);
+    if (a.gout_hm) {   // the row again, head-major, for the tile kernel
+      uint32_t *dst = reinterpret_cast<uint32_t *>(static_cast<T *>(a.gout_hm) +
+                                                   (((int64_t)b * a.G + g) * a.Q + q) * a.D + j * CPL);
+#pragma unroll
+      for (int c = 0; c < NW; ++c) dst[c] = tgw[c];
+    }
   } else {
 #pragma unroll
     for (int c = 0; c < NW; ++c) tgw[c] = 0u;
@@ -503,7 +508,8 @@ void fda_bwd_tile_kernel(const Args a) {
   }
   const uint32_t nbg = (uint32_t)a.B * (uint32_t)hpx;
   const uint32_t total = nbg * T_h;
-  const T *go = static_cast<const T *>(a.grad_out);
+  // grad_output rows in sample order / (L*K): the head-major copy, or grad_out itself (G == 1)
+  const T *go = static_cast<const T *>(a.gout_hm ? a.gout_hm : a.grad_out);
 
 #if OPS3D_FDA_TILE_TIMING
   unsigned long long t_acc[6] = {0, 0, 0, 0, 0, 0}, t_prev = clock64();

@@ -2,17 +2,22 @@
 //
 // Every sample inside the volume has a home tile (key) and a tile-local word (fda_device.h,
 // tile_word); it is listed in its home tile and in the next tile along each axis whose flag is
-// set, 1 to 8 entries.  Three kernels and a scan:
-//   tile_clear:   zero the per-tile counters,
-//   tile_count:   per block, a contiguous range of one head's samples (about 64 blocks per
-//                 head); an LDS histogram over all of the head's tiles, flushed with one global
-//                 atomic per touched tile (a head with more than kWin tiles counts straight
-//                 into global atomics: correct, slower),
-//   tile_scan:    one block: exclusive scan of the counters -> tile_start, tile_cursor,
-//   tile_scatter: the same histogram again, then one global atomic per touched tile reserves
-//                 the block's range of that tile, and LDS atomics rank the entries inside it.
-// The order of entries inside a tile depends on the order in which blocks reserve; the tile
-// kernel's sums are fp32 and so depend on that order at the rounding level.
+// set, 1 to 8 entries.  A block handles a contiguous range of one head's samples (about 64
+// blocks per head) and keeps an LDS histogram over all of the head's tiles.
+//
+// Matrix mode (the head has at most min(tcap, kWin) tiles; tcap is what the workspace holds):
+//   tile_count:   each block writes its histogram as a row of a [head][block][tile] matrix,
+//   tile_colscan: per tile, exclusive prefix over the head's blocks (in place) and the total,
+//   tile_scan:    one block: exclusive scan of the totals -> tile_start,
+//   tile_scatter: block c's entries of tile t go to tile_start[t] + prefix[c][t] + their rank
+//                 among the block's entries of t (LDS atomics).
+//   No global atomics: every position is computed.
+// Atomic mode (more tiles): the histograms are flushed with global atomics into zeroed
+// counters, and tile_scatter reserves each block's range of a tile with one global atomic on
+// the tile's cursor.  Correct for any size, slower (the atomics of all blocks contend).
+// The order of entries inside a tile (the LDS ranks, and in atomic mode the order of the
+// reservations) decides the order of the tile kernel's fp32 sums, so grad_value can differ
+// between runs at the rounding level.
 #include "fda_device.h"
 
 namespace ops3d_fda {
@@ -32,8 +37,15 @@ struct BucketArgs {
   int L, BG, TX, TY, TZ;
   uint32_t *counts;            // [BG * T_h]
   uint32_t *cursor;            // [BG * T_h]
+  const uint32_t *start;       // [BG * T_h + 1]
+  uint32_t *mat;               // [BG][blocks_per_head][T_h] (matrix mode)
+  uint32_t tcap;               // matrix mode when T_h <= min(tcap, kWin)
   uint2 *entries;              // [<= 8N]
 };
+
+__device__ __forceinline__ bool matrix_mode(const BucketArgs &a, uint32_t T_h) {
+  return T_h <= a.tcap && T_h <= (uint32_t)kWin;
+}
 
 struct LevelGrid {
   uint32_t sy, sz;             // tile-id strides of the level's tile grid (y: ntx, z: ntx*nty)
@@ -65,10 +77,11 @@ __device__ __forceinline__ void for_each_entry(uint32_t key, uint32_t word, cons
       }
 }
 
-__global__ __launch_bounds__(1024) void tile_clear_kernel(uint32_t *counts, const int64_t *shapes, int L, int BG,
-                                                         int TX, int TY, int TZ) {
-  const uint32_t total = (uint32_t)BG * tiles_per_head(shapes, L, TX, TY, TZ);
-  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) counts[i] = 0u;
+__global__ __launch_bounds__(1024) void tile_clear_kernel(const BucketArgs a) {
+  const uint32_t T_h = tiles_per_head(a.shapes, a.L, a.TX, a.TY, a.TZ);
+  if (matrix_mode(a, T_h)) return;   // the column scan writes every counter
+  const uint32_t total = (uint32_t)a.BG * T_h;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) a.counts[i] = 0u;
 }
 
 // Block -> its head and sample range [s0, s1).
@@ -101,8 +114,38 @@ __global__ __launch_bounds__(kBucketThreads) void tile_count_kernel(const Bucket
     });
   }
   __syncthreads();
-  for (uint32_t i = threadIdx.x; i < nw; i += kBucketThreads)
-    if (win[i]) atomicAdd(&a.counts[w0 + i], win[i]);
+  if (matrix_mode(a, T_h)) {
+    uint32_t *row = a.mat + (size_t)blockIdx.x * T_h;   // block index = bg * blocks_per_head + c
+    for (uint32_t i = threadIdx.x; i < T_h; i += kBucketThreads) row[i] = win[i];
+  } else {
+    for (uint32_t i = threadIdx.x; i < nw; i += kBucketThreads)
+      if (win[i]) atomicAdd(&a.counts[w0 + i], win[i]);
+  }
+}
+
+// Matrix mode: for each tile of each head, exclusive prefix of its counts over the head's
+// blocks (in place) and the total into counts.
+__global__ __launch_bounds__(256) void tile_colscan_kernel(const BucketArgs a) {
+  const uint32_t T_h = tiles_per_head(a.shapes, a.L, a.TX, a.TY, a.TZ);
+  if (!matrix_mode(a, T_h)) return;
+  const uint32_t total = (uint32_t)a.BG * T_h;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
+    const uint32_t bg = i / T_h, t = i - bg * T_h;
+    uint32_t *col = a.mat + (size_t)bg * a.blocks_per_head * T_h + t;
+    uint32_t run = 0;
+    // 16 loads in flight, then their prefix
+    for (uint32_t c0 = 0; c0 < a.blocks_per_head; c0 += 16) {
+      uint32_t v[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) v[k] = c0 + k < a.blocks_per_head ? col[(size_t)(c0 + k) * T_h] : 0u;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        if (c0 + k < a.blocks_per_head) col[(size_t)(c0 + k) * T_h] = run;
+        run += v[k];
+      }
+    }
+    a.counts[i] = run;
+  }
 }
 
 __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const BucketArgs a) {
@@ -120,18 +163,24 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
   uint32_t bg, s0, s1;
   block_range(a, bg, s0, s1);
   const uint32_t w0 = bg * T_h;
-  // pass A: counts of the window's tiles
+  if (matrix_mode(a, T_h)) {
+    // the block's first position in each tile: tile start + the earlier blocks' entries
+    const uint32_t *row = a.mat + (size_t)blockIdx.x * T_h;
+    for (uint32_t i = threadIdx.x; i < T_h; i += kBucketThreads) win[i] = a.start[w0 + i] + row[i];
+  } else {
+    // pass A: counts of the window's tiles, then one reservation per touched tile
 #pragma unroll 2
-  for (uint32_t s = s0 + threadIdx.x; s < s1; s += kBucketThreads) {
-    const uint32_t key = a.keys[s];
-    if (key == kKeyInvalid) continue;
-    for_each_entry(key, a.words[s], lg, [&](uint32_t id, uint32_t) {
-      if (id - w0 < nw) atomicAdd(&win[id - w0], 1u);
-    });
+    for (uint32_t s = s0 + threadIdx.x; s < s1; s += kBucketThreads) {
+      const uint32_t key = a.keys[s];
+      if (key == kKeyInvalid) continue;
+      for_each_entry(key, a.words[s], lg, [&](uint32_t id, uint32_t) {
+        if (id - w0 < nw) atomicAdd(&win[id - w0], 1u);
+      });
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < nw; i += kBucketThreads)
+      if (win[i]) win[i] = atomicAdd(&a.cursor[w0 + i], win[i]);
   }
-  __syncthreads();
-  for (uint32_t i = threadIdx.x; i < nw; i += kBucketThreads)
-    if (win[i]) win[i] = atomicAdd(&a.cursor[w0 + i], win[i]);
   __syncthreads();
   // pass B: place the entries
 #pragma unroll 2
@@ -183,23 +232,28 @@ __global__ __launch_bounds__(1024) void tile_scan_kernel(const uint32_t *counts,
   if (threadIdx.x == 0) start[total] = carry;
 }
 
+// Workspace words of the matrix of tile_count (blocks x tiles of every head) for heads of up
+// to tcap tiles.
+size_t tile_matrix_words(uint32_t BG, uint32_t tcap) { return (size_t)BG * kBlocksPerHead * tcap; }
+
 hipError_t launch_tile_bucketing(const uint32_t *keys, const uint32_t *words, uint32_t n, uint32_t per_head,
                                  const int64_t *shapes, int L, int BG, int TX, int TY, int TZ, uint32_t *counts,
-                                 uint32_t *start, uint32_t *cursor, uint2 *entries, hipStream_t st,
-                                 void (*mark)(int, hipStream_t)) {
-  hipLaunchKernelGGL(tile_clear_kernel, dim3(64), dim3(1024), 0, st, counts, shapes, L, BG, TX, TY, TZ);
+                                 uint32_t *start, uint32_t *cursor, uint32_t *mat, uint32_t tcap, uint2 *entries,
+                                 hipStream_t st, void (*mark)(int, hipStream_t)) {
   BucketArgs a{};
   a.keys = keys; a.words = words; a.n = n; a.per_head = per_head; a.shapes = shapes;
   a.L = L; a.BG = BG; a.TX = TX; a.TY = TY; a.TZ = TZ;
-  a.counts = counts; a.cursor = cursor; a.entries = entries;
+  a.counts = counts; a.cursor = cursor; a.start = start; a.mat = mat; a.tcap = tcap; a.entries = entries;
   // about kBlocksPerHead blocks per head, each a whole number of kBucketThreads-sample steps
-  a.blocks_per_head = kBlocksPerHead;
   a.chunk = (per_head + kBlocksPerHead - 1) / kBlocksPerHead;
   a.chunk = (a.chunk + kBucketThreads - 1) / kBucketThreads * kBucketThreads;
   if (a.chunk == 0) a.chunk = kBucketThreads;
   a.blocks_per_head = (per_head + a.chunk - 1) / a.chunk;
-  const unsigned blocks = n > 0 ? (unsigned)BG * a.blocks_per_head : 0u;
+  if (n == 0) a.blocks_per_head = 0;   // every counter is zero: the column scan writes zeros
+  const unsigned blocks = (unsigned)BG * a.blocks_per_head;
+  hipLaunchKernelGGL(tile_clear_kernel, dim3(64), dim3(1024), 0, st, a);
   if (blocks > 0) hipLaunchKernelGGL(tile_count_kernel, dim3(blocks), dim3(kBucketThreads), kWin * 4, st, a);
+  hipLaunchKernelGGL(tile_colscan_kernel, dim3(64), dim3(256), 0, st, a);
   hipLaunchKernelGGL(tile_scan_kernel, dim3(1), dim3(1024), 0, st, counts, start, cursor, shapes, L, BG, TX, TY, TZ);
   if (mark) mark(3, st);
   if (blocks > 0) hipLaunchKernelGGL(tile_scatter_kernel, dim3(blocks), dim3(kBucketThreads), kWin * 8, st, a);

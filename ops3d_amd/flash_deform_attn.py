@@ -100,38 +100,28 @@ class FlashDeformAttnFunction(Function):
                 )
             )
 
-        B, Q, G, C = value.shape[0], sampling_loc_attn.shape[1], value.shape[2], value.shape[3]
-        d_stride, blockthread = findspec(B, Q, G, C)
-        ctx.d_stride_backward, ctx.blockthread_backward = findspec_bwd(B, Q, G, C)
-
-        output = _C.flash_deform_attn_forward(
-            value,
-            value_spatial_shapes,
-            value_level_start_index,
-            sampling_loc_attn,
-            ctx.im2col_step,
-            K,
-            d_stride,
-            blockthread,
-            use_reg,
+        # The reference derives CUDA launch hints here (findspec / findspec_bwd, still exported);
+        # the gfx950 library chooses its own geometry, so they are not computed.  The forward's
+        # head-major copy of value is kept for the backward, which needs the same copy.
+        output, value_hm = _C.forward_keep_head_major(
+            value, value_spatial_shapes, value_level_start_index, sampling_loc_attn, ctx.im2col_step, K
         )
-        ctx.save_for_backward(value, value_spatial_shapes, value_level_start_index, sampling_loc_attn)
+        ctx.save_for_backward(value, value_spatial_shapes, value_level_start_index, sampling_loc_attn, value_hm)
         return output
 
     @staticmethod
     @once_differentiable
     def backward(ctx, grad_output):
-        value, value_spatial_shapes, value_level_start_index, sampling_loc_attn = ctx.saved_tensors
-        grad_value, grad_sampling_loc_attn = _C.flash_deform_attn_backward(
+        value, value_spatial_shapes, value_level_start_index, sampling_loc_attn, value_hm = ctx.saved_tensors
+        grad_value, grad_sampling_loc_attn = _C.backward_with_head_major(
             value,
+            value_hm,
             value_spatial_shapes,
             value_level_start_index,
             sampling_loc_attn,
             grad_output.contiguous(),
             ctx.im2col_step,
             ctx.K,
-            ctx.d_stride_backward,
-            ctx.blockthread_backward,
         )
         return grad_value, None, None, grad_sampling_loc_attn, None, None, None
 

@@ -125,6 +125,14 @@ def test_anisotropic_multilevel(gpu_device):
     _check("anisotropic", inp, gpu_device, torch.float32)
 
 
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_thin_levels_atomic_bucketing(gpu_device, dt):
+    """Levels one voxel thick and thousands long are cut into more tiles than the bucketing
+    matrix holds (S/16 + 64 per head), so the backward buckets them with global atomics."""
+    inp = random_inputs([(1, 1, 4096), (1, 2048, 1)], 1, 300, 8, 32, 4, dt, seed=8)
+    _check(f"thin levels {dt}", inp, gpu_device, dt)
+
+
 def test_out_of_volume_fp32(gpu_device):
     inp = random_inputs([(6, 5, 7), (3, 2, 4)], 2, 300, 8, 32, 4, torch.float32, seed=5, lo=-0.3, hi=1.3)
     _check("oob fp32", inp, gpu_device, torch.float32)
