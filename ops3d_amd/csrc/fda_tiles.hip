@@ -84,10 +84,24 @@ __global__ __launch_bounds__(1024) void tile_clear_kernel(const BucketArgs a) {
   for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) a.counts[i] = 0u;
 }
 
-// Block -> its head and sample range [s0, s1).
+// Block -> its head, its index c among the head's blocks and its sample range [s0, s1).  With
+// BG % 8 == 0 the blocks of head bg run on XCD bg % 8 (workgroups are dispatched to XCDs
+// round-robin), so the partly written lines of one head's tile runs stay in one XCD's L2.
+__device__ __forceinline__ uint32_t block_slot(const BucketArgs &a, uint32_t &bg, uint32_t &c) {
+  if ((a.BG & 7) == 0) {
+    const uint32_t x = blockIdx.x & 7u, r = blockIdx.x >> 3, hpx = (uint32_t)a.BG >> 3;
+    bg = x + 8u * (r % hpx);
+    c = r / hpx;
+  } else {
+    bg = blockIdx.x / a.blocks_per_head;
+    c = blockIdx.x - bg * a.blocks_per_head;
+  }
+  return bg * a.blocks_per_head + c;   // row of the block in the count matrix
+}
+
 __device__ __forceinline__ void block_range(const BucketArgs &a, uint32_t &bg, uint32_t &s0, uint32_t &s1) {
-  bg = blockIdx.x / a.blocks_per_head;
-  const uint32_t c = blockIdx.x - bg * a.blocks_per_head;
+  uint32_t c;
+  block_slot(a, bg, c);
   const uint32_t h0 = bg * a.per_head;
   s0 = h0 + min(c * a.chunk, a.per_head);
   s1 = h0 + min((c + 1) * a.chunk, a.per_head);
@@ -115,7 +129,8 @@ __global__ __launch_bounds__(kBucketThreads) void tile_count_kernel(const Bucket
   }
   __syncthreads();
   if (matrix_mode(a, T_h)) {
-    uint32_t *row = a.mat + (size_t)blockIdx.x * T_h;   // block index = bg * blocks_per_head + c
+    uint32_t hb, hc;
+    uint32_t *row = a.mat + (size_t)block_slot(a, hb, hc) * T_h;
     for (uint32_t i = threadIdx.x; i < T_h; i += kBucketThreads) row[i] = win[i];
   } else {
     for (uint32_t i = threadIdx.x; i < nw; i += kBucketThreads)
@@ -165,7 +180,8 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
   const uint32_t w0 = bg * T_h;
   if (matrix_mode(a, T_h)) {
     // the block's first position in each tile: tile start + the earlier blocks' entries
-    const uint32_t *row = a.mat + (size_t)blockIdx.x * T_h;
+    uint32_t hb, hc;
+    const uint32_t *row = a.mat + (size_t)block_slot(a, hb, hc) * T_h;
     for (uint32_t i = threadIdx.x; i < T_h; i += kBucketThreads) win[i] = a.start[w0 + i] + row[i];
   } else {
     // pass A: counts of the window's tiles, then one reservation per touched tile
