@@ -47,7 +47,7 @@ struct Args {
   uint32_t *vals;             // [N] tile-local base corner word of each sample (tile_word)
   float4 *stash;              // [N] (fx, fy, fz, attn) of each sample
   uint32_t *tile_counts;      // [B*G*T_h] entries per tile
-  uint32_t *tile_start;       // [B*G*T_h + 1] first entry of each tile (exclusive scan)
+  uint32_t *tile_start;       // [B*G*T_h] first entry of each tile (head base + exclusive scan)
   uint32_t *tile_cursor;      // [B*G*T_h] fill cursor of each tile
   uint2 *entries;             // [<= 8N] (sample, tile-local base corner word), grouped by tile
   int TX, TY, TZ;             // nominal tile dimensions (voxels), clipped per level

@@ -545,7 +545,7 @@ void fda_bwd_tile_kernel(const Args a) {
     const bool live = 2 * px < tx && py < ty && pz < tz && z < Dl && y < Hl && x0 < Wl;
     const bool two = 2 * px + 1 < tx && x0 + 1 < Wl;
     const uint32_t gid = (uint32_t)(b * G + g) * T_h + lbase + t;
-    const uint32_t e0 = a.tile_start[gid], e1 = a.tile_start[gid + 1];
+    const uint32_t e0 = a.tile_start[gid], e1 = e0 + a.tile_counts[gid];
     const int TXp = tx + 1, TYp = ty + 1;
     const int nb = TXp * TYp * (tz + 1);
 

@@ -6,15 +6,17 @@
 // blocks per head) and keeps an LDS histogram over all of the head's tiles.
 //
 // Matrix mode (the head has at most min(tcap, kWin) tiles; tcap is what the workspace holds):
-//   tile_count:   each block writes its histogram as a row of a [head][block][tile] matrix,
-//   tile_colscan: per tile, exclusive prefix over the head's blocks (in place) and the total,
-//   tile_scan:    one block: exclusive scan of the totals -> tile_start,
-//   tile_scatter: block c's entries of tile t go to tile_start[t] + prefix[c][t] + their rank
-//                 among the block's entries of t (LDS atomics).
+//   tile_count:    each block writes its histogram as a row of a [head][block][tile] matrix,
+//   tile_headscan: one block per head: per tile, exclusive prefix over the head's blocks (in
+//                  place) and the tile's total; exclusive scan of the totals -> tile_start,
+//   tile_scatter:  block c's entries of tile t go to tile_start[t] + prefix[c][t] + their rank
+//                  among the block's entries of t (LDS atomics).
 //   No global atomics: every position is computed.
 // Atomic mode (more tiles): the histograms are flushed with global atomics into zeroed
 // counters, and tile_scatter reserves each block's range of a tile with one global atomic on
 // the tile's cursor.  Correct for any size, slower (the atomics of all blocks contend).
+// Each head owns the entry range [bg * 8 * per_head, ...) (a sample has at most 8 entries), so
+// heads are bucketed independently; a tile's entries are [tile_start, tile_start + count).
 // The order of entries inside a tile (the LDS ranks, and in atomic mode the order of the
 // reservations) decides the order of the tile kernel's fp32 sums, so grad_value can differ
 // between runs at the rounding level.
@@ -35,7 +37,7 @@ struct BucketArgs {
   uint32_t blocks_per_head;
   const int64_t *shapes;
   int L, BG, TX, TY, TZ;
-  uint32_t *counts;            // [BG * T_h]
+  uint32_t *counts;            // [BG * T_h] entries per tile
   uint32_t *cursor;            // [BG * T_h]
   const uint32_t *start;       // [BG * T_h + 1]
   uint32_t *mat;               // [BG][blocks_per_head][T_h] (matrix mode)
@@ -118,7 +120,7 @@ __global__ __launch_bounds__(kBucketThreads) void tile_count_kernel(const Bucket
   uint32_t bg, s0, s1;
   block_range(a, bg, s0, s1);
   const uint32_t w0 = bg * T_h;
-#pragma unroll 2
+#pragma unroll 4
   for (uint32_t s = s0 + threadIdx.x; s < s1; s += kBucketThreads) {
     const uint32_t key = a.keys[s];
     if (key == kKeyInvalid) continue;
@@ -135,31 +137,6 @@ __global__ __launch_bounds__(kBucketThreads) void tile_count_kernel(const Bucket
   } else {
     for (uint32_t i = threadIdx.x; i < nw; i += kBucketThreads)
       if (win[i]) atomicAdd(&a.counts[w0 + i], win[i]);
-  }
-}
-
-// Matrix mode: for each tile of each head, exclusive prefix of its counts over the head's
-// blocks (in place) and the total into counts.
-__global__ __launch_bounds__(256) void tile_colscan_kernel(const BucketArgs a) {
-  const uint32_t T_h = tiles_per_head(a.shapes, a.L, a.TX, a.TY, a.TZ);
-  if (!matrix_mode(a, T_h)) return;
-  const uint32_t total = (uint32_t)a.BG * T_h;
-  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
-    const uint32_t bg = i / T_h, t = i - bg * T_h;
-    uint32_t *col = a.mat + (size_t)bg * a.blocks_per_head * T_h + t;
-    uint32_t run = 0;
-    // 16 loads in flight, then their prefix
-    for (uint32_t c0 = 0; c0 < a.blocks_per_head; c0 += 16) {
-      uint32_t v[16];
-#pragma unroll
-      for (int k = 0; k < 16; ++k) v[k] = c0 + k < a.blocks_per_head ? col[(size_t)(c0 + k) * T_h] : 0u;
-#pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        if (c0 + k < a.blocks_per_head) col[(size_t)(c0 + k) * T_h] = run;
-        run += v[k];
-      }
-    }
-    a.counts[i] = run;
   }
 }
 
@@ -185,7 +162,7 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
     for (uint32_t i = threadIdx.x; i < T_h; i += kBucketThreads) win[i] = a.start[w0 + i] + row[i];
   } else {
     // pass A: counts of the window's tiles, then one reservation per touched tile
-#pragma unroll 2
+#pragma unroll 4
     for (uint32_t s = s0 + threadIdx.x; s < s1; s += kBucketThreads) {
       const uint32_t key = a.keys[s];
       if (key == kKeyInvalid) continue;
@@ -199,7 +176,7 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
   }
   __syncthreads();
   // pass B: place the entries
-#pragma unroll 2
+#pragma unroll 4
   for (uint32_t s = s0 + threadIdx.x; s < s1; s += kBucketThreads) {
     const uint32_t key = a.keys[s];
     if (key == kKeyInvalid) continue;
@@ -212,18 +189,38 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
   }
 }
 
-// One block of 1024 threads: tile_start = exclusive scan of counts (and its total at the end),
-// cursor = tile_start.
-__global__ __launch_bounds__(1024) void tile_scan_kernel(const uint32_t *counts, uint32_t *start, uint32_t *cursor,
-                                                        const int64_t *shapes, int L, int BG, int TX, int TY,
-                                                        int TZ) {
+// One block per head: per tile, the exclusive prefix of its counts over the head's blocks (in
+// place, matrix mode) and its total (counts); tile_start = head base + exclusive scan of the
+// totals over the head's tiles; cursor = tile_start.
+__global__ __launch_bounds__(1024) void tile_headscan_kernel(const BucketArgs a, uint32_t *start) {
   __shared__ uint32_t tmp[16];
-  const uint32_t total = (uint32_t)BG * tiles_per_head(shapes, L, TX, TY, TZ);
+  const uint32_t T_h = tiles_per_head(a.shapes, a.L, a.TX, a.TY, a.TZ);
+  const bool mat = matrix_mode(a, T_h);
+  const uint32_t bg = blockIdx.x;
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
-  uint32_t carry = 0;
-  for (uint32_t base = 0; base < total; base += 1024) {
-    const uint32_t i = base + threadIdx.x;
-    const uint32_t x = i < total ? counts[i] : 0u;
+  uint32_t carry = bg * 8u * a.per_head;   // the head's entry range
+  for (uint32_t base = 0; base < T_h; base += 1024) {
+    const uint32_t t = base + threadIdx.x;
+    uint32_t x = 0;
+    if (t < T_h) {
+      if (mat) {
+        uint32_t *col = a.mat + (size_t)bg * a.blocks_per_head * T_h + t;
+        // 16 loads in flight, then their prefix
+        for (uint32_t c0 = 0; c0 < a.blocks_per_head; c0 += 16) {
+          uint32_t v[16];
+#pragma unroll
+          for (int k = 0; k < 16; ++k) v[k] = c0 + k < a.blocks_per_head ? col[(size_t)(c0 + k) * T_h] : 0u;
+#pragma unroll
+          for (int k = 0; k < 16; ++k) {
+            if (c0 + k < a.blocks_per_head) col[(size_t)(c0 + k) * T_h] = x;
+            x += v[k];
+          }
+        }
+        a.counts[bg * T_h + t] = x;
+      } else {
+        x = a.counts[bg * T_h + t];
+      }
+    }
     uint32_t inc = x;
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) {
@@ -238,14 +235,13 @@ __global__ __launch_bounds__(1024) void tile_scan_kernel(const uint32_t *counts,
       all += tmp[ww];
     }
     __syncthreads();
-    if (i < total) {
+    if (t < T_h) {
       const uint32_t v = carry + wofs + inc - x;
-      start[i] = v;
-      cursor[i] = v;
+      start[bg * T_h + t] = v;
+      a.cursor[bg * T_h + t] = v;
     }
     carry += all;
   }
-  if (threadIdx.x == 0) start[total] = carry;
 }
 
 // Workspace words of the matrix of tile_count (blocks x tiles of every head) for heads of up
@@ -265,12 +261,11 @@ hipError_t launch_tile_bucketing(const uint32_t *keys, const uint32_t *words, ui
   a.chunk = (a.chunk + kBucketThreads - 1) / kBucketThreads * kBucketThreads;
   if (a.chunk == 0) a.chunk = kBucketThreads;
   a.blocks_per_head = (per_head + a.chunk - 1) / a.chunk;
-  if (n == 0) a.blocks_per_head = 0;   // every counter is zero: the column scan writes zeros
+  if (n == 0) a.blocks_per_head = 0;   // every counter is zero: the head scan writes zeros
   const unsigned blocks = (unsigned)BG * a.blocks_per_head;
   hipLaunchKernelGGL(tile_clear_kernel, dim3(64), dim3(1024), 0, st, a);
   if (blocks > 0) hipLaunchKernelGGL(tile_count_kernel, dim3(blocks), dim3(kBucketThreads), kWin * 4, st, a);
-  hipLaunchKernelGGL(tile_colscan_kernel, dim3(64), dim3(256), 0, st, a);
-  hipLaunchKernelGGL(tile_scan_kernel, dim3(1), dim3(1024), 0, st, counts, start, cursor, shapes, L, BG, TX, TY, TZ);
+  if (BG > 0) hipLaunchKernelGGL(tile_headscan_kernel, dim3((unsigned)BG), dim3(1024), 0, st, a, start);
   if (mark) mark(3, st);
   if (blocks > 0) hipLaunchKernelGGL(tile_scatter_kernel, dim3(blocks), dim3(kBucketThreads), kWin * 8, st, a);
   return hipGetLastError();
