@@ -123,7 +123,8 @@ int common_checks(int dtype, int B, int S, int G, int D, int L, int Q, int K, in
     return fail(OPS3D_FDA_EINVAL, "value too large: S*G*D = %lld exceeds %lld elements per batch item",
                 (long long)S * G * D, (long long)kMaxLevelElems);
   const int LK = L * K, P = 4 * LK;
-  const int ulanes = (!backward && fwd_pairs(geo.cpl, geo.lpu, elem_size(dtype))) ? 2 * geo.lpu : geo.lpu;
+  // 64-byte rows: forward and backward query kernels give each unit 8 lanes (x-pair loads)
+  const int ulanes = fwd_pairs(geo.cpl, geo.lpu, elem_size(dtype)) ? 2 * geo.lpu : geo.lpu;
   const int UPB = kWavesPerBlock * (kWave / ulanes);
   const size_t lds = (size_t)UPB * (size_t)(backward ? bwd_query_lds_floats(P, LK) : P + 1) * sizeof(float);
   if (lds > 160 * 1024)   // gfx950: 160 KB of LDS per workgroup

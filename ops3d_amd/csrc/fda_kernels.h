@@ -263,6 +263,183 @@ __global__ __launch_bounds__(kBlock) void fda_forward_pair_kernel(const Args a) 
   if (live && dxl == 0) store_elems<T, CPL>(static_cast<T *>(a.out) + unit * a.D + j * CPL, acc);
 }
 
+// Backward phase 1 for rows of 64 bytes (4 lanes x 16 bytes), the x-pair form of the forward's
+// pair kernel: a unit has 8 lanes, lanes 0-3 take the x0 row and lanes 4-7 the x0+1 row of each
+// corner pair (one 128-byte span per pair), so each lane loads 4 corners per sample.  Sample
+// set-ups are made once per quad (lane k of a quad sets up sample k0+k) and broadcast by DPP;
+// the lane that made a set-up also records that sample's stash and base corner.  The partials
+// of grad_loc / grad_attn of a lane's x-row are summed over the unit's 8 lanes.
+template <typename T, int CPL>
+__global__ __launch_bounds__(kBlock) void fda_bwd_query_pair_kernel(const Args a) {
+  extern __shared__ float lds[];
+  constexpr int UL = 8;
+  constexpr int UPW = kWave / UL, UPB = kWavesPerBlock * UPW;
+  static_assert(CPL * sizeof(T) == 16, "pair kernel: 16 bytes per lane, 64-byte rows");
+  int b, g, qb;
+  if (!map_tile(a, blockIdx.x, b, g, qb)) return;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int ju = lane & (UL - 1);   // lane within the unit
+  const int j = ju & 3;             // channel chunk
+  const int dxl = ju >> 2;          // x-row of the corner pairs this lane loads
+  const int ub = wave * UPW + lane / UL;
+  const int q = qb * UPB + ub;
+  const bool live = q < a.Q;
+  const int L = a.L, K = a.K, LK = L * K, P = a.P;
+  const int RS = bwd_query_lds_floats(P, LK);
+  float *rec = lds + ub * RS;
+  float *gat_s = rec + P;
+  float4 *st_s = reinterpret_cast<float4 *>(lds + ub * RS + ((P + LK + 3) & ~3));
+  uint32_t *cx_s = reinterpret_cast<uint32_t *>(st_s + LK);
+  uint32_t *cy_s = cx_s + LK, *cz_s = cy_s + LK;
+  const int64_t unit = ((int64_t)b * a.Q + (live ? q : 0)) * a.G + g;
+  __shared__ LevelTiles lvt[5];
+  __shared__ uint32_t lvbase[5];
+  if (threadIdx.x == 0) {
+    uint32_t t = (uint32_t)(b * a.G + g) * tiles_per_head(a.shapes, L, a.TX, a.TY, a.TZ);
+    for (int l = 0; l < L; ++l) {
+      lvt[l] = level_tiles(a.shapes, l, a.TX, a.TY, a.TZ);
+      lvbase[l] = t;
+      t += lvt[l].count;
+    }
+  }
+  __syncthreads();
+
+  stage_record<T, UL>(static_cast<const T *>(a.loc_attn) + unit * P, P, ju, live, rec);
+  wave_lds_sync();
+  unit_softmax<UL>(rec + 3 * LK, LK, ju);
+  wave_lds_sync();
+
+  constexpr int NW = CPL * (int)sizeof(T) / 4;
+  uint32_t tgw[NW];
+  if (live) {
+    load_global_words<NW>(static_cast<const T *>(a.grad_out) + unit * a.D + j * CPL, tgw);
+    if (a.gout_hm && dxl == 0) {   // the row again, head-major, for the tile kernel
+      uint32_t *dst = reinterpret_cast<uint32_t *>(static_cast<T *>(a.gout_hm) +
+                                                   (((int64_t)b * a.G + g) * a.Q + q) * a.D + j * CPL);
+#pragma unroll
+      for (int c = 0; c < NW; ++c) dst[c] = tgw[c];
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < NW; ++c) tgw[c] = 0u;
+  }
+
+  const int RST = a.vhm ? a.D : a.G * a.D;
+  const uint32_t lane_elem = (uint32_t)((a.vhm ? 0 : g * a.D) + j * CPL);
+  const T *vb = static_cast<const T *>(a.value) +
+                (a.vhm ? ((int64_t)b * a.G + g) * a.S * a.D : (int64_t)b * a.S * a.G * a.D);
+  for (int l = 0; l < L; ++l) {
+    const int Dl = (int)a.shapes[3 * l], Hl = (int)a.shapes[3 * l + 1], Wl = (int)a.shapes[3 * l + 2];
+    const int64_t st = a.lsi[l];
+    const int64_t nel = (int64_t)Dl * Hl * Wl * RST;
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb + st * RST, (uint32_t)(nel * (int64_t)sizeof(T)));
+    for (int k0 = 0; k0 < K; k0 += 4) {
+      // lane k of each quad sets up sample k0 + k (both quads: each needs its own x-row)
+      const int kq = k0 + (ju & 3);
+      const bool have = kq < K;
+      const int sj = l * K + (have ? kq : K - 1);
+      Sample ms;
+      const bool in_s = sample_setup(rec[3 * sj], rec[3 * sj + 1], rec[3 * sj + 2], Wl, Hl, Dl, RST, ms) && live;
+      if (dxl == 0 && have) {
+        cx_s[sj] = in_s ? (uint32_t)(ms.x0 + 1) : kKeyInvalid;
+        cy_s[sj] = (uint32_t)(ms.y0 + 1);
+        cz_s[sj] = (uint32_t)(ms.z0 + 1);
+        st_s[sj] = make_float4(ms.wx[1], ms.wy[1], ms.wz[1], rec[3 * LK + sj]);
+      }
+      uint32_t off4[4];
+#pragma unroll
+      for (int c4 = 0; c4 < 4; ++c4)   // c4 = (dz, dy); a select, not an index, keeps ms in registers
+        off4[c4] = live ? (dxl ? ms.off[2 * c4 + 1] : ms.off[2 * c4]) : OOB_ELEM;
+      const float wv[6] = {ms.wx[0], ms.wx[1], ms.wy[0], ms.wy[1], ms.wz[0], ms.wz[1]};
+      // all four set-ups are computed (past K they repeat sample K-1), so U and W stay in
+      // registers; only the write-back below skips them
+      float U[4][4];
+      static_for<4>([&](auto uc) {
+        constexpr int u = decltype(uc)::value;
+#pragma unroll
+        for (int c4 = 0; c4 < 4; ++c4) {
+          const uint32_t o = unit_bcast<4, u>(off4[c4]);
+          U[u][c4] = dot_elems<T, CPL>(rv, (o + lane_elem) * (uint32_t)sizeof(T), tgw);
+        }
+      });
+      static_for<4>([&](auto uc) {
+        constexpr int u = decltype(uc)::value;
+        if (k0 + u < K) {
+          float W[6];   // (wx0, wx1, wy0, wy1, wz0, wz1) of sample k0 + u
+#pragma unroll
+          for (int i = 0; i < 6; ++i) W[i] = __uint_as_float(unit_bcast<4, u>(__float_as_uint(wv[i])));
+          const float wxd = dxl ? W[1] : W[0];
+          const float sx = dxl ? 1.f : -1.f;
+          float gx = 0.f, gy = 0.f, gz = 0.f, ga = 0.f;
+#pragma unroll
+          for (int c4 = 0; c4 < 4; ++c4) {
+            const int dz = c4 >> 1, dy = c4 & 1;
+            const float yz = W[2 + dy] * W[4 + dz];
+            ga = fmaf(wxd * yz, U[u][c4], ga);
+            gx = fmaf(sx * yz, U[u][c4], gx);
+          }
+          // d w / dy = (dy ? +1 : -1) * wx * wz, d w / dz = (dz ? +1 : -1) * wx * wy
+#pragma unroll
+          for (int dz = 0; dz < 2; ++dz) gy = fmaf(wxd * W[4 + dz], U[u][2 * dz + 1] - U[u][2 * dz], gy);
+#pragma unroll
+          for (int dy = 0; dy < 2; ++dy) gz = fmaf(wxd * W[2 + dy], U[u][2 + dy] - U[u][dy], gz);
+          gx = unit_sum<UL>(gx);
+          gy = unit_sum<UL>(gy);
+          gz = unit_sum<UL>(gz);
+          ga = unit_sum<UL>(ga);
+          if (ju == 0) {
+            const int su = l * K + k0 + u;
+            const float at = rec[3 * LK + su];
+            // d(pixel)/d(loc) = size (grid_sample: size/2 per unit of grid, grid = 2*loc - 1)
+            rec[3 * su] = gx * at * (float)Wl;
+            rec[3 * su + 1] = gy * at * (float)Hl;
+            rec[3 * su + 2] = gz * at * (float)Dl;
+            gat_s[su] = ga;
+          }
+        }
+      });
+    }
+  }
+  wave_lds_sync();
+  {
+    // the wave's units are consecutive q of one (b, g): their samples are one contiguous range
+    const int q0 = qb * UPB + wave * UPW;
+    const int nlive = min(UPW, a.Q - q0);
+    if (nlive > 0) {
+      const uint32_t gs0 = sample_index(b, g, q0, 0, a.G, a.Q, LK);
+      const int ntot = nlive * LK;
+      for (int e = lane; e < ntot; e += kWave) {
+        const int uu = e / LK, ss = e - uu * LK;
+        const int ubx = wave * UPW + uu;
+        const float4 *stx = reinterpret_cast<const float4 *>(lds + ubx * RS + ((P + LK + 3) & ~3));
+        const uint32_t *kx = reinterpret_cast<const uint32_t *>(stx + LK);
+        const int l = ss / K;
+        const LevelTiles &lt = lvt[l];
+        const uint32_t bx = kx[ss];
+        const int x0 = (int)bx - 1, y0 = (int)kx[LK + ss] - 1, z0 = (int)kx[2 * LK + ss] - 1;
+        const int hz = max(z0, 0) >> lt.sh[0], hy = max(y0, 0) >> lt.sh[1], hx = max(x0, 0) >> lt.sh[2];
+        const int lz = z0 - hz * lt.t[0], ly = y0 - hy * lt.t[1], lx = x0 - hx * lt.t[2];
+        const uint32_t ex = lx == lt.t[2] - 1 && (hx + 1) * lt.t[2] < lt.n[2];
+        const uint32_t ey = ly == lt.t[1] - 1 && (hy + 1) * lt.t[1] < lt.n[1];
+        const uint32_t ez = lz == lt.t[0] - 1 && (hz + 1) * lt.t[0] < lt.n[0];
+        a.keys[gs0 + e] = bx == kKeyInvalid ? kKeyInvalid : lvbase[l] + (uint32_t)((hz * lt.nt[1] + hy) * lt.nt[2] + hx);
+        a.vals[gs0 + e] = tile_word(lx, ly, lz) | (ex << 15) | (ey << 16) | (ez << 17) | ((uint32_t)l << 18);
+        a.stash[gs0 + e] = stx[ss];
+      }
+    }
+  }
+  // softmax backward over the unit's L*K attention weights
+  float dot = 0.f;
+  for (int t = ju; t < LK; t += UL) dot = fmaf(rec[3 * LK + t], gat_s[t], dot);
+  dot = unit_sum<UL>(dot);
+  for (int t = ju; t < LK; t += UL) {
+    const float at = rec[3 * LK + t];
+    rec[3 * LK + t] = at * (gat_s[t] - dot);
+  }
+  wave_lds_sync();
+  if (live) write_record<T, UL>(static_cast<T *>(a.grad_loc_attn) + unit * P, P, ju, rec);
+}
+
 template <typename T, int CPL, int LPU>
 __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
   extern __shared__ float lds[];
@@ -708,8 +885,12 @@ hipError_t launch_one(int which, const Args &a, unsigned grid, size_t lds, hipSt
     else
       hipLaunchKernelGGL((fda_forward_kernel<T, CPL, LPU>), dim3(grid), dim3(kBlock), lds, st, a);
   }
-  else if (which == 1)
-    hipLaunchKernelGGL((fda_bwd_query_kernel<T, CPL, LPU>), dim3(grid), dim3(kBlock), lds, st, a);
+  else if (which == 1) {
+    if constexpr (fwd_pairs(CPL, LPU, (int)sizeof(T)))
+      hipLaunchKernelGGL((fda_bwd_query_pair_kernel<T, CPL>), dim3(grid), dim3(kBlock), lds, st, a);
+    else
+      hipLaunchKernelGGL((fda_bwd_query_kernel<T, CPL, LPU>), dim3(grid), dim3(kBlock), lds, st, a);
+  }
   else {
     // persistent: `grid` (the CU count, a multiple of 8 with XCD affinity) times the blocks that
     // fit on a CU at once
