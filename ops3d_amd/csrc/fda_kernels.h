@@ -218,12 +218,14 @@ __global__ __launch_bounds__(kBlock) void fda_forward_pair_kernel(const Args a) 
       sample_setup(rec[3 * sj], rec[3 * sj + 1], rec[3 * sj + 2], Wl, Hl, Dl, RST, ms);
       uint32_t off4[4];
       float w4[4];
+      // corner weights times the sample's attention weight (made once per set-up, not per channel)
+      const float at_s = rec[3 * LK + sj];
+      const float wxd = dxl ? ms.wx[1] : ms.wx[0];
 #pragma unroll
       for (int c4 = 0; c4 < 4; ++c4) {   // c4 = (dz, dy); this lane's corner c = 2*c4 + dxl
         off4[c4] = live ? (dxl ? ms.off[2 * c4 + 1] : ms.off[2 * c4]) : OOB_ELEM;
-        w4[c4] = (ms.wx[dxl] * ms.wy[c4 & 1]) * ms.wz[c4 >> 1];
+        w4[c4] = ((wxd * ms.wy[c4 & 1]) * ms.wz[c4 >> 1]) * at_s;
       }
-      const uint32_t at_mine = __float_as_uint(rec[3 * LK + sj]);
       static_for<4>([&](auto uc) {
         constexpr int u = decltype(uc)::value;
         if (k0 + u < K) {
@@ -234,25 +236,19 @@ __global__ __launch_bounds__(kBlock) void fda_forward_pair_kernel(const Args a) 
             off[c4] = unit_bcast<4, u>(off4[c4]);
             w[c4] = __uint_as_float(unit_bcast<4, u>(__float_as_uint(w4[c4])));
           }
-          const float at = __uint_as_float(unit_bcast<4, u>(at_mine));
           uint32_t v[4][NW];
 #pragma unroll
           for (int c4 = 0; c4 < 4; ++c4)
             bload<NW * 4>(rv, (off[c4] + lane_elem) * (uint32_t)sizeof(T), v[c4]);
 #pragma unroll
           for (int i = 0; i < NW; ++i) {
-            float t[EPW], f[EPW];
-            Elem<T>::unpack(v[0][i], f);
 #pragma unroll
-            for (int e = 0; e < EPW; ++e) t[e] = f[e] * w[0];
-#pragma unroll
-            for (int c4 = 1; c4 < 4; ++c4) {
+            for (int c4 = 0; c4 < 4; ++c4) {
+              float f[EPW];
               Elem<T>::unpack(v[c4][i], f);
 #pragma unroll
-              for (int e = 0; e < EPW; ++e) t[e] = fmaf(f[e], w[c4], t[e]);
+              for (int e = 0; e < EPW; ++e) acc[i * EPW + e] = fmaf(f[e], w[c4], acc[i * EPW + e]);
             }
-#pragma unroll
-            for (int e = 0; e < EPW; ++e) acc[i * EPW + e] = fmaf(at, t[e], acc[i * EPW + e]);
           }
         }
       });

@@ -89,7 +89,8 @@ def forward(value, shapes, loc_attn, K, coord_mode=1):
 
 def backward(value, shapes, loc_attn, grad_out, K, coord_mode=1, abs_mode=0):
     """-> (grad_value [B,S,G,D], grad_loc_attn [B,Q,G,4LK]) in float64.  abs_mode=1 returns
-    the per-element magnitude M (sum of |terms|) instead, for rounding-error bounds."""
+    the per-element magnitude M (sum of |terms|) instead, for rounding-error bounds; abs_mode=2
+    the same with grad_value holding each element's number of terms."""
     lib = _load()
     value, loc_attn, grad_out = _d(value), _d(loc_attn), _d(grad_out)
     shapes, lsi = _meta(shapes)
@@ -106,6 +107,18 @@ def backward(value, shapes, loc_attn, grad_out, K, coord_mode=1, abs_mode=0):
 
 
 FP32_UNIT_ROUNDOFF = 2.0 ** -24
+
+
+def fp32_grad_value_allowance(value, shapes, loc_attn, grad_out, K):
+    """Per-element rounding allowance for fp32 grad_value: 4 * sqrt(n) * u * M, with M the sum
+    of |terms| of the element and n its number of terms (sample corners on that voxel) plus 3
+    (the rounded products attn * w * g).  Each element is a sum whose order the GPU's bucketing
+    leaves to run time (as the reference's atomic adds do), so no fixed relative bar holds for
+    elements whose terms cancel; this is the same random-walk bound as for the location
+    gradients (fp32_rounding_allowance)."""
+    m, _ = backward(value, shapes, loc_attn, grad_out, K, coord_mode=1, abs_mode=1)
+    n, _ = backward(value, shapes, loc_attn, grad_out, K, coord_mode=1, abs_mode=2)
+    return 4.0 * np.sqrt(n + 3.0) * FP32_UNIT_ROUNDOFF * m
 
 
 def fp32_rounding_allowance(value, shapes, loc_attn, grad_out, K):

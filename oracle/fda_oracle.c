@@ -109,7 +109,8 @@ void fda_oracle_forward(const double *value, const int64_t *shapes, const int64_
  * abs_mode = 1 computes, instead of the gradients, the sum of the absolute values of the terms
  * each gradient element is a sum of (|value|, |grad_out|, |d w / d pixel|, and for the logits
  * a_i * (|g_i| + sum_j a_j |g_j|)): the magnitude M that bounds the rounding error of any
- * fp32 evaluation order, |fl(x) - x| <= n * eps * M for an n-term sum. */
+ * fp32 evaluation order, |fl(x) - x| <= n * eps * M for an n-term sum.  abs_mode = 2 is
+ * abs_mode = 1 with grad_value holding the number n of terms of each element instead. */
 void fda_oracle_backward(const double *value, const int64_t *shapes, const int64_t *lsi,
                          const double *loc_attn, const double *grad_out, double *grad_value,
                          double *grad_loc_attn, int B, int S, int G, int D, int L, int Q, int K,
@@ -143,7 +144,10 @@ void fda_oracle_backward(const double *value, const int64_t *shapes, const int64
                 double dot = 0.0;
                 for (int d = 0; d < D; ++d) {
                   dot += abs_mode ? fabs(tg[d] * v[d]) : tg[d] * v[d];
-                  gv[d] += attn[s] * c.w[k8] * (abs_mode ? fabs(tg[d]) : tg[d]);
+                  if (abs_mode == 2)
+                    gv[d] += 1.0;   /* term count */
+                  else
+                    gv[d] += attn[s] * c.w[k8] * (abs_mode ? fabs(tg[d]) : tg[d]);
                 }
                 ga += c.w[k8] * dot;
                 gx += (abs_mode ? fabs(c.dwx[k8]) : c.dwx[k8]) * dot;

@@ -99,7 +99,12 @@ def compare_all(tag, got, ref, L, K, dtype, tol=None, inp=None):
     ro, rgv, rgs = ref
     assert_close(f"{tag} output", out, ro, rtol, atol)
     if gv is not None:
-        assert_close(f"{tag} grad_value", gv, rgv, rtol, atol)
+        xv = None
+        if dtype == torch.float32 and inp is not None:
+            xv = oracle.fp32_grad_value_allowance(
+                inp["value"].double().numpy(), inp["shapes"], inp["sampling_loc_attn"].double().numpy(),
+                inp["grad_output"].double().numpy(), inp["K"]).reshape(gv.shape)
+        assert_close(f"{tag} grad_value", gv, rgv, rtol, atol, xv)
         n = 3 * L * K
         extra = None
         if dtype == torch.float32 and inp is not None:

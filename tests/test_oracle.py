@@ -222,3 +222,39 @@ def test_level_meta():
     st, lsi = level_meta(((4, 8, 16), (2, 4, 8)), "cpu")
     assert st.tolist() == [[4, 8, 16], [2, 4, 8]]
     assert lsi.tolist() == [0, 512]
+
+
+def test_oracle_term_counts():
+    """abs_mode=2: grad_value holds each element's number of terms -- whole numbers, the same
+    for every channel, summing to D x (in-volume corners of all samples), counted here
+    independently from the fp32 pixel coordinates."""
+    shapes = [(3, 4, 5), (2, 2, 3)]
+    B, Q, G, D, K = 1, 17, 2, 4, 4
+    L = len(shapes)
+    v, sla, go = (t.numpy() for t in _inputs(shapes, B, Q, G, D, K, seed=7, lo=-0.2, hi=1.2))
+    n, _ = oracle.backward(v, shapes, sla, go, K, coord_mode=1, abs_mode=2)
+    assert np.all(n == np.round(n)) and np.all(n >= 0)
+    assert np.all(n == n[..., :1])
+
+    def pix(loc, size):   # torch grid_sample's fp32 rounding, as the oracle's coord_mode=1
+        l = np.float32(loc)
+        t = np.float32(np.float32(np.float32(np.float32(2.0) * l) - np.float32(1.0)) + np.float32(1.0))
+        return float(np.float32(np.float32(np.float32(t * np.float32(size)) - np.float32(1.0)) * np.float32(0.5)))
+
+    corners = 0
+    for b in range(B):
+        for q in range(Q):
+            for g in range(G):
+                rec = sla[b, q, g]
+                for l, (dd, hh, ww) in enumerate(shapes):
+                    for k in range(K):
+                        s = l * K + k
+                        x, y, z = pix(rec[3 * s], ww), pix(rec[3 * s + 1], hh), pix(rec[3 * s + 2], dd)
+                        if not (-1 <= x < ww and -1 <= y < hh and -1 <= z < dd):
+                            continue
+                        x0, y0, z0 = math.floor(x), math.floor(y), math.floor(z)
+                        for dz in (0, 1):
+                            for dy in (0, 1):
+                                for dx in (0, 1):
+                                    corners += (0 <= x0 + dx < ww) and (0 <= y0 + dy < hh) and (0 <= z0 + dz < dd)
+    assert n.sum() == D * corners
