@@ -759,24 +759,23 @@ void fda_bwd_tile_kernel(const Args a) {
       }
       __syncthreads();
       TILE_MARK(1);
-      // 1b. grad_output rows into LDS, 16-byte pieces spread over all threads (loads first)
+      // 1b. grad_output rows into LDS: 16-byte pieces loaded by the memory unit straight into
+      // LDS (global_load_lds_dwordx4: lane k of a wave fills base + 16*k), no registers held;
+      // piece i of the chunk is row i / PPR, part i % PPR.  A wave's last instruction may fill
+      // pieces past n*PPR with copies of the last piece: they stay inside the chunk's row
+      // buffer (CH * PPR is a multiple of 64) and are never read.
       {
         constexpr int PPR = RB / 16;                 // pieces per row
         const int np = n * PPR;
-        for (int i0 = 0; i0 < np; i0 += 4 * NT) {
-          u32x4 v[4];
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const int i = min(i0 + k * NT + tid, np - 1);
-            const int e = i / PPR, q = i - e * PPR;
-            v[k] = reinterpret_cast<const u32x4 *>(go + (size_t)rowi_l[e] * (uint32_t)D)[q];
-          }
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const int i = i0 + k * NT + tid;
-            if (i < np) reinterpret_cast<u32x4 *>(row_l)[i] = v[k];
-          }
+        const int lane = tid & (kWave - 1);
+        for (int base = tid - lane; base < np; base += NT) {
+          const int i = min(base + lane, np - 1);
+          const int e = i / PPR, q = i - e * PPR;
+          const u32x4 *src = reinterpret_cast<const u32x4 *>(go + (size_t)rowi_l[e] * (uint32_t)D) + q;
+          __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(row_l + (size_t)base * 16),
+                                           16, 0, 0);
         }
+        __builtin_amdgcn_s_waitcnt(0);   // the pieces are in LDS before the barrier below
       }
       // 2. bin starts: thread tid scans bins [tid*per, (tid+1)*per)
       {
