@@ -217,7 +217,7 @@ int tile_chunk(int D, int e, int lpu) {
 #endif
   const size_t budget = (nt >= 1024 ? 150 : (nt >= 512 ? 76 : OPS3D_FDA_TILE_LDS_KB_256)) * (size_t)1024;
   if (budget <= bins) return 0;
-  int ch = (int)((budget - bins) / (size_t)(rb + 24));
+  int ch = (int)((budget - bins) / (size_t)(rb + 20));
   ch = ch > kTileKPT * nt ? kTileKPT * nt : ch;
   ch &= ~63;
   return ch;

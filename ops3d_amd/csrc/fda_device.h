@@ -525,7 +525,7 @@ inline size_t tile_kernel_lds_bytes(int chunk, int row_bytes, int lpu) {
   int tx, ty, tz;
   tile_dims(lpu, tx, ty, tz);
   const size_t nb = (size_t)(tx + 1) * (ty + 1) * (tz + 1);
-  return (size_t)chunk * (16 + (size_t)row_bytes + 8) + (2 * nb + 1) * 4 + 4;
+  return (size_t)chunk * (16 + (size_t)row_bytes + 4) + (2 * nb + 1) * 4;
 }
 
 struct LevelTiles {

@@ -658,13 +658,12 @@ void fda_bwd_tile_kernel(const Args a) {
   constexpr int RB = CPL * LPU * (int)sizeof(T);   // bytes of a grad_output row (D = CPL*LPU)
   const int CH = a.chunk;                          // <= kTileKPT * NT
   const int NBX = (a.TX + 1) * (a.TY + 1) * (a.TZ + 1);
+  // a chunk's entries in LDS in bin-sorted order: stash, grad_output row, row index
   float4 *st_l = reinterpret_cast<float4 *>(tsm);
   unsigned char *row_l = tsm + (size_t)CH * 16;
   uint32_t *start_l = reinterpret_cast<uint32_t *>(row_l + (size_t)CH * RB);   // [NBX + 1]
   uint32_t *cur_l = start_l + NBX + 1;                                        // [NBX]
-  uint16_t *lbin_l = reinterpret_cast<uint16_t *>(cur_l + NBX);               // [CH]
-  uint16_t *sorted_l = lbin_l + CH;                                          // [CH]
-  uint32_t *rowi_l = reinterpret_cast<uint32_t *>(sorted_l + CH + (CH & 1));  // [CH]
+  uint32_t *rowi_l = cur_l + NBX;                                             // [CH]
 
   // owner: x-pair p of the nominal tile, channel chunk j
   const int p = tid / LPU, j = tid & (LPU - 1);
@@ -731,52 +730,24 @@ void fda_bwd_tile_kernel(const Args a) {
       for (int i = tid; i < nb; i += NT) cur_l[i] = 0u;
       __syncthreads();
       TILE_MARK(0);
-      // 1a. entries: local bin, stash, grad_output row index; bin counts.  All global loads of
-      // the thread's entries are issued before any is used.
-      {
-        uint2 en[kTileKPT];
-#pragma unroll
-        for (int k = 0; k < kTileKPT; ++k) {
-          const int e = tid + k * NT;
-          en[k] = a.entries[c0 + (e < n ? e : 0)];
-        }
-        float4 st[kTileKPT];   // unconditional loads (entry 0 stands in for absent ones): no scratch
-#pragma unroll
-        for (int k = 0; k < kTileKPT; ++k) st[k] = a.stash[en[k].x];
-#pragma unroll
-        for (int k = 0; k < kTileKPT; ++k) {
-          const int e = tid + k * NT;
-          if (e < n) {
-            const uint32_t w = en[k].y;
-            const uint32_t lb = ((w >> 10) & 31u) * (uint32_t)TYp * (uint32_t)TXp +
-                                ((w >> 5) & 31u) * (uint32_t)TXp + (w & 31u);
-            lbin_l[e] = (uint16_t)lb;
-            st_l[e] = st[k];
-            rowi_l[e] = (uint32_t)(((double)en[k].x + 0.5) * a.inv_lk);   // sample / (L*K), exact
-            atomicAdd(&cur_l[lb], 1u);
-          }
-        }
-      }
+      // 1a. the thread's two entries (registers): local bin, stash, grad_output row index; bin
+      // counts.  All global loads are issued before any is used; an absent entry reads entry 0
+      // (unconditional loads keep everything in registers).
+      static_assert(kTileKPT == 2, "two entries per thread and chunk");
+      const int eA = tid, eB = tid + NT;
+      const bool hA = eA < n, hB = eB < n;
+      const uint2 enA = a.entries[c0 + (hA ? eA : 0)], enB = a.entries[c0 + (hB ? eB : 0)];
+      const float4 stA = a.stash[enA.x], stB = a.stash[enB.x];
+      const auto local_bin = [&](uint32_t w) {
+        return ((w >> 10) & 31u) * (uint32_t)TYp * (uint32_t)TXp + ((w >> 5) & 31u) * (uint32_t)TXp + (w & 31u);
+      };
+      const uint32_t lbA = local_bin(enA.y), lbB = local_bin(enB.y);
+      const uint32_t riA = (uint32_t)(((double)enA.x + 0.5) * a.inv_lk);   // sample / (L*K), exact
+      const uint32_t riB = (uint32_t)(((double)enB.x + 0.5) * a.inv_lk);
+      if (hA) atomicAdd(&cur_l[lbA], 1u);
+      if (hB) atomicAdd(&cur_l[lbB], 1u);
       __syncthreads();
       TILE_MARK(1);
-      // 1b. grad_output rows into LDS: 16-byte pieces loaded by the memory unit straight into
-      // LDS (global_load_lds_dwordx4: lane k of a wave fills base + 16*k), no registers held;
-      // piece i of the chunk is row i / PPR, part i % PPR.  A wave's last instruction may fill
-      // pieces past n*PPR with copies of the last piece: they stay inside the chunk's row
-      // buffer (CH * PPR is a multiple of 64) and are never read.
-      {
-        constexpr int PPR = RB / 16;                 // pieces per row
-        const int np = n * PPR;
-        const int lane = tid & (kWave - 1);
-        for (int base = tid - lane; base < np; base += NT) {
-          const int i = min(base + lane, np - 1);
-          const int e = i / PPR, q = i - e * PPR;
-          const u32x4 *src = reinterpret_cast<const u32x4 *>(go + (size_t)rowi_l[e] * (uint32_t)D) + q;
-          __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(row_l + (size_t)base * 16),
-                                           16, 0, 0);
-        }
-        __builtin_amdgcn_s_waitcnt(0);   // the pieces are in LDS before the barrier below
-      }
       // 2. bin starts: thread tid scans bins [tid*per, (tid+1)*per)
       {
         const int per = (nb + NT - 1) / NT;
@@ -796,10 +767,35 @@ void fda_bwd_tile_kernel(const Args a) {
       }
       __syncthreads();
       TILE_MARK(2);
-      // 3. counting sort by bin
-      for (int e = tid; e < n; e += NT) {
-        const uint32_t pos = atomicAdd(&cur_l[lbin_l[e]], 1u);
-        sorted_l[pos] = (uint16_t)e;
+      // 3. counting sort by bin: each entry's stash and row index go to its sorted position
+      if (hA) {
+        const uint32_t pos = atomicAdd(&cur_l[lbA], 1u);
+        st_l[pos] = stA;
+        rowi_l[pos] = riA;
+      }
+      if (hB) {
+        const uint32_t pos = atomicAdd(&cur_l[lbB], 1u);
+        st_l[pos] = stB;
+        rowi_l[pos] = riB;
+      }
+      __syncthreads();
+      // 3b. grad_output rows into LDS in sorted order: 16-byte pieces loaded by the memory unit
+      // straight into LDS (global_load_lds_dwordx4: lane k of a wave fills base + 16*k), no
+      // registers held; piece i is part i % PPR of the row of sorted entry i / PPR.  A wave's
+      // last instruction may fill pieces past n*PPR with copies of the last piece: they stay
+      // inside the chunk's row buffer (CH * PPR is a multiple of 64) and are never read.
+      {
+        constexpr int PPR = RB / 16;                 // pieces per row
+        const int np = n * PPR;
+        const int lane = tid & (kWave - 1);
+        for (int base = tid - lane; base < np; base += NT) {
+          const int i = min(base + lane, np - 1);
+          const int e = i / PPR, q = i - e * PPR;
+          const u32x4 *src = reinterpret_cast<const u32x4 *>(go + (size_t)rowi_l[e] * (uint32_t)D) + q;
+          __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(row_l + (size_t)base * 16),
+                                           16, 0, 0);
+        }
+        __builtin_amdgcn_s_waitcnt(0);   // the pieces are in LDS before the barrier below
       }
       __syncthreads();
       TILE_MARK(3);
@@ -814,10 +810,9 @@ void fda_bwd_tile_kernel(const Args a) {
           const uint32_t s3 = two ? start_l[rb + 3] : m2;
 #pragma unroll 2
           for (uint32_t i = s0; i < s3; ++i) {
-            const int slot = sorted_l[i];
-            const float4 st = st_l[slot];
+            const float4 st = st_l[i];
             uint32_t wv[NW];
-            const uint32_t *rw = reinterpret_cast<const uint32_t *>(row_l + (size_t)slot * RB + j * EB);
+            const uint32_t *rw = reinterpret_cast<const uint32_t *>(row_l + (size_t)i * RB + j * EB);
 #pragma unroll
             for (int q = 0; q < NW; ++q) wv[q] = rw[q];
             float tg[CPL];
