@@ -21,6 +21,9 @@
 
 #include "fda_device.h"
 
+#ifndef OPS3D_FDA_TILE_UNROLL
+#define OPS3D_FDA_TILE_UNROLL 2   // entries in flight per owner loop step
+#endif
 #ifndef OPS3D_FDA_TILE_TIMING
 #define OPS3D_FDA_TILE_TIMING 0   // 1: per-phase cycle counts of the tile kernel into Args::dbg
 #endif
@@ -670,7 +673,22 @@ void fda_bwd_tile_kernel(const Args a) {
   const int hxn = a.TX / 2;
   const int px = p % hxn, py = (p / hxn) % a.TY, pz = p / (hxn * a.TY);
 
-  const uint32_t T_h = tiles_per_head(a.shapes, L, a.TX, a.TY, a.TZ);
+  // per level: tile geometry, first tile id within a head, voxel offset (read once)
+  __shared__ LevelTiles lvt[5];
+  __shared__ uint32_t lvbase[6];
+  __shared__ int64_t lvsi[5];
+  if (tid == 0) {
+    uint32_t t = 0;
+    for (int u = 0; u < L; ++u) {
+      lvt[u] = level_tiles(a.shapes, u, a.TX, a.TY, a.TZ);
+      lvbase[u] = t;
+      lvsi[u] = a.lsi[u];
+      t += lvt[u].count;
+    }
+    lvbase[L] = t;
+  }
+  __syncthreads();
+  const uint32_t T_h = lvbase[L];
   int xcd = 0, bi = blockIdx.x, nbx = gridDim.x, hpx = G;   // heads served by this block's group
   if (a.tile_affinity) {
     xcd = blockIdx.x & 7;
@@ -696,15 +714,15 @@ void fda_bwd_tile_kernel(const Args a) {
 #endif
   for (uint32_t k = (uint32_t)bi; k < total; k += (uint32_t)nbx) {
     // k -> (level, head, tile), coarse (last) levels first
-    uint32_t rem = k, lbase = 0;
+    uint32_t rem = k;
     int l = L - 1;
     for (; l > 0; --l) {
-      const uint32_t nl = nbg * level_tiles(a.shapes, l, a.TX, a.TY, a.TZ).count;
+      const uint32_t nl = nbg * lvt[l].count;
       if (rem < nl) break;
       rem -= nl;
     }
-    for (int u = 0; u < l; ++u) lbase += level_tiles(a.shapes, u, a.TX, a.TY, a.TZ).count;
-    const LevelTiles lt = level_tiles(a.shapes, l, a.TX, a.TY, a.TZ);
+    const uint32_t lbase = lvbase[l];
+    const LevelTiles lt = lvt[l];
     const uint32_t bgi = rem / lt.count, t = rem - bgi * lt.count;
     const int b = (int)(bgi / (uint32_t)hpx);
     const int g = a.tile_affinity ? xcd + 8 * (int)(bgi % (uint32_t)hpx) : (int)(bgi % (uint32_t)hpx);
@@ -808,7 +826,7 @@ void fda_bwd_tile_kernel(const Args a) {
           const int rb = ((pz - dz + 1) * TYp + (py - dy + 1)) * TXp + 2 * px;
           const uint32_t s0 = start_l[rb], m1 = start_l[rb + 1], m2 = start_l[rb + 2];
           const uint32_t s3 = two ? start_l[rb + 3] : m2;
-#pragma unroll 2
+#pragma unroll OPS3D_FDA_TILE_UNROLL
           for (uint32_t i = s0; i < s3; ++i) {
             const float4 st = st_l[i];
             uint32_t wv[NW];
@@ -838,7 +856,7 @@ void fda_bwd_tile_kernel(const Args a) {
       TILE_MARK(4);
     }
     if (live) {
-      const int64_t vox = a.lsi[l] + ((int64_t)z * Hl + y) * Wl + x0;
+      const int64_t vox = lvsi[l] + ((int64_t)z * Hl + y) * Wl + x0;
       const int64_t o = (((int64_t)b * a.S + vox) * G + g) * D + j * CPL;
       for (int h = 0; h < (two ? 2 : 1); ++h) {
         float res[CPL];
