@@ -29,7 +29,7 @@ hipError_t launch_f16(int, int, int, const Args &, unsigned, size_t, hipStream_t
 hipError_t launch_bf16(int, int, int, const Args &, unsigned, size_t, hipStream_t);
 hipError_t launch_tile_bucketing(const uint32_t *keys, const uint32_t *words, uint32_t n, uint32_t per_head,
                                  const int64_t *shapes, int L, int BG, int TX, int TY, int TZ, uint32_t *counts,
-                                 uint32_t *start, uint32_t *cursor, uint32_t *mat, uint32_t tcap, uint2 *entries,
+                                 uint32_t *start, uint32_t *cursor, uint32_t *mat, uint32_t tcap, uint32_t *entries, uint32_t *queue,
                                  hipStream_t st, void (*mark)(int, hipStream_t));
 size_t tile_matrix_words(uint32_t BG, uint32_t tcap);
 }  // namespace ops3d_fda
@@ -164,17 +164,18 @@ hipError_t launch(int dtype, int which, const Geometry &g, hipStream_t st) {
 
 // Workspace of the backward (all offsets 256-byte aligned):
 //   keys, words    : N uint32 each, N = B*Q*G*L*K samples (home tile, tile-local word)
-//   stash          : N float4 (fx, fy, fz, attn)
-//   entries        : 8N uint2 (a sample is listed in at most 8 tiles)
+//   stash          : N float4 (x, y, z, attn), level pixel coordinates
+//   entries        : 8N uint32 sample indices (a sample is listed in at most 8 tiles)
 //   counts, start, cursor : B*G*S + 1 uint32 each (a tile holds at least one voxel, so a head
 //                    has at most S tiles)
 //   bucketing matrix: B*G x 64 blocks x tcap uint32, tcap = S/16 + 64 tiles per head (volumes
 //                    cut into more tiles are bucketed with global atomics instead)
+//   tile queues    : 8 uint32 (the tile kernel's per-XCD work counters, cleared by the bucketing)
 //   head-major copies of value and grad_output (G > 1)
 struct BwdLayout {
   uint64_t n, ntiles_bound;
   uint32_t tcap;
-  size_t off_keys, off_words, off_stash, off_entries, off_counts, off_start, off_cursor, off_mat, off_vhm, off_ghm;
+  size_t off_keys, off_words, off_stash, off_entries, off_counts, off_start, off_cursor, off_queue, off_mat, off_vhm, off_ghm;
   size_t total;
 };
 
@@ -193,10 +194,11 @@ int bwd_layout(int B, int S, int G, int D, int e, int L, int Q, int K, BwdLayout
   ly.off_keys = o; o += n4;
   ly.off_words = o; o += n4;
   ly.off_stash = o; o += align256(ly.n * 16);
-  ly.off_entries = o; o += align256(ly.n * 8 * 8);
+  ly.off_entries = o; o += align256(ly.n * 8 * 4);
   ly.off_counts = o; o += t4;
   ly.off_start = o; o += t4;
   ly.off_cursor = o; o += t4;
+  ly.off_queue = o; o += 256;
   ly.tcap = (uint32_t)(S / 16 + 64);
   ly.off_mat = o; o += align256(tile_matrix_words((uint32_t)(B * G), ly.tcap) * 4);
   ly.off_vhm = o; o += G > 1 ? align256((size_t)B * S * G * D * e) : 0;
@@ -372,7 +374,7 @@ static int backward_impl(const void *value, const void *value_head_major, const 
   uint32_t *keys = reinterpret_cast<uint32_t *>(ws + ly.off_keys);
   uint32_t *words = reinterpret_cast<uint32_t *>(ws + ly.off_words);
   float4 *stash = reinterpret_cast<float4 *>(ws + ly.off_stash);
-  uint2 *entries = reinterpret_cast<uint2 *>(ws + ly.off_entries);
+  uint32_t *entries = reinterpret_cast<uint32_t *>(ws + ly.off_entries);
   uint32_t *counts = reinterpret_cast<uint32_t *>(ws + ly.off_counts);
   uint32_t *tstart = reinterpret_cast<uint32_t *>(ws + ly.off_start);
   uint32_t *cursor = reinterpret_cast<uint32_t *>(ws + ly.off_cursor);
@@ -391,6 +393,7 @@ static int backward_impl(const void *value, const void *value_head_major, const 
   a.tile_start = tstart;
   a.tile_cursor = cursor;
   a.entries = entries;
+  a.tile_queue = reinterpret_cast<uint32_t *>(ws + ly.off_queue);
   tile_dims(tile_lanes(geo.lpu, geo.cpl * elem_size(dtype)), a.TX, a.TY, a.TZ);
   a.inv_lk = 1.0 / (double)(num_levels * num_point);
   hipError_t e;
@@ -422,7 +425,8 @@ static int backward_impl(const void *value, const void *value_head_major, const 
   e = launch_tile_bucketing(keys, words, work ? (uint32_t)ly.n : 0u,
                             (uint32_t)num_query * (uint32_t)(num_levels * num_point), spatial_shapes, num_levels,
                             batch * num_heads, a.TX, a.TY, a.TZ, counts, tstart, cursor,
-                            reinterpret_cast<uint32_t *>(ws + ly.off_mat), ly.tcap, entries, st,
+                            reinterpret_cast<uint32_t *>(ws + ly.off_mat), ly.tcap, entries,
+                            reinterpret_cast<uint32_t *>(ws + ly.off_queue), st,
                             g_prof_on ? prof_mark : nullptr);
   if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "tile bucketing failed: %s", hipGetErrorString(e));
   prof_mark(4, st);

@@ -45,11 +45,12 @@ struct Args {
   // backward, tile formulation of grad_value
   uint32_t *keys;             // [N] home tile of each sample's base corner (kKeyInvalid if outside)
   uint32_t *vals;             // [N] tile-local base corner word of each sample (tile_word)
-  float4 *stash;              // [N] (fx, fy, fz, attn) of each sample
+  float4 *stash;              // [N] (x, y, z, attn) of each sample: level pixel coordinates
   uint32_t *tile_counts;      // [B*G*T_h] entries per tile
   uint32_t *tile_start;       // [B*G*T_h] first entry of each tile (head base + exclusive scan)
   uint32_t *tile_cursor;      // [B*G*T_h] fill cursor of each tile
-  uint2 *entries;             // [<= 8N] (sample, tile-local base corner word), grouped by tile
+  uint32_t *tile_queue;       // [8] tile kernel work counters (one per XCD group), zero at launch
+  uint32_t *entries;          // [<= 8N] sample indices, grouped by tile
   int TX, TY, TZ;             // nominal tile dimensions (voxels), clipped per level
   int chunk;                  // entries per LDS chunk of the tile kernel
   int tile_affinity;          // tiles of head g run on XCD g % 8 (G % 8 == 0)

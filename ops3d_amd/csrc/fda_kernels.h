@@ -31,6 +31,16 @@
 #define OPS3D_FDA_TILE_WPE 4    // minimum waves per SIMD the tile kernel is compiled for
 #endif
 
+// Occupancy hint of the backward query kernel (waves per SIMD it is compiled for; 0: none).
+#ifndef OPS3D_FDA_QUERY_WPE
+#define OPS3D_FDA_QUERY_WPE 0
+#endif
+#if OPS3D_FDA_QUERY_WPE > 0
+#define OPS3D_FDA_QUERY_ATTR __attribute__((amdgpu_waves_per_eu(OPS3D_FDA_QUERY_WPE)))
+#else
+#define OPS3D_FDA_QUERY_ATTR
+#endif
+
 namespace ops3d_fda {
 
 // NW raw words from a plain global pointer (aligned to 16 bytes when NW % 4 == 0).
@@ -269,7 +279,7 @@ __global__ __launch_bounds__(kBlock) void fda_forward_pair_kernel(const Args a) 
 // the lane that made a set-up also records that sample's stash and base corner.  The partials
 // of grad_loc / grad_attn of a lane's x-row are summed over the unit's 8 lanes.
 template <typename T, int CPL>
-__global__ __launch_bounds__(kBlock) void fda_bwd_query_pair_kernel(const Args a) {
+__global__ __launch_bounds__(kBlock) OPS3D_FDA_QUERY_ATTR void fda_bwd_query_pair_kernel(const Args a) {
   extern __shared__ float lds[];
   constexpr int UL = 8;
   constexpr int UPW = kWave / UL, UPB = kWavesPerBlock * UPW;
@@ -312,7 +322,11 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_pair_kernel(const Args a
   uint32_t tgw[NW];
   if (live) {
     load_global_words<NW>(static_cast<const T *>(a.grad_out) + unit * a.D + j * CPL, tgw);
+#ifdef EXP_NO_GOUTHM
+    if (false) {
+#else
     if (a.gout_hm && dxl == 0) {   // the row again, head-major, for the tile kernel
+#endif
       uint32_t *dst = reinterpret_cast<uint32_t *>(static_cast<T *>(a.gout_hm) +
                                                    (((int64_t)b * a.G + g) * a.Q + q) * a.D + j * CPL);
 #pragma unroll
@@ -343,7 +357,9 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_pair_kernel(const Args a
         cx_s[sj] = in_s ? (uint32_t)(ms.x0 + 1) : kKeyInvalid;
         cy_s[sj] = (uint32_t)(ms.y0 + 1);
         cz_s[sj] = (uint32_t)(ms.z0 + 1);
-        st_s[sj] = make_float4(ms.wx[1], ms.wy[1], ms.wz[1], rec[3 * LK + sj]);
+        // pixel coordinates (base corner + fraction: exact), from which the tile kernel takes both
+        st_s[sj] = make_float4((float)ms.x0 + ms.wx[1], (float)ms.y0 + ms.wy[1], (float)ms.z0 + ms.wz[1],
+                               rec[3 * LK + sj]);
       }
       uint32_t off4[4];
 #pragma unroll
@@ -401,6 +417,7 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_pair_kernel(const Args a
   }
   wave_lds_sync();
   {
+#ifndef EXP_NO_WRITEOUT
     // the wave's units are consecutive q of one (b, g): their samples are one contiguous range
     const int q0 = qb * UPB + wave * UPW;
     const int nlive = min(UPW, a.Q - q0);
@@ -426,6 +443,14 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_pair_kernel(const Args a
         a.stash[gs0 + e] = stx[ss];
       }
     }
+#else
+    {
+      const int q0 = qb * UPB + wave * UPW;
+      const int nlive = min(UPW, a.Q - q0);
+      const uint32_t gs0 = sample_index(b, g, q0, 0, a.G, a.Q, LK);
+      for (int e = lane; e < nlive * LK; e += kWave) a.keys[gs0 + e] = kKeyInvalid;
+    }
+#endif
   }
   // softmax backward over the unit's L*K attention weights
   float dot = 0.f;
@@ -565,7 +590,7 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
           cx_s[su] = in[u] ? (uint32_t)(m.x0 + 1) : kKeyInvalid;
           cy_s[su] = (uint32_t)(m.y0 + 1);
           cz_s[su] = (uint32_t)(m.z0 + 1);
-          st_s[su] = make_float4(m.wx[1], m.wy[1], m.wz[1], at[u]);
+          st_s[su] = make_float4((float)m.x0 + m.wx[1], (float)m.y0 + m.wy[1], (float)m.z0 + m.wz[1], at[u]);
         }
       }
     }
@@ -712,20 +737,61 @@ void fda_bwd_tile_kernel(const Args a) {
 #else
 #define TILE_MARK(i) ((void)0)
 #endif
-  for (uint32_t k = (uint32_t)bi; k < total; k += (uint32_t)nbx) {
-    // k -> (level, head, tile), coarse (last) levels first
+  // k -> (level, head, tile), coarse (last) levels first
+  const auto decode = [&](uint32_t k, int &l, uint32_t &bgi, uint32_t &t) {
     uint32_t rem = k;
-    int l = L - 1;
+    l = L - 1;
     for (; l > 0; --l) {
       const uint32_t nl = nbg * lvt[l].count;
       if (rem < nl) break;
       rem -= nl;
     }
-    const uint32_t lbase = lvbase[l];
+    bgi = rem / lvt[l].count;
+    t = rem - bgi * lvt[l].count;
+  };
+  const auto head_of = [&](uint32_t bgi, int &b, int &g) {
+    b = (int)(bgi / (uint32_t)hpx);
+    g = a.tile_affinity ? xcd + 8 * (int)(bgi % (uint32_t)hpx) : (int)(bgi % (uint32_t)hpx);
+  };
+  const auto tile_gid = [&](uint32_t k) {
+    int l, b, g;
+    uint32_t bgi, t;
+    decode(k, l, bgi, t);
+    head_of(bgi, b, g);
+    return (uint32_t)(b * G + g) * T_h + lvbase[l] + t;
+  };
+  // Tiles: the block's first two are bi and bi + nbx; after them each block takes the next
+  // unclaimed tile of its XCD group from a work counter (one atomic per tile, made a tile ahead),
+  // so blocks that drew light tiles take more of them.
+  // Software pipeline: the entries of the block's next chunk are loaded when a chunk starts and
+  // their stash before its rows are loaded, so both arrive during the owner phase; tile headers
+  // (first entry, count) are loaded a tile ahead of use.
+  __shared__ uint32_t grab_l[2];
+  uint32_t k1 = (uint32_t)bi + (uint32_t)nbx;      // the next tile
+  uint32_t h0s = 0, h0c = 0, h1s = 0, h1c = 0;     // headers of the current and the next tile
+  if ((uint32_t)bi < total) {
+    const uint32_t gid = tile_gid((uint32_t)bi);
+    h0s = a.tile_start[gid];
+    h0c = a.tile_counts[gid];
+  }
+  if (k1 < total) {
+    const uint32_t gid = tile_gid(k1);
+    h1s = a.tile_start[gid];
+    h1c = a.tile_counts[gid];
+  }
+  bool pf = false;               // the current chunk's entries and stash are in pA.. / psA..
+  uint32_t pA = 0, pB = 0;
+  float4 psA = make_float4(0.f, 0.f, 0.f, 0.f), psB = psA;
+  int par = 0;
+  for (uint32_t k = (uint32_t)bi; k < total; par ^= 1) {
+    // claim the tile after the next one (read after this tile's barriers)
+    if (tid == 0)
+      grab_l[par] = k1 < total ? 2u * (uint32_t)nbx + atomicAdd(a.tile_queue + xcd, 1u) : total;
+    int l, b, g;
+    uint32_t bgi, t;
+    decode(k, l, bgi, t);
+    head_of(bgi, b, g);
     const LevelTiles lt = lvt[l];
-    const uint32_t bgi = rem / lt.count, t = rem - bgi * lt.count;
-    const int b = (int)(bgi / (uint32_t)hpx);
-    const int g = a.tile_affinity ? xcd + 8 * (int)(bgi % (uint32_t)hpx) : (int)(bgi % (uint32_t)hpx);
     const int itx = (int)(t % (uint32_t)lt.nt[2]);
     const int ity = (int)((t / (uint32_t)lt.nt[2]) % (uint32_t)lt.nt[1]);
     const int itz = (int)(t / ((uint32_t)lt.nt[2] * (uint32_t)lt.nt[1]));
@@ -734,8 +800,8 @@ void fda_bwd_tile_kernel(const Args a) {
     const int z = itz * tz + pz, y = ity * ty + py, x0 = itx * tx + 2 * px;
     const bool live = 2 * px < tx && py < ty && pz < tz && z < Dl && y < Hl && x0 < Wl;
     const bool two = 2 * px + 1 < tx && x0 + 1 < Wl;
-    const uint32_t gid = (uint32_t)(b * G + g) * T_h + lbase + t;
-    const uint32_t e0 = a.tile_start[gid], e1 = e0 + a.tile_counts[gid];
+    const uint32_t e0 = h0s, e1 = h0s + h0c;
+    const uint32_t ns = h1s, nc = h1c;   // next tile's header
     const int TXp = tx + 1, TYp = ty + 1;
     const int nb = TXp * TYp * (tz + 1);
 
@@ -745,25 +811,53 @@ void fda_bwd_tile_kernel(const Args a) {
 
     for (uint32_t c0 = e0; c0 < e1; c0 += (uint32_t)CH) {
       const int n = (int)min((uint32_t)CH, e1 - c0);
-      for (int i = tid; i < nb; i += NT) cur_l[i] = 0u;
-      __syncthreads();
-      TILE_MARK(0);
-      // 1a. the thread's two entries (registers): local bin, stash, grad_output row index; bin
-      // counts.  All global loads are issued before any is used; an absent entry reads entry 0
-      // (unconditional loads keep everything in registers).
       static_assert(kTileKPT == 2, "two entries per thread and chunk");
       const int eA = tid, eB = tid + NT;
       const bool hA = eA < n, hB = eB < n;
-      const uint2 enA = a.entries[c0 + (hA ? eA : 0)], enB = a.entries[c0 + (hB ? eB : 0)];
-      const float4 stA = a.stash[enA.x], stB = a.stash[enB.x];
-      const auto local_bin = [&](uint32_t w) {
-        return ((w >> 10) & 31u) * (uint32_t)TYp * (uint32_t)TXp + ((w >> 5) & 31u) * (uint32_t)TXp + (w & 31u);
+      // this chunk's entries and stash (prefetched, or loaded now); an absent entry reads entry 0
+      // (unconditional loads keep everything in registers)
+      uint32_t enA, enB;
+      float4 stA, stB;
+      if (pf) {
+        enA = pA; enB = pB; stA = psA; stB = psB;
+      } else {
+        enA = a.entries[c0 + (hA ? eA : 0)];
+        enB = a.entries[c0 + (hB ? eB : 0)];
+        stA = a.stash[enA];
+        stB = a.stash[enB];
+      }
+      // the next chunk: the rest of this tile, or the next tile's first chunk
+      const bool nxt_here = c0 + (uint32_t)CH < e1;
+      const uint32_t nc0 = nxt_here ? c0 + (uint32_t)CH : ns;
+      const uint32_t nn = nxt_here ? min((uint32_t)CH, e1 - nc0) : min((uint32_t)CH, nc);
+      const bool npf = nxt_here || (k1 < total && nc > 0);
+      for (int i = tid; i < nb; i += NT) cur_l[i] = 0u;
+      __syncthreads();
+      TILE_MARK(0);
+      // 1a. local bin of each entry's base corner, grad_output row index, bin counts.  The stash
+      // holds the pixel coordinates: base corner = floor, fraction = coordinate - floor (exact).
+      const int ox = itx * tx - 1, oy = ity * ty - 1, oz = itz * tz - 1;   // bin 0 = local -1
+      const auto local_bin = [&](float4 &st) {
+        const float xf = floorf(st.x), yf = floorf(st.y), zf = floorf(st.z);
+        const uint32_t bin = ((uint32_t)((int)zf - oz) * (uint32_t)TYp + (uint32_t)((int)yf - oy)) * (uint32_t)TXp +
+                             (uint32_t)((int)xf - ox);
+        st.x -= xf;
+        st.y -= yf;
+        st.z -= zf;
+        return bin;
       };
-      const uint32_t lbA = local_bin(enA.y), lbB = local_bin(enB.y);
-      const uint32_t riA = (uint32_t)(((double)enA.x + 0.5) * a.inv_lk);   // sample / (L*K), exact
-      const uint32_t riB = (uint32_t)(((double)enB.x + 0.5) * a.inv_lk);
+      const uint32_t lbA = local_bin(stA), lbB = local_bin(stB);
+      const uint32_t riA = (uint32_t)(((double)enA + 0.5) * a.inv_lk);   // sample / (L*K), exact
+      const uint32_t riB = (uint32_t)(((double)enB + 0.5) * a.inv_lk);
       if (hA) atomicAdd(&cur_l[lbA], 1u);
       if (hB) atomicAdd(&cur_l[lbB], 1u);
+      // the next chunk's entries, issued after this chunk's stash is used (loads complete in order,
+      // so a wait for the stash would also wait for them; the scheduling barrier keeps them here)
+      __builtin_amdgcn_sched_barrier(0);
+      if (npf) {
+        pA = a.entries[nc0 + ((uint32_t)eA < nn ? (uint32_t)eA : 0u)];
+        pB = a.entries[nc0 + ((uint32_t)eB < nn ? (uint32_t)eB : 0u)];
+      }
       __syncthreads();
       TILE_MARK(1);
       // 2. bin starts: thread tid scans bins [tid*per, (tid+1)*per)
@@ -797,6 +891,11 @@ void fda_bwd_tile_kernel(const Args a) {
         rowi_l[pos] = riB;
       }
       __syncthreads();
+      if (npf) {   // the next chunk's stash (its entries have arrived by now)
+        psA = a.stash[pA];
+        psB = a.stash[pB];
+      }
+      pf = npf;
       // 3b. grad_output rows into LDS in sorted order: 16-byte pieces loaded by the memory unit
       // straight into LDS (global_load_lds_dwordx4: lane k of a wave fills base + 16*k), no
       // registers held; piece i is part i % PPR of the row of sorted entry i / PPR.  A wave's
@@ -876,6 +975,17 @@ void fda_bwd_tile_kernel(const Args a) {
       }
     }
     TILE_MARK(5);
+    if (e0 == e1) __syncthreads();   // the claim is read after a barrier of this tile
+    const uint32_t k2 = grab_l[par];
+    uint32_t h2s = 0, h2c = 0;
+    if (k2 < total) {
+      const uint32_t gid = tile_gid(k2);
+      h2s = a.tile_start[gid];
+      h2c = a.tile_counts[gid];
+    }
+    k = k1; k1 = k2;
+    h0s = ns; h0c = nc;
+    h1s = h2s; h1c = h2c;
   }
 #if OPS3D_FDA_TILE_TIMING
   if (tid == 0 && a.dbg)

@@ -5,12 +5,13 @@
 // set, 1 to 8 entries.  A block handles a contiguous range of one head's samples (about 64
 // blocks per head) and keeps an LDS histogram over all of the head's tiles.
 //
-// Matrix mode (the head has at most min(tcap, kWin) tiles; tcap is what the workspace holds):
+// Matrix mode (the head has at most wcap = min(tcap, kWin) tiles; tcap is what the workspace
+// holds, and the LDS window is wcap tiles):
 //   tile_count:    each block writes its histogram as a row of a [head][block][tile] matrix,
 //   tile_headscan: one block per head: per tile, exclusive prefix over the head's blocks (in
 //                  place) and the tile's total; exclusive scan of the totals -> tile_start,
 //   tile_scatter:  block c's entries of tile t go to tile_start[t] + prefix[c][t] + their rank
-//                  among the block's entries of t (LDS atomics).
+//                  among the block's entries of t (LDS staging, below).
 //   No global atomics: every position is computed.
 // Atomic mode (more tiles): the histograms are flushed with global atomics into zeroed
 // counters, and tile_scatter reserves each block's range of a tile with one global atomic on
@@ -25,7 +26,7 @@
 namespace ops3d_fda {
 
 constexpr int kBucketThreads = 1024;
-constexpr int kWin = 16384;                           // LDS histogram window (tiles of one head)
+constexpr int kWin = 8192;                            // LDS histogram window (tiles of one head)
 constexpr int kBlocksPerHead = 64;
 
 struct BucketArgs {
@@ -41,12 +42,14 @@ struct BucketArgs {
   uint32_t *cursor;            // [BG * T_h]
   const uint32_t *start;       // [BG * T_h + 1]
   uint32_t *mat;               // [BG][blocks_per_head][T_h] (matrix mode)
-  uint32_t tcap;               // matrix mode when T_h <= min(tcap, kWin)
-  uint2 *entries;              // [<= 8N]
+  uint32_t tcap;               // matrix mode when T_h <= tcap
+  uint32_t wcap;               // LDS histogram window in tiles: min(tcap, kWin)
+  uint32_t *entries;           // [<= 8N] sample indices
+  uint32_t *queue;             // [8] the tile kernel's work counters, cleared here
 };
 
 __device__ __forceinline__ bool matrix_mode(const BucketArgs &a, uint32_t T_h) {
-  return T_h <= a.tcap && T_h <= (uint32_t)kWin;
+  return T_h <= a.wcap;
 }
 
 struct LevelGrid {
@@ -110,10 +113,10 @@ __device__ __forceinline__ void block_range(const BucketArgs &a, uint32_t &bg, u
 }
 
 __global__ __launch_bounds__(kBucketThreads) void tile_count_kernel(const BucketArgs a) {
-  extern __shared__ uint32_t win[];   // [kWin]
+  extern __shared__ uint32_t win[];   // [wcap]
   __shared__ LevelGrid lg[5];
   const uint32_t T_h = tiles_per_head(a.shapes, a.L, a.TX, a.TY, a.TZ);
-  const uint32_t nw = min(T_h, (uint32_t)kWin);
+  const uint32_t nw = min(T_h, a.wcap);
   if (threadIdx.x == 0) level_grids(a, lg);
   for (uint32_t i = threadIdx.x; i < nw; i += kBucketThreads) win[i] = 0u;
   __syncthreads();
@@ -140,16 +143,32 @@ __global__ __launch_bounds__(kBucketThreads) void tile_count_kernel(const Bucket
   }
 }
 
+// Entries are staged in LDS before they are written: a round of kRound samples is counted per
+// tile, scanned, and placed in LDS grouped by tile; the writes then go out in that order, so
+// consecutive lanes write consecutive positions of a tile's run instead of one scattered word
+// each.  An entry past the staging capacity is written directly at the same position.
+constexpr int kRound = 4096;        // samples per staging round (kRound / kBucketThreads per thread)
+constexpr int kStage = 8192;        // staged entries per round (a round holds 1.5-1.8 per sample
+                                    // on average, at most 8)
+constexpr int kRoundBits = 12;      // kRound == 1 << kRoundBits
+
+size_t tile_scatter_lds_bytes(uint32_t wcap) { return (size_t)kStage * 4 + (size_t)2 * (wcap + 1) * 4; }
+
 __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const BucketArgs a) {
-  extern __shared__ uint32_t win[];   // [kWin] counts, then the block's first position in each tile
-  uint32_t *rk = win + kWin;          // [kWin] rank counters
+  static_assert(kRound == (1 << kRoundBits), "round size");
+  extern __shared__ uint32_t lsm[];
+  uint32_t *rec = lsm;                    // [kStage] (tile - w0) << kRoundBits | (sample - round start)
+  uint32_t *win = rec + kStage;           // [wcap] next free position of the block in each tile
+  uint32_t *cur = win + a.wcap + 1;       // [wcap] per-round counts, then placement cursors
   __shared__ LevelGrid lg[5];
+  __shared__ uint32_t scan_tmp[kBucketThreads / kWave + 1];
   const uint32_t T_h = tiles_per_head(a.shapes, a.L, a.TX, a.TY, a.TZ);
-  const uint32_t nw = min(T_h, (uint32_t)kWin);
-  if (threadIdx.x == 0) level_grids(a, lg);
-  for (uint32_t i = threadIdx.x; i < nw; i += kBucketThreads) {
+  const uint32_t nw = min(T_h, a.wcap);
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
+  if (tid == 0) level_grids(a, lg);
+  for (uint32_t i = tid; i < nw; i += kBucketThreads) {
     win[i] = 0u;
-    rk[i] = 0u;
+    cur[i] = 0u;
   }
   __syncthreads();
   uint32_t bg, s0, s1;
@@ -159,11 +178,11 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
     // the block's first position in each tile: tile start + the earlier blocks' entries
     uint32_t hb, hc;
     const uint32_t *row = a.mat + (size_t)block_slot(a, hb, hc) * T_h;
-    for (uint32_t i = threadIdx.x; i < T_h; i += kBucketThreads) win[i] = a.start[w0 + i] + row[i];
+    for (uint32_t i = tid; i < T_h; i += kBucketThreads) win[i] = a.start[w0 + i] + row[i];
   } else {
-    // pass A: counts of the window's tiles, then one reservation per touched tile
+    // counts of the window's tiles, then one reservation per touched tile
 #pragma unroll 4
-    for (uint32_t s = s0 + threadIdx.x; s < s1; s += kBucketThreads) {
+    for (uint32_t s = s0 + tid; s < s1; s += kBucketThreads) {
       const uint32_t key = a.keys[s];
       if (key == kKeyInvalid) continue;
       for_each_entry(key, a.words[s], lg, [&](uint32_t id, uint32_t) {
@@ -171,21 +190,95 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
       });
     }
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < nw; i += kBucketThreads)
+    for (uint32_t i = tid; i < nw; i += kBucketThreads)
       if (win[i]) win[i] = atomicAdd(&a.cursor[w0 + i], win[i]);
   }
   __syncthreads();
-  // pass B: place the entries
-#pragma unroll 4
-  for (uint32_t s = s0 + threadIdx.x; s < s1; s += kBucketThreads) {
-    const uint32_t key = a.keys[s];
-    if (key == kKeyInvalid) continue;
-    for_each_entry(key, a.words[s], lg, [&](uint32_t id, uint32_t w) {
-      uint32_t pos;
-      if (id - w0 < nw) pos = win[id - w0] + atomicAdd(&rk[id - w0], 1u);
-      else pos = atomicAdd(&a.cursor[id], 1u);
-      a.entries[pos] = make_uint2(s, w);
-    });
+  constexpr int SPT = kRound / kBucketThreads;
+  const uint32_t per = (nw + kBucketThreads - 1) / kBucketThreads;   // tiles per thread in the scans
+  for (uint32_t r0 = s0; r0 < s1; r0 += kRound) {
+    uint32_t key[SPT], word[SPT];
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) {
+      const uint32_t s = r0 + (uint32_t)(k * kBucketThreads + tid);
+      key[k] = s < s1 ? a.keys[s] : kKeyInvalid;
+      word[k] = s < s1 ? a.words[s] : 0u;
+    }
+    // (a) the round's entries per tile; tiles outside the window take a position at once
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) {
+      if (key[k] == kKeyInvalid) continue;
+      const uint32_t s = r0 + (uint32_t)(k * kBucketThreads + tid);
+      for_each_entry(key[k], word[k], lg, [&](uint32_t id, uint32_t) {
+        if (id - w0 < nw) atomicAdd(&cur[id - w0], 1u);
+        else a.entries[atomicAdd(&a.cursor[id], 1u)] = s;
+      });
+    }
+    __syncthreads();
+    // (b) exclusive scan of the counts: cur = the tile's first staging slot; win -= that slot,
+    // so that staging slot i of tile t goes to win[t] + i
+    {
+      const uint32_t b0 = (uint32_t)tid * per;
+      uint32_t sum = 0;
+      for (uint32_t i = 0; i < per; ++i)
+        if (b0 + i < nw) sum += cur[b0 + i];
+      uint32_t inc = sum;
+#pragma unroll
+      for (int o = 1; o < kWave; o <<= 1) {
+        const uint32_t y = __shfl_up(inc, o, kWave);
+        if (lane >= o) inc += y;
+      }
+      if (lane == kWave - 1) scan_tmp[wv] = inc;
+      __syncthreads();
+      if (tid == 0) {
+        uint32_t run = 0;
+        for (int w = 0; w < kBucketThreads / kWave; ++w) {
+          const uint32_t t = scan_tmp[w];
+          scan_tmp[w] = run;
+          run += t;
+        }
+        scan_tmp[kBucketThreads / kWave] = run;
+      }
+      __syncthreads();
+      uint32_t run = scan_tmp[wv] + inc - sum;
+      for (uint32_t i = 0; i < per; ++i)
+        if (b0 + i < nw) {
+          const uint32_t c = cur[b0 + i];
+          cur[b0 + i] = run;
+          win[b0 + i] -= run;
+          run += c;
+        }
+    }
+    __syncthreads();
+    const uint32_t staged = min(scan_tmp[kBucketThreads / kWave], (uint32_t)kStage);
+    // (c) placement: staging slot by tile (LDS), or the final position past the capacity
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) {
+      if (key[k] == kKeyInvalid) continue;
+      const uint32_t so = (uint32_t)(k * kBucketThreads + tid);
+      for_each_entry(key[k], word[k], lg, [&](uint32_t id, uint32_t) {
+        const uint32_t t = id - w0;
+        if (t < nw) {
+          const uint32_t slot = atomicAdd(&cur[t], 1u);
+          if (slot < (uint32_t)kStage) rec[slot] = (t << kRoundBits) | so;
+          else a.entries[win[t] + slot] = r0 + so;
+        }
+      });
+    }
+    __syncthreads();
+    // (d) the staged entries in tile order: runs of consecutive positions
+    for (uint32_t i = tid; i < staged; i += kBucketThreads) {
+      const uint32_t v = rec[i];
+      const uint32_t t = v >> kRoundBits;
+      a.entries[win[t] + i] = r0 + (v & (uint32_t)(kRound - 1));
+    }
+    __syncthreads();
+    // (e) next free positions (cur ends at the tile's first slot + its count); counts cleared
+    for (uint32_t i = tid; i < nw; i += kBucketThreads) {
+      win[i] += cur[i];
+      cur[i] = 0u;
+    }
+    __syncthreads();
   }
 }
 
@@ -198,6 +291,7 @@ __global__ __launch_bounds__(1024) void tile_headscan_kernel(const BucketArgs a,
   const bool mat = matrix_mode(a, T_h);
   const uint32_t bg = blockIdx.x;
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+  if (bg == 0 && threadIdx.x < 8) a.queue[threadIdx.x] = 0u;
   uint32_t carry = bg * 8u * a.per_head;   // the head's entry range
   for (uint32_t base = 0; base < T_h; base += 1024) {
     const uint32_t t = base + threadIdx.x;
@@ -250,12 +344,15 @@ size_t tile_matrix_words(uint32_t BG, uint32_t tcap) { return (size_t)BG * kBloc
 
 hipError_t launch_tile_bucketing(const uint32_t *keys, const uint32_t *words, uint32_t n, uint32_t per_head,
                                  const int64_t *shapes, int L, int BG, int TX, int TY, int TZ, uint32_t *counts,
-                                 uint32_t *start, uint32_t *cursor, uint32_t *mat, uint32_t tcap, uint2 *entries,
+                                 uint32_t *start, uint32_t *cursor, uint32_t *mat, uint32_t tcap, uint32_t *entries, uint32_t *queue,
                                  hipStream_t st, void (*mark)(int, hipStream_t)) {
   BucketArgs a{};
   a.keys = keys; a.words = words; a.n = n; a.per_head = per_head; a.shapes = shapes;
   a.L = L; a.BG = BG; a.TX = TX; a.TY = TY; a.TZ = TZ;
-  a.counts = counts; a.cursor = cursor; a.start = start; a.mat = mat; a.tcap = tcap; a.entries = entries;
+  a.counts = counts; a.cursor = cursor; a.start = start; a.mat = mat; a.tcap = tcap; a.entries = entries; a.queue = queue;
+  // LDS sized to what the matrix can hold (tiles past the window take the global-atomic path),
+  // so that two 1024-thread blocks fit on a CU
+  a.wcap = tcap < (uint32_t)kWin ? (tcap > 0 ? tcap : 1u) : (uint32_t)kWin;
   // about kBlocksPerHead blocks per head, each a whole number of kBucketThreads-sample steps
   a.chunk = (per_head + kBlocksPerHead - 1) / kBlocksPerHead;
   a.chunk = (a.chunk + kBucketThreads - 1) / kBucketThreads * kBucketThreads;
@@ -264,10 +361,10 @@ hipError_t launch_tile_bucketing(const uint32_t *keys, const uint32_t *words, ui
   if (n == 0) a.blocks_per_head = 0;   // every counter is zero: the head scan writes zeros
   const unsigned blocks = (unsigned)BG * a.blocks_per_head;
   hipLaunchKernelGGL(tile_clear_kernel, dim3(64), dim3(1024), 0, st, a);
-  if (blocks > 0) hipLaunchKernelGGL(tile_count_kernel, dim3(blocks), dim3(kBucketThreads), kWin * 4, st, a);
+  if (blocks > 0) hipLaunchKernelGGL(tile_count_kernel, dim3(blocks), dim3(kBucketThreads), a.wcap * 4, st, a);
   if (BG > 0) hipLaunchKernelGGL(tile_headscan_kernel, dim3((unsigned)BG), dim3(1024), 0, st, a, start);
   if (mark) mark(3, st);
-  if (blocks > 0) hipLaunchKernelGGL(tile_scatter_kernel, dim3(blocks), dim3(kBucketThreads), kWin * 8, st, a);
+  if (blocks > 0) hipLaunchKernelGGL(tile_scatter_kernel, dim3(blocks), dim3(kBucketThreads), tile_scatter_lds_bytes(a.wcap), st, a);
   return hipGetLastError();
 }
 

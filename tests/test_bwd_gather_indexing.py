@@ -1,6 +1,7 @@
 """CPU emulation of the backward's tile index arithmetic (no GPU): the home tile and tile-local
-word of the query kernel, the entry expansion of the bucketing kernels, and the tile kernel's
-local bins, counting sort and x-pair ranges, checked against the float64 oracle's grad_value.
+word of the query kernel, the entry expansion of the bucketing kernels (entries are sample
+indices), and the tile kernel's local bins (from the stashed pixel coordinates and the tile's
+origin), counting sort and x-pair ranges, checked against the float64 oracle's grad_value.
 Every LDS index the tile kernel would use is asserted to stay inside its array.  Covers odd
 widths, 1-voxel rows and levels, levels smaller than a tile, partial last tiles, several heads
 and batch items, and nominal tile sizes down to 2x1x1 (every sample then crosses tiles)."""
@@ -75,7 +76,7 @@ def emulate_grad_value(value, shapes, sla, grad_out, K, TX, TY, TZ):
                         s = l * K + k
                         x, y, z = (_pixel(rec[3 * s], Wl), _pixel(rec[3 * s + 1], Hl), _pixel(rec[3 * s + 2], Dl))
                         inside = x >= -1 and y >= -1 and z >= -1 and x < Wl and y < Hl and z < Dl
-                        stash.append((x - math.floor(x), y - math.floor(y), z - math.floor(z), attn[s]))
+                        stash.append((x, y, z, attn[s]))   # pixel coordinates
                         if not inside:
                             keys.append(None)
                             words.append(0)
@@ -110,7 +111,7 @@ def emulate_grad_value(value, shapes, sla, grad_out, K, TX, TY, TZ):
                         ww &= ~(0x1F << 10)
                     tid = key + dx + dy * ntx + dz * ntx * nty
                     assert tid < B * G * T_h
-                    buckets[tid].append((sidx, ww))
+                    buckets[tid].append(sidx)
     # phase 3: tile kernel
     gv = np.full_like(value, np.nan, dtype=np.float64)
     go_rows = grad_out.reshape(B, Q, G, D).transpose(0, 2, 1, 3).reshape(-1, D)   # head-major rows
@@ -125,9 +126,11 @@ def emulate_grad_value(value, shapes, sla, grad_out, K, TX, TY, TZ):
                 for t in range(cnt):
                     itx, ity, itz = t % ntx, (t // ntx) % nty, t // (ntx * nty)
                     ent = buckets[(b * G + g) * T_h + lbase[l] + t]
+                    ox, oy, oz = itx * tx - 1, ity * ty - 1, itz * tz - 1   # bin 0 = local -1
                     lb = []
-                    for (_, w) in ent:
-                        v = ((w >> 10) & 31) * TYp * TXp + ((w >> 5) & 31) * TXp + (w & 31)
+                    for sidx in ent:
+                        sx, sy, sz, _ = stash[sidx]
+                        v = ((math.floor(sz) - oz) * TYp + (math.floor(sy) - oy)) * TXp + (math.floor(sx) - ox)
                         assert 0 <= v < nb
                         lb.append(v)
                     counts = np.bincount(np.array(lb, dtype=int), minlength=nb) if lb else np.zeros(nb, int)
@@ -153,8 +156,9 @@ def emulate_grad_value(value, shapes, sla, grad_out, K, TX, TY, TZ):
                                     s0, m1, m2 = st(rb), st(rb + 1), st(rb + 2)
                                     s3 = st(rb + 3) if two else m2
                                     for i in range(s0, s3):
-                                        sidx = ent[order[i]][0]
-                                        fx, fy, fz, at = stash[sidx]
+                                        sidx = ent[order[i]]
+                                        sx, sy, sz, at = stash[sidx]
+                                        fx, fy, fz = sx - math.floor(sx), sy - math.floor(sy), sz - math.floor(sz)
                                         wy = fy if dy else 1 - fy
                                         wz = fz if dz else 1 - fz
                                         lft, ctr = i < m1, i < m2

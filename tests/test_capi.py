@@ -65,7 +65,7 @@ def test_workspace_bytes(lib):
 
     # keys, words, stash, <= 8 entries per sample, 3 tile arrays of B*G*S+1 words, the bucketing
     # matrix (64 blocks x S/16+64 tiles per head), head-major copies of value and grad_output
-    want = (2 * al(4 * n) + al(16 * n) + al(64 * n) + 3 * al(4 * (B * G * S + 1))
+    want = (2 * al(4 * n) + al(16 * n) + al(32 * n) + 3 * al(4 * (B * G * S + 1)) + 256
             + al(4 * B * G * 64 * (S // 16 + 64)) + al(B * S * G * D * 2) + al(B * Q * G * D * 2))
     assert lib.ops3d_fda_backward_workspace_bytes(2, B, S, G, D, L, Q, K) == want
     assert lib.ops3d_fda_backward_workspace_bytes(9, B, S, G, D, L, Q, K) == 0
