@@ -322,11 +322,7 @@ __global__ __launch_bounds__(kBlock) OPS3D_FDA_QUERY_ATTR void fda_bwd_query_pai
   uint32_t tgw[NW];
   if (live) {
     load_global_words<NW>(static_cast<const T *>(a.grad_out) + unit * a.D + j * CPL, tgw);
-#ifdef EXP_NO_GOUTHM
-    if (false) {
-#else
     if (a.gout_hm && dxl == 0) {   // the row again, head-major, for the tile kernel
-#endif
       uint32_t *dst = reinterpret_cast<uint32_t *>(static_cast<T *>(a.gout_hm) +
                                                    (((int64_t)b * a.G + g) * a.Q + q) * a.D + j * CPL);
 #pragma unroll
@@ -417,7 +413,6 @@ __global__ __launch_bounds__(kBlock) OPS3D_FDA_QUERY_ATTR void fda_bwd_query_pai
   }
   wave_lds_sync();
   {
-#ifndef EXP_NO_WRITEOUT
     // the wave's units are consecutive q of one (b, g): their samples are one contiguous range
     const int q0 = qb * UPB + wave * UPW;
     const int nlive = min(UPW, a.Q - q0);
@@ -443,14 +438,6 @@ __global__ __launch_bounds__(kBlock) OPS3D_FDA_QUERY_ATTR void fda_bwd_query_pai
         a.stash[gs0 + e] = stx[ss];
       }
     }
-#else
-    {
-      const int q0 = qb * UPB + wave * UPW;
-      const int nlive = min(UPW, a.Q - q0);
-      const uint32_t gs0 = sample_index(b, g, q0, 0, a.G, a.Q, LK);
-      for (int e = lane; e < nlive * LK; e += kWave) a.keys[gs0 + e] = kKeyInvalid;
-    }
-#endif
   }
   // softmax backward over the unit's L*K attention weights
   float dot = 0.f;
