@@ -31,9 +31,10 @@
 #define OPS3D_FDA_TILE_WPE 4    // minimum waves per SIMD the tile kernel is compiled for
 #endif
 
-// Occupancy hint of the backward query kernel (waves per SIMD it is compiled for; 0: none).
+// Occupancy hint of the backward query pair kernel (waves per SIMD it is compiled for; 0: none).
+// Left to itself the compiler takes 107 VGPRs (4 waves); 5 waves fit without spills.
 #ifndef OPS3D_FDA_QUERY_WPE
-#define OPS3D_FDA_QUERY_WPE 0
+#define OPS3D_FDA_QUERY_WPE 5
 #endif
 #if OPS3D_FDA_QUERY_WPE > 0
 #define OPS3D_FDA_QUERY_ATTR __attribute__((amdgpu_waves_per_eu(OPS3D_FDA_QUERY_WPE)))
@@ -353,9 +354,7 @@ __global__ __launch_bounds__(kBlock) OPS3D_FDA_QUERY_ATTR void fda_bwd_query_pai
         cx_s[sj] = in_s ? (uint32_t)(ms.x0 + 1) : kKeyInvalid;
         cy_s[sj] = (uint32_t)(ms.y0 + 1);
         cz_s[sj] = (uint32_t)(ms.z0 + 1);
-        // pixel coordinates (base corner + fraction: exact), from which the tile kernel takes both
-        st_s[sj] = make_float4((float)ms.x0 + ms.wx[1], (float)ms.y0 + ms.wy[1], (float)ms.z0 + ms.wz[1],
-                               rec[3 * LK + sj]);
+        st_s[sj] = make_float4(ms.wx[1], ms.wy[1], ms.wz[1], rec[3 * LK + sj]);
       }
       uint32_t off4[4];
 #pragma unroll
@@ -435,7 +434,9 @@ __global__ __launch_bounds__(kBlock) OPS3D_FDA_QUERY_ATTR void fda_bwd_query_pai
         const uint32_t ez = lz == lt.t[0] - 1 && (hz + 1) * lt.t[0] < lt.n[0];
         a.keys[gs0 + e] = bx == kKeyInvalid ? kKeyInvalid : lvbase[l] + (uint32_t)((hz * lt.nt[1] + hy) * lt.nt[2] + hx);
         a.vals[gs0 + e] = tile_word(lx, ly, lz) | (ex << 15) | (ey << 16) | (ez << 17) | ((uint32_t)l << 18);
-        a.stash[gs0 + e] = stx[ss];
+        // pixel coordinates = base corner + fraction (exact), from which the tile kernel takes both
+        const float4 fr = stx[ss];
+        a.stash[gs0 + e] = make_float4((float)x0 + fr.x, (float)y0 + fr.y, (float)z0 + fr.z, fr.w);
       }
     }
   }
@@ -577,7 +578,7 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
           cx_s[su] = in[u] ? (uint32_t)(m.x0 + 1) : kKeyInvalid;
           cy_s[su] = (uint32_t)(m.y0 + 1);
           cz_s[su] = (uint32_t)(m.z0 + 1);
-          st_s[su] = make_float4((float)m.x0 + m.wx[1], (float)m.y0 + m.wy[1], (float)m.z0 + m.wz[1], at[u]);
+          st_s[su] = make_float4(m.wx[1], m.wy[1], m.wz[1], at[u]);
         }
       }
     }
@@ -610,7 +611,9 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
         const uint32_t ez = lz == lt.t[0] - 1 && (hz + 1) * lt.t[0] < lt.n[0];
         a.keys[gs0 + e] = bx == kKeyInvalid ? kKeyInvalid : lvbase[l] + (uint32_t)((hz * lt.nt[1] + hy) * lt.nt[2] + hx);
         a.vals[gs0 + e] = tile_word(lx, ly, lz) | (ex << 15) | (ey << 16) | (ez << 17) | ((uint32_t)l << 18);
-        a.stash[gs0 + e] = stx[ss];
+        // pixel coordinates = base corner + fraction (exact), from which the tile kernel takes both
+        const float4 fr = stx[ss];
+        a.stash[gs0 + e] = make_float4((float)x0 + fr.x, (float)y0 + fr.y, (float)z0 + fr.z, fr.w);
       }
     }
   }
