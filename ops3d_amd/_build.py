@@ -22,6 +22,10 @@ ARCH = "gfx950"
 # -packed-fp32-ops off: hipcc must not form v_pk_{add,mul,fma}_f32 on its own.
 # -munsafe-fp-atomics: fp32 atomics lower to the hardware add (no CAS loop); all our atomics
 # target coarse-grained device memory, where that is exact.
+# atomic optimizer off: it turns a one-lane atomic with a uniform address (the tile kernel's work
+# counter) into a wave-aggregated one that reads the result back at once, so the wave waits for
+# the atomic's round trip where the kernel means to hide it; no kernel here has atomics that
+# aggregation would help (their addresses vary per lane).
 HIP_FLAGS = [
     "-std=c++17",
     "-O3",
@@ -30,6 +34,7 @@ HIP_FLAGS = [
     "-fPIC",
     "-fvisibility=hidden",
     "-munsafe-fp-atomics",
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",
 ]

@@ -750,33 +750,48 @@ void fda_bwd_tile_kernel(const Args a) {
     head_of(bgi, b, g);
     return (uint32_t)(b * G + g) * T_h + lvbase[l] + t;
   };
-  // Tiles: the block's first two are bi and bi + nbx; after them each block takes the next
-  // unclaimed tile of its XCD group from a work counter (one atomic per tile, made a tile ahead),
-  // so blocks that drew light tiles take more of them.
+  // Tiles: the block's first three are bi, bi + nbx and bi + 2 nbx; after them each block takes
+  // the next unclaimed tile of its XCD group from a work counter (one atomic per tile, made
+  // three tiles ahead), so blocks that drew light tiles take more of them.
   // Software pipeline: the entries of the block's next chunk are loaded when a chunk starts and
   // their stash before its rows are loaded, so both arrive during the owner phase; tile headers
-  // (first entry, count) are loaded a tile ahead of use.
+  // (first entry, count) are loaded two tiles before they are read.
   __shared__ uint32_t grab_l[2];
-  uint32_t k1 = (uint32_t)bi + (uint32_t)nbx;      // the next tile
-  uint32_t h0s = 0, h0c = 0, h1s = 0, h1c = 0;     // headers of the current and the next tile
-  if ((uint32_t)bi < total) {
-    const uint32_t gid = tile_gid((uint32_t)bi);
-    h0s = a.tile_start[gid];
-    h0c = a.tile_counts[gid];
+  // Tile headers (first entry, count) live in a 4-slot LDS ring indexed by the tile's position in
+  // the block's sequence.  Thread 0 loads the header of the tile two ahead into registers at the
+  // end of a tile and writes it to the ring only where its wave has waited for its row loads
+  // anyway (end of an owner phase), so no wave waits for it; the block reads it a tile later.
+  __shared__ uint32_t hdr_l[4][2];
+  uint32_t k1 = (uint32_t)bi + (uint32_t)nbx, k2 = k1 + (uint32_t)nbx;   // the next two tiles
+  uint32_t hs_pend = 0, hc_pend = 0;   // header of k2 (thread 0), not yet in the ring
+  if (tid == 0) {
+    const uint32_t kk[2] = {(uint32_t)bi, k1};
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t gid = kk[i] < total ? tile_gid(kk[i]) : 0u;
+      hdr_l[i][0] = kk[i] < total ? a.tile_start[gid] : 0u;
+      hdr_l[i][1] = kk[i] < total ? a.tile_counts[gid] : 0u;
+    }
+    if (k2 < total) {
+      const uint32_t gid = tile_gid(k2);
+      hs_pend = a.tile_start[gid];
+      hc_pend = a.tile_counts[gid];
+    }
   }
-  if (k1 < total) {
-    const uint32_t gid = tile_gid(k1);
-    h1s = a.tile_start[gid];
-    h1c = a.tile_counts[gid];
-  }
+  __syncthreads();
+  uint32_t pos = 0;   // position of the current tile in the block's sequence
+  // the work counter's value claimed for the current tile (thread 0; declared outside the tile
+  // loop so that no per-tile re-initialisation waits for the previous atomic's return)
+  uint32_t taken = 0;
   bool pf = false;               // the current chunk's entries and stash are in pA.. / psA..
   uint32_t pA = 0, pB = 0;
   float4 psA = make_float4(0.f, 0.f, 0.f, 0.f), psB = psA;
   int par = 0;
   for (uint32_t k = (uint32_t)bi; k < total; par ^= 1) {
-    // claim the tile after the next one (read after this tile's barriers)
-    if (tid == 0)
-      grab_l[par] = k1 < total ? 2u * (uint32_t)nbx + atomicAdd(a.tile_queue + xcd, 1u) : total;
+    // claim the tile after k2; thread 0 publishes the claim in LDS only before the owner phase's
+    // closing barrier (so no wave waits for the atomic) and the block reads it after this tile's
+    // last barrier
+    if (tid == 0 && k2 < total) taken = atomicAdd(a.tile_queue + xcd, 1u);
+    const bool claimed = k2 < total;
     int l, b, g;
     uint32_t bgi, t;
     decode(k, l, bgi, t);
@@ -790,8 +805,8 @@ void fda_bwd_tile_kernel(const Args a) {
     const int z = itz * tz + pz, y = ity * ty + py, x0 = itx * tx + 2 * px;
     const bool live = 2 * px < tx && py < ty && pz < tz && z < Dl && y < Hl && x0 < Wl;
     const bool two = 2 * px + 1 < tx && x0 + 1 < Wl;
-    const uint32_t e0 = h0s, e1 = h0s + h0c;
-    const uint32_t ns = h1s, nc = h1c;   // next tile's header
+    const uint32_t e0 = hdr_l[pos & 3u][0], e1 = e0 + hdr_l[pos & 3u][1];
+    const uint32_t ns = hdr_l[(pos + 1u) & 3u][0], nc = hdr_l[(pos + 1u) & 3u][1];   // next tile's
     const int TXp = tx + 1, TYp = ty + 1;
     const int nb = TXp * TYp * (tz + 1);
 
@@ -815,6 +830,9 @@ void fda_bwd_tile_kernel(const Args a) {
         enB = a.entries[c0 + (hB ? eB : 0)];
         stA = a.stash[enA];
         stB = a.stash[enB];
+        // wait here, so that after the two paths join nothing of this one is pending: the
+        // prefetched path must not wait for the stores and claims issued since its loads
+        __builtin_amdgcn_s_waitcnt(0);
       }
       // the next chunk: the rest of this tile, or the next tile's first chunk
       const bool nxt_here = c0 + (uint32_t)CH < e1;
@@ -941,6 +959,11 @@ void fda_bwd_tile_kernel(const Args a) {
           }
         }
       }
+      if (tid == 0) {
+        grab_l[par] = taken;
+        hdr_l[(pos + 2u) & 3u][0] = hs_pend;
+        hdr_l[(pos + 2u) & 3u][1] = hc_pend;
+      }
       __syncthreads();
       TILE_MARK(4);
     }
@@ -965,17 +988,22 @@ void fda_bwd_tile_kernel(const Args a) {
       }
     }
     TILE_MARK(5);
-    if (e0 == e1) __syncthreads();   // the claim is read after a barrier of this tile
-    const uint32_t k2 = grab_l[par];
-    uint32_t h2s = 0, h2c = 0;
-    if (k2 < total) {
-      const uint32_t gid = tile_gid(k2);
-      h2s = a.tile_start[gid];
-      h2c = a.tile_counts[gid];
+    if (e0 == e1) {   // no chunk: publish the claim here
+      if (tid == 0) {
+        grab_l[par] = taken;
+        hdr_l[(pos + 2u) & 3u][0] = hs_pend;
+        hdr_l[(pos + 2u) & 3u][1] = hc_pend;
+      }
+      __syncthreads();
     }
-    k = k1; k1 = k2;
-    h0s = ns; h0c = nc;
-    h1s = h2s; h1c = h2c;
+    const uint32_t k3 = claimed ? 3u * (uint32_t)nbx + grab_l[par] : total;
+    if (tid == 0 && k3 < total) {
+      const uint32_t gid = tile_gid(k3);
+      hs_pend = a.tile_start[gid];
+      hc_pend = a.tile_counts[gid];
+    }
+    k = k1; k1 = k2; k2 = k3;
+    ++pos;
   }
 #if OPS3D_FDA_TILE_TIMING
   if (tid == 0 && a.dbg)
