@@ -30,8 +30,9 @@ hipError_t launch_bf16(int, int, int, const Args &, unsigned, size_t, hipStream_
 hipError_t launch_tile_bucketing(const uint32_t *keys, const uint32_t *words, uint32_t n, uint32_t per_head,
                                  const int64_t *shapes, int L, int BG, int TX, int TY, int TZ, uint32_t *counts,
                                  uint32_t *start, uint32_t *cursor, uint32_t *mat, uint32_t tcap, uint32_t *entries, uint32_t *queue,
-                                 hipStream_t st, void (*mark)(int, hipStream_t));
+                                 bool counts_cleared, hipStream_t st, void (*mark)(int, hipStream_t));
 size_t tile_matrix_words(uint32_t BG, uint32_t tcap);
+uint32_t tile_window(uint32_t tcap);
 }  // namespace ops3d_fda
 
 using namespace ops3d_fda;
@@ -394,6 +395,7 @@ static int backward_impl(const void *value, const void *value_head_major, const 
   a.tile_cursor = cursor;
   a.entries = entries;
   a.tile_queue = reinterpret_cast<uint32_t *>(ws + ly.off_queue);
+  a.count_clear_wcap = tile_window(ly.tcap);   // the query kernel clears the counters (atomic mode)
   tile_dims(tile_lanes(geo.lpu, geo.cpl * elem_size(dtype)), a.TX, a.TY, a.TZ);
   a.inv_lk = 1.0 / (double)(num_levels * num_point);
   hipError_t e;
@@ -426,7 +428,7 @@ static int backward_impl(const void *value, const void *value_head_major, const 
                             (uint32_t)num_query * (uint32_t)(num_levels * num_point), spatial_shapes, num_levels,
                             batch * num_heads, a.TX, a.TY, a.TZ, counts, tstart, cursor,
                             reinterpret_cast<uint32_t *>(ws + ly.off_mat), ly.tcap, entries,
-                            reinterpret_cast<uint32_t *>(ws + ly.off_queue), st,
+                            reinterpret_cast<uint32_t *>(ws + ly.off_queue), work, st,
                             g_prof_on ? prof_mark : nullptr);
   if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "tile bucketing failed: %s", hipGetErrorString(e));
   prof_mark(4, st);

@@ -50,6 +50,8 @@ struct Args {
   uint32_t *tile_start;       // [B*G*T_h] first entry of each tile (head base + exclusive scan)
   uint32_t *tile_cursor;      // [B*G*T_h] fill cursor of each tile
   uint32_t *tile_queue;       // [8] tile kernel work counters (one per XCD group), zero at launch
+  uint32_t count_clear_wcap;  // != 0: the query kernel zeroes tile_counts when a head has more
+                              // tiles than this (the bucketing's atomic mode)
   uint32_t *entries;          // [<= 8N] sample indices, grouped by tile
   int TX, TY, TZ;             // nominal tile dimensions (voxels), clipped per level
   int chunk;                  // entries per LDS chunk of the tile kernel
@@ -557,6 +559,20 @@ __device__ __forceinline__ uint32_t tiles_per_head(const int64_t *shapes, int L,
   uint32_t t = 0;
   for (int l = 0; l < L; ++l) t += level_tiles(shapes, l, TX, TY, TZ).count;
   return t;
+}
+
+// The bucketing's atomic mode (a head has more tiles than its LDS window) adds into tile_counts,
+// so they must start at zero; block 0 of the query kernel, which runs just before, clears them
+// as its last work (block 0 always has queries; a whole-block call, with a barrier).
+__device__ __forceinline__ void clear_tile_counts(const Args &a) {
+  __shared__ uint32_t th_s;
+  if (a.count_clear_wcap == 0u || blockIdx.x != 0) return;
+  if (threadIdx.x == 0) th_s = tiles_per_head(a.shapes, a.L, a.TX, a.TY, a.TZ);
+  __syncthreads();
+  const uint32_t T_h = th_s;
+  if (T_h <= a.count_clear_wcap) return;
+  const uint32_t total = (uint32_t)(a.B * a.G) * T_h;
+  for (uint32_t i = threadIdx.x; i < total; i += blockDim.x) a.tile_counts[i] = 0u;
 }
 
 // Tile-local word of an entry: base corner relative to the tile origin, each coordinate in

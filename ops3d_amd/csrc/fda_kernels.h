@@ -450,6 +450,7 @@ __global__ __launch_bounds__(kBlock) OPS3D_FDA_QUERY_ATTR void fda_bwd_query_pai
   }
   wave_lds_sync();
   if (live) write_record<T, UL>(static_cast<T *>(a.grad_loc_attn) + unit * P, P, ju, rec);
+  clear_tile_counts(a);
 }
 
 template <typename T, int CPL, int LPU>
@@ -627,6 +628,7 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
   }
   wave_lds_sync();
   if (live) write_record<T, LPU>(static_cast<T *>(a.grad_loc_attn) + unit * P, P, j, rec);
+  clear_tile_counts(a);
 }
 
 // ---------------------------------------------------------------------------------------------

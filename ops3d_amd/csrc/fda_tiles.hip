@@ -123,14 +123,24 @@ __global__ __launch_bounds__(kBucketThreads) void tile_count_kernel(const Bucket
   uint32_t bg, s0, s1;
   block_range(a, bg, s0, s1);
   const uint32_t w0 = bg * T_h;
-#pragma unroll 4
-  for (uint32_t s = s0 + threadIdx.x; s < s1; s += kBucketThreads) {
-    const uint32_t key = a.keys[s];
-    if (key == kKeyInvalid) continue;
-    for_each_entry(key, a.words[s], lg, [&](uint32_t id, uint32_t) {
-      if (id - w0 < nw) atomicAdd(&win[id - w0], 1u);
-      else atomicAdd(&a.counts[id], 1u);
-    });
+  // batches of kCountBatch samples per thread: all their loads are issued before any is used
+  constexpr int kCountBatch = 8;
+  for (uint32_t sb = s0 + threadIdx.x; sb < s1; sb += kCountBatch * kBucketThreads) {
+    uint32_t key[kCountBatch], word[kCountBatch];
+#pragma unroll
+    for (int i = 0; i < kCountBatch; ++i) {
+      const uint32_t s = sb + (uint32_t)i * kBucketThreads;
+      key[i] = s < s1 ? a.keys[s] : kKeyInvalid;
+      word[i] = s < s1 ? a.words[s] : 0u;
+    }
+#pragma unroll
+    for (int i = 0; i < kCountBatch; ++i) {
+      if (key[i] == kKeyInvalid) continue;
+      for_each_entry(key[i], word[i], lg, [&](uint32_t id, uint32_t) {
+        if (id - w0 < nw) atomicAdd(&win[id - w0], 1u);
+        else atomicAdd(&a.counts[id], 1u);
+      });
+    }
   }
   __syncthreads();
   if (matrix_mode(a, T_h)) {
@@ -299,13 +309,15 @@ __global__ __launch_bounds__(1024) void tile_headscan_kernel(const BucketArgs a,
     if (t < T_h) {
       if (mat) {
         uint32_t *col = a.mat + (size_t)bg * a.blocks_per_head * T_h + t;
-        // 16 loads in flight, then their prefix
-        for (uint32_t c0 = 0; c0 < a.blocks_per_head; c0 += 16) {
-          uint32_t v[16];
+        // kScanBatch loads in flight, then their prefix
+        constexpr int kScanBatch = 32;
+        for (uint32_t c0 = 0; c0 < a.blocks_per_head; c0 += kScanBatch) {
+          uint32_t v[kScanBatch];
 #pragma unroll
-          for (int k = 0; k < 16; ++k) v[k] = c0 + k < a.blocks_per_head ? col[(size_t)(c0 + k) * T_h] : 0u;
+          for (int k = 0; k < kScanBatch; ++k)
+            v[k] = c0 + k < a.blocks_per_head ? col[(size_t)(c0 + k) * T_h] : 0u;
 #pragma unroll
-          for (int k = 0; k < 16; ++k) {
+          for (int k = 0; k < kScanBatch; ++k) {
             if (c0 + k < a.blocks_per_head) col[(size_t)(c0 + k) * T_h] = x;
             x += v[k];
           }
@@ -338,6 +350,10 @@ __global__ __launch_bounds__(1024) void tile_headscan_kernel(const BucketArgs a,
   }
 }
 
+// LDS histogram window (tiles) of the bucketing kernels for a workspace matrix of tcap tiles; a
+// head with more tiles is bucketed in atomic mode.
+uint32_t tile_window(uint32_t tcap) { return tcap < (uint32_t)kWin ? (tcap > 0 ? tcap : 1u) : (uint32_t)kWin; }
+
 // Workspace words of the matrix of tile_count (blocks x tiles of every head) for heads of up
 // to tcap tiles.
 size_t tile_matrix_words(uint32_t BG, uint32_t tcap) { return (size_t)BG * kBlocksPerHead * tcap; }
@@ -345,14 +361,14 @@ size_t tile_matrix_words(uint32_t BG, uint32_t tcap) { return (size_t)BG * kBloc
 hipError_t launch_tile_bucketing(const uint32_t *keys, const uint32_t *words, uint32_t n, uint32_t per_head,
                                  const int64_t *shapes, int L, int BG, int TX, int TY, int TZ, uint32_t *counts,
                                  uint32_t *start, uint32_t *cursor, uint32_t *mat, uint32_t tcap, uint32_t *entries, uint32_t *queue,
-                                 hipStream_t st, void (*mark)(int, hipStream_t)) {
+                                 bool counts_cleared, hipStream_t st, void (*mark)(int, hipStream_t)) {
   BucketArgs a{};
   a.keys = keys; a.words = words; a.n = n; a.per_head = per_head; a.shapes = shapes;
   a.L = L; a.BG = BG; a.TX = TX; a.TY = TY; a.TZ = TZ;
   a.counts = counts; a.cursor = cursor; a.start = start; a.mat = mat; a.tcap = tcap; a.entries = entries; a.queue = queue;
   // LDS sized to what the matrix can hold (tiles past the window take the global-atomic path),
   // so that two 1024-thread blocks fit on a CU
-  a.wcap = tcap < (uint32_t)kWin ? (tcap > 0 ? tcap : 1u) : (uint32_t)kWin;
+  a.wcap = tile_window(tcap);
   // about kBlocksPerHead blocks per head, each a whole number of kBucketThreads-sample steps
   a.chunk = (per_head + kBlocksPerHead - 1) / kBlocksPerHead;
   a.chunk = (a.chunk + kBucketThreads - 1) / kBucketThreads * kBucketThreads;
@@ -360,7 +376,7 @@ hipError_t launch_tile_bucketing(const uint32_t *keys, const uint32_t *words, ui
   a.blocks_per_head = (per_head + a.chunk - 1) / a.chunk;
   if (n == 0) a.blocks_per_head = 0;   // every counter is zero: the head scan writes zeros
   const unsigned blocks = (unsigned)BG * a.blocks_per_head;
-  hipLaunchKernelGGL(tile_clear_kernel, dim3(64), dim3(1024), 0, st, a);
+  if (!counts_cleared) hipLaunchKernelGGL(tile_clear_kernel, dim3(64), dim3(1024), 0, st, a);
   if (blocks > 0) hipLaunchKernelGGL(tile_count_kernel, dim3(blocks), dim3(kBucketThreads), a.wcap * 4, st, a);
   if (BG > 0) hipLaunchKernelGGL(tile_headscan_kernel, dim3((unsigned)BG), dim3(1024), 0, st, a, start);
   if (mark) mark(3, st);
