@@ -500,7 +500,10 @@ __device__ __forceinline__ uint32_t sample_index(int b, int g, int q, int s, int
 __host__ __device__ constexpr int tile_threads(int lpu) {
   return lpu <= 4 ? 256 : (lpu >= 16 ? 1024 : 64 * lpu);
 }
-constexpr int kTileKPT = 2;          // entries per thread and chunk (chunk <= 2 * threads)
+#ifndef OPS3D_FDA_TILE_KPT
+#define OPS3D_FDA_TILE_KPT 2
+#endif
+constexpr int kTileKPT = OPS3D_FDA_TILE_KPT;   // entries per thread and chunk (chunk <= KPT * threads)
 constexpr uint32_t kKeyInvalid = 0xffffffffu;
 
 // Lanes per x-pair of voxels in the tile kernel (lane_bytes = CPL * sizeof(T) of the query

@@ -784,9 +784,14 @@ void fda_bwd_tile_kernel(const Args a) {
   // the work counter's value claimed for the current tile (thread 0; declared outside the tile
   // loop so that no per-tile re-initialisation waits for the previous atomic's return)
   uint32_t taken = 0;
-  bool pf = false;               // the current chunk's entries and stash are in pA.. / psA..
-  uint32_t pA = 0, pB = 0;
-  float4 psA = make_float4(0.f, 0.f, 0.f, 0.f), psB = psA;
+  bool pf = false;               // the current chunk's entries and stash are in pE / pS
+  uint32_t pE[kTileKPT];
+  float4 pS[kTileKPT];
+#pragma unroll
+  for (int e = 0; e < kTileKPT; ++e) {
+    pE[e] = 0u;
+    pS[e] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   int par = 0;
   for (uint32_t k = (uint32_t)bi; k < total; par ^= 1) {
     // claim the tile after k2; thread 0 publishes the claim in LDS only before the owner phase's
@@ -818,20 +823,22 @@ void fda_bwd_tile_kernel(const Args a) {
 
     for (uint32_t c0 = e0; c0 < e1; c0 += (uint32_t)CH) {
       const int n = (int)min((uint32_t)CH, e1 - c0);
-      static_assert(kTileKPT == 2, "two entries per thread and chunk");
-      const int eA = tid, eB = tid + NT;
-      const bool hA = eA < n, hB = eB < n;
+      constexpr int KPT = kTileKPT;   // entries per thread and chunk (registers)
       // this chunk's entries and stash (prefetched, or loaded now); an absent entry reads entry 0
       // (unconditional loads keep everything in registers)
-      uint32_t enA, enB;
-      float4 stA, stB;
+      uint32_t en[KPT];
+      float4 st[KPT];
       if (pf) {
-        enA = pA; enB = pB; stA = psA; stB = psB;
+#pragma unroll
+        for (int e = 0; e < KPT; ++e) {
+          en[e] = pE[e];
+          st[e] = pS[e];
+        }
       } else {
-        enA = a.entries[c0 + (hA ? eA : 0)];
-        enB = a.entries[c0 + (hB ? eB : 0)];
-        stA = a.stash[enA];
-        stB = a.stash[enB];
+#pragma unroll
+        for (int e = 0; e < KPT; ++e) en[e] = a.entries[c0 + (tid + e * NT < n ? tid + e * NT : 0)];
+#pragma unroll
+        for (int e = 0; e < KPT; ++e) st[e] = a.stash[en[e]];
         // wait here, so that after the two paths join nothing of this one is pending: the
         // prefetched path must not wait for the stores and claims issued since its loads
         __builtin_amdgcn_s_waitcnt(0);
@@ -847,26 +854,25 @@ void fda_bwd_tile_kernel(const Args a) {
       // 1a. local bin of each entry's base corner, grad_output row index, bin counts.  The stash
       // holds the pixel coordinates: base corner = floor, fraction = coordinate - floor (exact).
       const int ox = itx * tx - 1, oy = ity * ty - 1, oz = itz * tz - 1;   // bin 0 = local -1
-      const auto local_bin = [&](float4 &st) {
-        const float xf = floorf(st.x), yf = floorf(st.y), zf = floorf(st.z);
-        const uint32_t bin = ((uint32_t)((int)zf - oz) * (uint32_t)TYp + (uint32_t)((int)yf - oy)) * (uint32_t)TXp +
-                             (uint32_t)((int)xf - ox);
-        st.x -= xf;
-        st.y -= yf;
-        st.z -= zf;
-        return bin;
-      };
-      const uint32_t lbA = local_bin(stA), lbB = local_bin(stB);
-      const uint32_t riA = (uint32_t)(((double)enA + 0.5) * a.inv_lk);   // sample / (L*K), exact
-      const uint32_t riB = (uint32_t)(((double)enB + 0.5) * a.inv_lk);
-      if (hA) atomicAdd(&cur_l[lbA], 1u);
-      if (hB) atomicAdd(&cur_l[lbB], 1u);
+      uint32_t lb[KPT], ri[KPT];
+#pragma unroll
+      for (int e = 0; e < KPT; ++e) {
+        const float xf = floorf(st[e].x), yf = floorf(st[e].y), zf = floorf(st[e].z);
+        lb[e] = ((uint32_t)((int)zf - oz) * (uint32_t)TYp + (uint32_t)((int)yf - oy)) * (uint32_t)TXp +
+                (uint32_t)((int)xf - ox);
+        st[e].x -= xf;
+        st[e].y -= yf;
+        st[e].z -= zf;
+        ri[e] = (uint32_t)(((double)en[e] + 0.5) * a.inv_lk);   // sample / (L*K), exact
+        if (tid + e * NT < n) atomicAdd(&cur_l[lb[e]], 1u);
+      }
       // the next chunk's entries, issued after this chunk's stash is used (loads complete in order,
       // so a wait for the stash would also wait for them; the scheduling barrier keeps them here)
       __builtin_amdgcn_sched_barrier(0);
       if (npf) {
-        pA = a.entries[nc0 + ((uint32_t)eA < nn ? (uint32_t)eA : 0u)];
-        pB = a.entries[nc0 + ((uint32_t)eB < nn ? (uint32_t)eB : 0u)];
+#pragma unroll
+        for (int e = 0; e < KPT; ++e)
+          pE[e] = a.entries[nc0 + ((uint32_t)(tid + e * NT) < nn ? (uint32_t)(tid + e * NT) : 0u)];
       }
       __syncthreads();
       TILE_MARK(1);
@@ -890,20 +896,17 @@ void fda_bwd_tile_kernel(const Args a) {
       __syncthreads();
       TILE_MARK(2);
       // 3. counting sort by bin: each entry's stash and row index go to its sorted position
-      if (hA) {
-        const uint32_t pos = atomicAdd(&cur_l[lbA], 1u);
-        st_l[pos] = stA;
-        rowi_l[pos] = riA;
-      }
-      if (hB) {
-        const uint32_t pos = atomicAdd(&cur_l[lbB], 1u);
-        st_l[pos] = stB;
-        rowi_l[pos] = riB;
-      }
+#pragma unroll
+      for (int e = 0; e < KPT; ++e)
+        if (tid + e * NT < n) {
+          const uint32_t pos = atomicAdd(&cur_l[lb[e]], 1u);
+          st_l[pos] = st[e];
+          rowi_l[pos] = ri[e];
+        }
       __syncthreads();
       if (npf) {   // the next chunk's stash (its entries have arrived by now)
-        psA = a.stash[pA];
-        psB = a.stash[pB];
+#pragma unroll
+        for (int e = 0; e < KPT; ++e) pS[e] = a.stash[pE[e]];
       }
       pf = npf;
       // 3b. grad_output rows into LDS in sorted order: 16-byte pieces loaded by the memory unit
