@@ -31,6 +31,12 @@
 #define OPS3D_FDA_TILE_WPE 4    // minimum waves per SIMD the tile kernel is compiled for
 #endif
 
+// Tile order of the tile kernel: 1 = after three static tiles, a per-XCD work counter;
+// 0 = static snake order (no atomics).
+#ifndef OPS3D_FDA_TILE_QUEUE
+#define OPS3D_FDA_TILE_QUEUE 1
+#endif
+
 // Occupancy hint of the backward query pair kernel (waves per SIMD it is compiled for; 0: none).
 // Left to itself the compiler takes 107 VGPRs (4 waves); 5 waves fit without spills.
 #ifndef OPS3D_FDA_QUERY_WPE
@@ -752,19 +758,24 @@ void fda_bwd_tile_kernel(const Args a) {
     head_of(bgi, b, g);
     return (uint32_t)(b * G + g) * T_h + lvbase[l] + t;
   };
-  // Tiles: the block's first three are bi, bi + nbx and bi + 2 nbx; after them each block takes
-  // the next unclaimed tile of its XCD group from a work counter (one atomic per tile, made
-  // three tiles ahead), so blocks that drew light tiles take more of them.
+  // Tiles: the block's first four are bi + j nbx (j < 4); after them each block takes the next
+  // unclaimed tile of its XCD group from a work counter (one atomic per tile, made four tiles
+  // ahead and read three ahead, so its round trip hides behind a whole tile even when tiles are
+  // tiny), so blocks that drew light tiles take more of them.
   // Software pipeline: the entries of the block's next chunk are loaded when a chunk starts and
   // their stash before its rows are loaded, so both arrive during the owner phase; tile headers
   // (first entry, count) are loaded two tiles before they are read.
-  __shared__ uint32_t grab_l[2];
+  __shared__ uint32_t grab_l[4];   // claim made at tile position p in slot p & 3 (~0u: none)
   // Tile headers (first entry, count) live in a 4-slot LDS ring indexed by the tile's position in
   // the block's sequence.  Thread 0 loads the header of the tile two ahead into registers at the
   // end of a tile and writes it to the ring only where its wave has waited for its row loads
   // anyway (end of an owner phase), so no wave waits for it; the block reads it a tile later.
   __shared__ uint32_t hdr_l[4][2];
   uint32_t k1 = (uint32_t)bi + (uint32_t)nbx, k2 = k1 + (uint32_t)nbx;   // the next two tiles
+  if (!OPS3D_FDA_TILE_QUEUE) {
+    k1 = 2u * (uint32_t)nbx - 1u - (uint32_t)bi;
+    k2 = 2u * (uint32_t)nbx + (uint32_t)bi;
+  }
   uint32_t hs_pend = 0, hc_pend = 0;   // header of k2 (thread 0), not yet in the ring
   if (tid == 0) {
     const uint32_t kk[2] = {(uint32_t)bi, k1};
@@ -792,13 +803,12 @@ void fda_bwd_tile_kernel(const Args a) {
     pE[e] = 0u;
     pS[e] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  int par = 0;
-  for (uint32_t k = (uint32_t)bi; k < total; par ^= 1) {
-    // claim the tile after k2; thread 0 publishes the claim in LDS only before the owner phase's
-    // closing barrier (so no wave waits for the atomic) and the block reads it after this tile's
-    // last barrier
-    if (tid == 0 && k2 < total) taken = atomicAdd(a.tile_queue + xcd, 1u);
-    const bool claimed = k2 < total;
+  for (uint32_t k = (uint32_t)bi; k < total;) {
+    // claim the tile of position pos + 4 (if pos + 2 exists, the queue may still hold tiles);
+    // thread 0 publishes the claim in LDS only before the owner phase's closing barrier (so no
+    // wave waits for the atomic), and the block reads it at the end of the next tile
+    const bool claimed = OPS3D_FDA_TILE_QUEUE && k2 < total;
+    if (claimed && tid == 0) taken = atomicAdd(a.tile_queue + xcd, 1u);
     int l, b, g;
     uint32_t bgi, t;
     decode(k, l, bgi, t);
@@ -965,7 +975,7 @@ void fda_bwd_tile_kernel(const Args a) {
         }
       }
       if (tid == 0) {
-        grab_l[par] = taken;
+        grab_l[pos & 3u] = claimed ? taken : ~0u;
         hdr_l[(pos + 2u) & 3u][0] = hs_pend;
         hdr_l[(pos + 2u) & 3u][1] = hc_pend;
       }
@@ -995,13 +1005,26 @@ void fda_bwd_tile_kernel(const Args a) {
     TILE_MARK(5);
     if (e0 == e1) {   // no chunk: publish the claim here
       if (tid == 0) {
-        grab_l[par] = taken;
+        grab_l[pos & 3u] = claimed ? taken : ~0u;
         hdr_l[(pos + 2u) & 3u][0] = hs_pend;
         hdr_l[(pos + 2u) & 3u][1] = hc_pend;
       }
       __syncthreads();
     }
-    const uint32_t k3 = claimed ? 3u * (uint32_t)nbx + grab_l[par] : total;
+    uint32_t k3;   // the tile of position pos + 3
+    if (OPS3D_FDA_TILE_QUEUE) {
+      if (pos == 0) {
+        k3 = (uint32_t)bi + 3u * (uint32_t)nbx;
+      } else {   // claimed at the previous tile
+        const uint32_t raw = grab_l[(pos - 1u) & 3u];
+        k3 = raw == ~0u ? total : 4u * (uint32_t)nbx + raw;
+      }
+      if (k3 >= total) k3 = total;
+    } else {   // static snake order: position p takes p*nbx + (p odd ? nbx-1-bi : bi)
+      const uint32_t p3 = pos + 3u;
+      k3 = p3 * (uint32_t)nbx + ((p3 & 1u) ? (uint32_t)(nbx - 1 - bi) : (uint32_t)bi);
+      if (k3 >= total) k3 = total;
+    }
     if (tid == 0 && k3 < total) {
       const uint32_t gid = tile_gid(k3);
       hs_pend = a.tile_start[gid];
