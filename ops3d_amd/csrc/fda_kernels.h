@@ -870,9 +870,10 @@ void fda_bwd_tile_kernel(const Args a) {
         const float xf = floorf(st[e].x), yf = floorf(st[e].y), zf = floorf(st[e].z);
         lb[e] = ((uint32_t)((int)zf - oz) * (uint32_t)TYp + (uint32_t)((int)yf - oy)) * (uint32_t)TXp +
                 (uint32_t)((int)xf - ox);
-        st[e].x -= xf;
-        st[e].y -= yf;
-        st[e].z -= zf;
+        // LDS record: (fx, attn*fy, attn*(1-fy), fz) -- the owner loop's y weight is static per
+        // (dz, dy) row, so it picks one of the two products
+        const float fx = st[e].x - xf, fy = st[e].y - yf, fz = st[e].z - zf, at = st[e].w;
+        st[e] = make_float4(fx, at * fy, at * (1.f - fy), fz);
         ri[e] = (uint32_t)(((double)en[e] + 0.5) * a.inv_lk);   // sample / (L*K), exact
         if (tid + e * NT < n) atomicAdd(&cur_l[lb[e]], 1u);
       }
@@ -958,9 +959,9 @@ void fda_bwd_tile_kernel(const Args a) {
             float tg[CPL];
 #pragma unroll
             for (int q = 0; q < NW; ++q) Elem<T>::unpack(wv[q], tg + q * Elem<T>::kPerWord);
-            const float wy = dy ? st.y : 1.f - st.y;
-            const float wz = dz ? st.z : 1.f - st.z;
-            const float ayz = st.w * (wy * wz);
+            const float ay = dy ? st.y : st.z;          // attn * (y weight)
+            const float wz = dz ? st.w : 1.f - st.w;
+            const float ayz = ay * wz;
             // base x0-1: (x0, dx=1); base x0: (x0, dx=0), (x0+1, dx=1); base x0+1: (x0+1, dx=0)
             const bool lft = i < m1, ctr = i < m2;
             const float fx = st.x, gx = 1.f - st.x;
