@@ -80,10 +80,10 @@ OPS3D_FDA_API int ops3d_fda_forward(const void *value, const int64_t *spatial_sh
 
 /*
  * Bytes of device workspace ops3d_fda_backward / ops3d_fda_backward_accumulate_f32 need (0 on
- * invalid sizes, or when no HIP device is present to size the sort for): per sample
- * (N = B*Q*G*L*K) a sort key, an index and a 16-byte stash and their sorted copies, per
- * spatial bin (<= 8*B*G*S) a start offset, the radix sort's temporary storage, and head-major
- * copies of value and grad_output (G > 1).  The pointer passed must be 256-byte aligned.
+ * invalid sizes): per sample (N = B*Q*G*L*K) its home tile, tile-local corner word and a 16-byte
+ * stash, up to 8 four-byte tile entries; per tile (<= B*G*S) a count, a start and a cursor; 8
+ * work counters; the bucketing matrix (B*G x 64 x (S/16 + 64) words); and head-major copies of
+ * value and grad_output (G > 1).  The pointer passed must be 256-byte aligned.
  */
 OPS3D_FDA_API size_t ops3d_fda_backward_workspace_bytes(int dtype, int batch, int spatial_size,
                                                         int num_heads, int channels,
@@ -94,10 +94,13 @@ OPS3D_FDA_API size_t ops3d_fda_backward_workspace_bytes(int dtype, int batch, in
  * Backward.  Replaces flash_deform_attn_backward (reference csrc/flash_deform_attn.h:27-52 ->
  * csrc/cuda/flash_deform_attn_cuda.cu:93-179).  Writes every element of grad_value and
  * grad_sampling_loc_attn in `dtype` (the caller need not zero them).  grad_value is a gather:
- * the samples are sorted by base corner (in `workspace`, at least
+ * the samples are grouped by spatial tile (in `workspace`, at least
  * ops3d_fda_backward_workspace_bytes() bytes) and each grad_value row is summed in fp32 by one
- * owner and written once, so the result is deterministic.  Samples whose pixel coordinate lies
- * outside [-1, size) on any axis contribute nothing and get zero location gradients.
+ * owner and written once (no atomics).  The order of that sum follows the order in which the
+ * grouping fills a tile, which can differ between runs, so grad_value can differ at the fp32
+ * rounding level (as with the reference's atomic scatter); grad_sampling_loc_attn is bitwise
+ * repeatable.  Samples whose pixel coordinate lies outside [-1, size) on any axis contribute
+ * nothing and get zero location gradients.
  */
 OPS3D_FDA_API int ops3d_fda_backward(const void *value, const int64_t *spatial_shapes,
                        const int64_t *level_start_index, const void *sampling_loc_attn,
@@ -143,7 +146,7 @@ OPS3D_FDA_API int ops3d_fda_backward_accumulate_f32(
  * ops3d_fda_profile_enable(1), every call records HIP events on its stream around its phases.
  * ops3d_fda_profile_read(which, ms, n) waits for the last call of that kind to finish and writes
  * up to n durations in ms; which = 0 (backward): [0] head-major copies, [1] query-major kernel,
- * [2] sort + permute, [3] bin offsets, [4] value-gradient kernel; which = 1 (forward):
+ * [2] tile counting and head scan, [3] entry scatter, [4] tile kernel; which = 1 (forward):
  * [0] head-major copy, [1] forward kernel.  Returns the number written (0 if nothing recorded).
  * Process-wide state, not thread-safe; enable on the device the calls run on.
  */
