@@ -31,8 +31,9 @@
 #define OPS3D_FDA_TILE_WPE 4    // minimum waves per SIMD the tile kernel is compiled for
 #endif
 
-// Tile order of the tile kernel: 1 = after three static tiles, a per-XCD work counter;
-// 0 = static snake order (no atomics).
+// Tile order of the tile kernel: 1 = a per-XCD work counter after four static tiles when the
+// tiles hold at least a chunk of entries on average (else the static snake order, whose blocks
+// pay no claim per tiny tile); 0 = always the static snake order (no atomics).
 #ifndef OPS3D_FDA_TILE_QUEUE
 #define OPS3D_FDA_TILE_QUEUE 1
 #endif
@@ -700,6 +701,7 @@ void fda_bwd_tile_kernel(const Args a) {
   __shared__ LevelTiles lvt[5];
   __shared__ uint32_t lvbase[6];
   __shared__ int64_t lvsi[5];
+  __shared__ bool queue_l;
   if (tid == 0) {
     uint32_t t = 0;
     for (int u = 0; u < L; ++u) {
@@ -709,9 +711,14 @@ void fda_bwd_tile_kernel(const Args a) {
       t += lvt[u].count;
     }
     lvbase[L] = t;
+    // work counter or static order: from the first head's entries per tile (same in every block)
+    const uint32_t last = t > 0 ? t - 1 : 0;
+    const uint32_t ent = t > 0 ? a.tile_start[last] + a.tile_counts[last] - a.tile_start[0] : 0u;
+    queue_l = OPS3D_FDA_TILE_QUEUE && (uint64_t)ent >= (uint64_t)a.chunk * t;
   }
   __syncthreads();
   const uint32_t T_h = lvbase[L];
+  const bool use_queue = queue_l;
   int xcd = 0, bi = blockIdx.x, nbx = gridDim.x, hpx = G;   // heads served by this block's group
   if (a.tile_affinity) {
     xcd = blockIdx.x & 7;
@@ -772,7 +779,7 @@ void fda_bwd_tile_kernel(const Args a) {
   // anyway (end of an owner phase), so no wave waits for it; the block reads it a tile later.
   __shared__ uint32_t hdr_l[4][2];
   uint32_t k1 = (uint32_t)bi + (uint32_t)nbx, k2 = k1 + (uint32_t)nbx;   // the next two tiles
-  if (!OPS3D_FDA_TILE_QUEUE) {
+  if (!use_queue) {
     k1 = 2u * (uint32_t)nbx - 1u - (uint32_t)bi;
     k2 = 2u * (uint32_t)nbx + (uint32_t)bi;
   }
@@ -807,7 +814,7 @@ void fda_bwd_tile_kernel(const Args a) {
     // claim the tile of position pos + 4 (if pos + 2 exists, the queue may still hold tiles);
     // thread 0 publishes the claim in LDS only before the owner phase's closing barrier (so no
     // wave waits for the atomic), and the block reads it at the end of the next tile
-    const bool claimed = OPS3D_FDA_TILE_QUEUE && k2 < total;
+    const bool claimed = use_queue && k2 < total;
     if (claimed && tid == 0) taken = atomicAdd(a.tile_queue + xcd, 1u);
     int l, b, g;
     uint32_t bgi, t;
@@ -1013,7 +1020,7 @@ void fda_bwd_tile_kernel(const Args a) {
       __syncthreads();
     }
     uint32_t k3;   // the tile of position pos + 3
-    if (OPS3D_FDA_TILE_QUEUE) {
+    if (use_queue) {
       if (pos == 0) {
         k3 = (uint32_t)bi + 3u * (uint32_t)nbx;
       } else {   // claimed at the previous tile
