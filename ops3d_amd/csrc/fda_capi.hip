@@ -172,17 +172,23 @@ hipError_t launch(int dtype, int which, const Geometry &g, hipStream_t st) {
 //   bucketing matrix: B*G x 64 blocks x tcap uint32, tcap = S/16 + 64 tiles per head (volumes
 //                    cut into more tiles are bucketed with global atomics instead)
 //   tile queues    : 8 uint32 (the tile kernel's per-XCD work counters, cleared by the bucketing)
+//                    and the tile kernel's split factor
+//   split scratch  : when fewer than kSplitTiles tiles can exist (at least ceil(S / tile voxels)
+//                    per head), kSplitSlots fp32 partial tiles [tile voxels][D] for the tile
+//                    kernel's split tiles; else nothing
 //   head-major copies of value and grad_output (G > 1)
+constexpr uint64_t kSplitTiles = 2048, kSplitSlots = 4096;
 struct BwdLayout {
   uint64_t n, ntiles_bound;
-  uint32_t tcap;
-  size_t off_keys, off_words, off_stash, off_entries, off_counts, off_start, off_cursor, off_queue, off_mat, off_vhm, off_ghm;
+  uint32_t tcap, split_slots;
+  size_t off_keys, off_words, off_stash, off_entries, off_counts, off_start, off_cursor, off_queue, off_split,
+      off_mat, off_vhm, off_ghm;
   size_t total;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-int bwd_layout(int B, int S, int G, int D, int e, int L, int Q, int K, BwdLayout &ly) {
+int bwd_layout(int B, int S, int G, int D, int e, int lpu, int L, int Q, int K, BwdLayout &ly) {
   ly = BwdLayout{};
   ly.n = (uint64_t)B * Q * G * L * K;
   ly.ntiles_bound = (uint64_t)B * G * (uint64_t)S;
@@ -200,6 +206,12 @@ int bwd_layout(int B, int S, int G, int D, int e, int L, int Q, int K, BwdLayout
   ly.off_start = o; o += t4;
   ly.off_cursor = o; o += t4;
   ly.off_queue = o; o += 256;
+  {
+    const uint64_t tvox = (uint64_t)(2 * tile_threads(lpu) / lpu);   // voxels of a nominal tile
+    const uint64_t lb = (uint64_t)B * G * ((uint64_t)S + tvox - 1) / tvox;
+    ly.split_slots = (S > 0 && lb < kSplitTiles) ? (uint32_t)kSplitSlots : 0u;
+    ly.off_split = o; o += align256((size_t)ly.split_slots * tvox * D * 4);
+  }
   ly.tcap = (uint32_t)(S / 16 + 64);
   ly.off_mat = o; o += align256(tile_matrix_words((uint32_t)(B * G), ly.tcap) * 4);
   ly.off_vhm = o; o += G > 1 ? align256((size_t)B * S * G * D * e) : 0;
@@ -335,7 +347,10 @@ size_t ops3d_fda_backward_workspace_bytes(int dtype, int batch, int spatial_size
       num_levels < 1 || num_query < 0 || num_point < 1)
     return 0;
   BwdLayout ly;
-  if (bwd_layout(batch, spatial_size, num_heads, channels, elem_size(dtype), num_levels, num_query, num_point, ly))
+  int cpl = 0, lpu = 0;
+  if (!pick_config(dtype, channels, cpl, lpu)) return 0;
+  if (bwd_layout(batch, spatial_size, num_heads, channels, elem_size(dtype), tile_lanes(lpu, cpl * elem_size(dtype)),
+                 num_levels, num_query, num_point, ly))
     return 0;
   return ly.total;
 }
@@ -352,7 +367,8 @@ static int backward_impl(const void *value, const void *value_head_major, const 
                          num_point, im2col_step, true, geo);
   if (rc) return rc;
   BwdLayout ly;
-  rc = bwd_layout(batch, spatial_size, num_heads, channels, elem_size(dtype), num_levels, num_query, num_point, ly);
+  rc = bwd_layout(batch, spatial_size, num_heads, channels, elem_size(dtype),
+                  tile_lanes(geo.lpu, geo.cpl * elem_size(dtype)), num_levels, num_query, num_point, ly);
   if (rc) return rc;
   const int64_t nval = (int64_t)batch * spatial_size * num_heads * channels;
   const bool work = (int64_t)batch * num_query > 0;
@@ -396,6 +412,8 @@ static int backward_impl(const void *value, const void *value_head_major, const 
   a.entries = entries;
   a.tile_queue = reinterpret_cast<uint32_t *>(ws + ly.off_queue);
   a.count_clear_wcap = tile_window(ly.tcap);   // the query kernel clears the counters (atomic mode)
+  a.split_scratch = reinterpret_cast<float *>(ws + ly.off_split);
+  a.split_slots = ly.split_slots;
   tile_dims(tile_lanes(geo.lpu, geo.cpl * elem_size(dtype)), a.TX, a.TY, a.TZ);
   a.inv_lk = 1.0 / (double)(num_levels * num_point);
   hipError_t e;
@@ -468,6 +486,16 @@ static int backward_impl(const void *value, const void *value_head_major, const 
       }
     }
 #endif
+    if (ly.split_slots > 0) {
+      // split tiles: add the parts' partial sums (a split needs at least 2 parts per tile, so a
+      // group has at most slots / (2 * groups) tiles; the kernel exits when nothing was split)
+      Geometry g4 = g3;
+      g4.grid = ly.split_slots / 2;
+      g4.lds = 0;
+      e = launch(dtype, 3, g4, st);
+      if (e != hipSuccess)
+        return fail(OPS3D_FDA_ERUNTIME, "split combine kernel launch failed: %s", hipGetErrorString(e));
+    }
   }
   prof_mark(5, st);
   if (g_prof_on) g_prof_recorded[0] = true;

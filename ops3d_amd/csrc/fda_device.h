@@ -49,7 +49,10 @@ struct Args {
   uint32_t *tile_counts;      // [B*G*T_h] entries per tile
   uint32_t *tile_start;       // [B*G*T_h] first entry of each tile (head base + exclusive scan)
   uint32_t *tile_cursor;      // [B*G*T_h] fill cursor of each tile
-  uint32_t *tile_queue;       // [8] tile kernel work counters (one per XCD group), zero at launch
+  uint32_t *tile_queue;       // [8] tile kernel work counters (one per XCD group), zero at launch;
+                              // [8] the tile kernel's split factor, for the combine kernel
+  float *split_scratch;       // [split_slots][tile voxels][D] fp32 partial sums of split tiles
+  uint32_t split_slots;       // scratch slots (0: tiles are never split)
   uint32_t count_clear_wcap;  // != 0: the query kernel zeroes tile_counts when a head has more
                               // tiles than this (the bucketing's atomic mode)
   uint32_t *entries;          // [<= 8N] sample indices, grouped by tile

@@ -728,6 +728,25 @@ void fda_bwd_tile_kernel(const Args a) {
   }
   const uint32_t nbg = (uint32_t)a.B * (uint32_t)hpx;
   const uint32_t total = nbg * T_h;
+  // Split tiles: when the group has fewer tiles than twice its blocks, each tile is cut into F
+  // parts (jobs) over its entry range; a part sums into fp32 and writes its partial to a scratch
+  // slot, and the tile's last part to finish adds the others' partials and writes grad_value.
+  const uint32_t ngroups = a.tile_affinity ? 8u : 1u;
+  uint32_t F = 1;
+  if (a.split_slots > 0 && total > 0 && total < 2u * (uint32_t)nbx) {
+    F = min((2u * (uint32_t)nbx + total - 1u) / total, 8u);
+    F = min(F, a.split_slots / ngroups / total);
+    if (F < 1) F = 1;
+  }
+  const uint32_t njobs = total * F;
+  if (blockIdx.x == 0 && tid == 0) a.tile_queue[8] = F;   // for the combine kernel
+  const uint32_t gslot = (uint32_t)xcd * (a.split_slots / ngroups);   // the group's first slot
+  // part `part` of F of a tile with entries [s0, s0 + c)
+  const auto part_range = [&](uint32_t s0, uint32_t c, uint32_t part, uint32_t &hs, uint32_t &hc) {
+    const uint32_t lo = (uint32_t)((uint64_t)c * part / F), hi = (uint32_t)((uint64_t)c * (part + 1u) / F);
+    hs = s0 + lo;
+    hc = hi - lo;
+  };
   // grad_output rows in sample order / (L*K): the head-major copy, or grad_out itself (G == 1)
   const T *go = static_cast<const T *>(a.gout_hm ? a.gout_hm : a.grad_out);
 
@@ -783,18 +802,24 @@ void fda_bwd_tile_kernel(const Args a) {
     k1 = 2u * (uint32_t)nbx - 1u - (uint32_t)bi;
     k2 = 2u * (uint32_t)nbx + (uint32_t)bi;
   }
-  uint32_t hs_pend = 0, hc_pend = 0;   // header of k2 (thread 0), not yet in the ring
+  // header of k2 (thread 0: the tile's first entry and count, and k2's part), not yet in the ring
+  uint32_t hs_pend = 0, hc_pend = 0, hp_pend = 0;
   if (tid == 0) {
     const uint32_t kk[2] = {(uint32_t)bi, k1};
     for (int i = 0; i < 2; ++i) {
-      const uint32_t gid = kk[i] < total ? tile_gid(kk[i]) : 0u;
-      hdr_l[i][0] = kk[i] < total ? a.tile_start[gid] : 0u;
-      hdr_l[i][1] = kk[i] < total ? a.tile_counts[gid] : 0u;
+      uint32_t hs = 0u, hc = 0u;
+      if (kk[i] < njobs) {
+        const uint32_t gid = tile_gid(kk[i] / F);
+        part_range(a.tile_start[gid], a.tile_counts[gid], kk[i] % F, hs, hc);
+      }
+      hdr_l[i][0] = hs;
+      hdr_l[i][1] = hc;
     }
-    if (k2 < total) {
-      const uint32_t gid = tile_gid(k2);
+    if (k2 < njobs) {
+      const uint32_t gid = tile_gid(k2 / F);
       hs_pend = a.tile_start[gid];
       hc_pend = a.tile_counts[gid];
+      hp_pend = k2 % F;
     }
   }
   __syncthreads();
@@ -810,15 +835,16 @@ void fda_bwd_tile_kernel(const Args a) {
     pE[e] = 0u;
     pS[e] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  for (uint32_t k = (uint32_t)bi; k < total;) {
-    // claim the tile of position pos + 4 (if pos + 2 exists, the queue may still hold tiles);
+  for (uint32_t k = (uint32_t)bi; k < njobs;) {
+    // claim the job of position pos + 4 (if pos + 2 exists, the queue may still hold jobs);
     // thread 0 publishes the claim in LDS only before the owner phase's closing barrier (so no
-    // wave waits for the atomic), and the block reads it at the end of the next tile
-    const bool claimed = use_queue && k2 < total;
+    // wave waits for the atomic), and the block reads it at the end of the next job
+    const bool claimed = use_queue && k2 < njobs;
     if (claimed && tid == 0) taken = atomicAdd(a.tile_queue + xcd, 1u);
+    const uint32_t ktile = k / F, part = k - ktile * F;
     int l, b, g;
     uint32_t bgi, t;
-    decode(k, l, bgi, t);
+    decode(ktile, l, bgi, t);
     head_of(bgi, b, g);
     const LevelTiles lt = lvt[l];
     const int itx = (int)(t % (uint32_t)lt.nt[2]);
@@ -864,7 +890,7 @@ void fda_bwd_tile_kernel(const Args a) {
       const bool nxt_here = c0 + (uint32_t)CH < e1;
       const uint32_t nc0 = nxt_here ? c0 + (uint32_t)CH : ns;
       const uint32_t nn = nxt_here ? min((uint32_t)CH, e1 - nc0) : min((uint32_t)CH, nc);
-      const bool npf = nxt_here || (k1 < total && nc > 0);
+      const bool npf = nxt_here || (k1 < njobs && nc > 0);
       for (int i = tid; i < nb; i += NT) cur_l[i] = 0u;
       __syncthreads();
       TILE_MARK(0);
@@ -984,13 +1010,26 @@ void fda_bwd_tile_kernel(const Args a) {
       }
       if (tid == 0) {
         grab_l[pos & 3u] = claimed ? taken : ~0u;
-        hdr_l[(pos + 2u) & 3u][0] = hs_pend;
-        hdr_l[(pos + 2u) & 3u][1] = hc_pend;
+        uint32_t hs, hc;
+        part_range(hs_pend, hc_pend, hp_pend, hs, hc);
+        hdr_l[(pos + 2u) & 3u][0] = hs;
+        hdr_l[(pos + 2u) & 3u][1] = hc;
       }
       __syncthreads();
       TILE_MARK(4);
     }
-    if (live) {
+    if (F > 1) {
+      // this part's sums go to its scratch slot (voxels of the nominal tile: pair p, x-half h);
+      // fda_bwd_split_combine_kernel adds a tile's parts and writes its rows
+      constexpr int kTileVox = 2 * (NT / LPU);
+      float *sl = a.split_scratch + ((size_t)(gslot + ktile * F + part) * kTileVox + (size_t)p * 2u) * (uint32_t)D +
+                  (uint32_t)(j * CPL);
+      if (live) {
+        store_elems<float, CPL>(sl, acc0);
+        if (two) store_elems<float, CPL>(sl + D, acc1);
+      }
+    }
+    if (live && F == 1) {
       const int64_t vox = lvsi[l] + ((int64_t)z * Hl + y) * Wl + x0;
       const int64_t o = (((int64_t)b * a.S + vox) * G + g) * D + j * CPL;
       for (int h = 0; h < (two ? 2 : 1); ++h) {
@@ -1014,8 +1053,10 @@ void fda_bwd_tile_kernel(const Args a) {
     if (e0 == e1) {   // no chunk: publish the claim here
       if (tid == 0) {
         grab_l[pos & 3u] = claimed ? taken : ~0u;
-        hdr_l[(pos + 2u) & 3u][0] = hs_pend;
-        hdr_l[(pos + 2u) & 3u][1] = hc_pend;
+        uint32_t hs, hc;
+        part_range(hs_pend, hc_pend, hp_pend, hs, hc);
+        hdr_l[(pos + 2u) & 3u][0] = hs;
+        hdr_l[(pos + 2u) & 3u][1] = hc;
       }
       __syncthreads();
     }
@@ -1023,20 +1064,21 @@ void fda_bwd_tile_kernel(const Args a) {
     if (use_queue) {
       if (pos == 0) {
         k3 = (uint32_t)bi + 3u * (uint32_t)nbx;
-      } else {   // claimed at the previous tile
+      } else {   // claimed at the previous job
         const uint32_t raw = grab_l[(pos - 1u) & 3u];
-        k3 = raw == ~0u ? total : 4u * (uint32_t)nbx + raw;
+        k3 = raw == ~0u ? njobs : 4u * (uint32_t)nbx + raw;
       }
-      if (k3 >= total) k3 = total;
+      if (k3 >= njobs) k3 = njobs;
     } else {   // static snake order: position p takes p*nbx + (p odd ? nbx-1-bi : bi)
       const uint32_t p3 = pos + 3u;
       k3 = p3 * (uint32_t)nbx + ((p3 & 1u) ? (uint32_t)(nbx - 1 - bi) : (uint32_t)bi);
-      if (k3 >= total) k3 = total;
+      if (k3 >= njobs) k3 = njobs;
     }
-    if (tid == 0 && k3 < total) {
-      const uint32_t gid = tile_gid(k3);
+    if (tid == 0 && k3 < njobs) {
+      const uint32_t gid = tile_gid(k3 / F);
       hs_pend = a.tile_start[gid];
       hc_pend = a.tile_counts[gid];
+      hp_pend = k3 % F;
     }
     k = k1; k1 = k2; k2 = k3;
     ++pos;
@@ -1046,6 +1088,81 @@ void fda_bwd_tile_kernel(const Args a) {
     for (int i = 0; i < 6; ++i) atomicAdd(a.dbg + i, t_acc[i]);
 #endif
 #undef TILE_MARK
+}
+
+// Split tiles (see the tile kernel): one block per tile of every group adds the F parts'
+// partial sums of each of its voxels and writes the rows (in T, or added to the caller's fp32
+// buffer).  Runs after the tile kernel, so plain loads see the parts; exits when F == 1.
+template <typename T, int CPL, int LPU>
+__global__ __launch_bounds__(tile_threads(LPU)) void fda_bwd_split_combine_kernel(const Args a) {
+  constexpr int NT = tile_threads(LPU);
+  constexpr int kTileVox = 2 * (NT / LPU);
+  const uint32_t F = a.tile_queue[8];
+  if (F <= 1) return;
+  const int tid = threadIdx.x, D = a.D, G = a.G, L = a.L;
+  const int p = tid / LPU, j = tid & (LPU - 1);
+  const int hxn = a.TX / 2;
+  const int px = p % hxn, py = (p / hxn) % a.TY, pz = p / (hxn * a.TY);
+  const uint32_t T_h = tiles_per_head(a.shapes, L, a.TX, a.TY, a.TZ);
+  const uint32_t ngroups = a.tile_affinity ? 8u : 1u;
+  const int hpx = a.tile_affinity ? G / 8 : G;
+  const uint32_t nbg = (uint32_t)a.B * (uint32_t)hpx, total = nbg * T_h;
+  const uint32_t xcd = blockIdx.x % ngroups, k = blockIdx.x / ngroups;   // tile k of group xcd
+  if (k >= total) return;
+  // k -> (level, head, tile) as in the tile kernel: coarse (last) levels first
+  uint32_t rem = k;
+  int l = L - 1;
+  for (; l > 0; --l) {
+    const uint32_t nl = nbg * level_tiles(a.shapes, l, a.TX, a.TY, a.TZ).count;
+    if (rem < nl) break;
+    rem -= nl;
+  }
+  const LevelTiles lt = level_tiles(a.shapes, l, a.TX, a.TY, a.TZ);
+  const uint32_t bgi = rem / lt.count, t = rem - bgi * lt.count;
+  const int b = (int)(bgi / (uint32_t)hpx);
+  const int g = a.tile_affinity ? (int)xcd + 8 * (int)(bgi % (uint32_t)hpx) : (int)(bgi % (uint32_t)hpx);
+  const int itx = (int)(t % (uint32_t)lt.nt[2]);
+  const int ity = (int)((t / (uint32_t)lt.nt[2]) % (uint32_t)lt.nt[1]);
+  const int itz = (int)(t / ((uint32_t)lt.nt[2] * (uint32_t)lt.nt[1]));
+  const int z = itz * lt.t[0] + pz, y = ity * lt.t[1] + py, x0 = itx * lt.t[2] + 2 * px;
+  const bool live = 2 * px < lt.t[2] && py < lt.t[1] && pz < lt.t[0] && z < lt.n[0] && y < lt.n[1] && x0 < lt.n[2];
+  if (!live) return;
+  const bool two = 2 * px + 1 < lt.t[2] && x0 + 1 < lt.n[2];
+  const uint32_t gslot = xcd * (a.split_slots / ngroups);
+  const float *sl = a.split_scratch + ((size_t)(gslot + k * F) * kTileVox + (size_t)p * 2u) * (uint32_t)D +
+                    (uint32_t)(j * CPL);
+  float acc0[CPL], acc1[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) acc0[c] = acc1[c] = 0.f;
+  for (uint32_t q = 0; q < F; ++q) {
+    float o0[CPL], o1[CPL];
+    const float *sq = sl + (size_t)q * kTileVox * D;
+    load_global_elems<float, CPL>(sq, o0);
+    load_global_elems<float, CPL>(two ? sq + D : sq, o1);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      acc0[c] += o0[c];
+      acc1[c] += two ? o1[c] : 0.f;
+    }
+  }
+  const int64_t vox = a.lsi[l] + ((int64_t)z * lt.n[1] + y) * lt.n[2] + x0;
+  const int64_t o = (((int64_t)b * a.S + vox) * G + g) * D + j * CPL;
+  for (int h = 0; h < (two ? 2 : 1); ++h) {
+    float res[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) res[c] = h ? acc1[c] : acc0[c];
+    const int64_t oh = o + (int64_t)h * G * D;
+    if (a.accumulate) {
+      float *dst = static_cast<float *>(a.out) + oh;
+      float old[CPL];
+      load_global_elems<float, CPL>(dst, old);
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) res[c] += old[c];
+      store_elems<float, CPL>(dst, res);
+    } else {
+      store_elems<T, CPL>(static_cast<T *>(a.out) + oh, res);
+    }
+  }
 }
 
 // which: 0 forward, 1 backward phase 1 (query-major), 2 backward phase 3 (tile-major)
@@ -1062,6 +1179,11 @@ hipError_t launch_one(int which, const Args &a, unsigned grid, size_t lds, hipSt
       hipLaunchKernelGGL((fda_bwd_query_pair_kernel<T, CPL>), dim3(grid), dim3(kBlock), lds, st, a);
     else
       hipLaunchKernelGGL((fda_bwd_query_kernel<T, CPL, LPU>), dim3(grid), dim3(kBlock), lds, st, a);
+  }
+  else if (which == 3) {
+    // one block per tile of every group (`grid` = the bound on tiles times the groups)
+    constexpr int TL = tile_lanes(LPU, CPL * (int)sizeof(T)), TC = CPL * LPU / TL;
+    hipLaunchKernelGGL((fda_bwd_split_combine_kernel<T, TC, TL>), dim3(grid), dim3(tile_threads(TL)), 0, st, a);
   }
   else {
     // persistent: `grid` (the CU count, a multiple of 8 with XCD affinity) times the blocks that

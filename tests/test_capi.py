@@ -63,12 +63,20 @@ def test_workspace_bytes(lib):
     def al(x):
         return (x + 255) // 256 * 256
 
-    # keys, words, stash, <= 8 entries per sample, 3 tile arrays of B*G*S+1 words, the bucketing
-    # matrix (64 blocks x S/16+64 tiles per head), head-major copies of value and grad_output
-    want = (2 * al(4 * n) + al(16 * n) + al(32 * n) + 3 * al(4 * (B * G * S + 1)) + 256
-            + al(4 * B * G * 64 * (S // 16 + 64)) + al(B * S * G * D * 2) + al(B * Q * G * D * 2))
-    assert lib.ops3d_fda_backward_workspace_bytes(2, B, S, G, D, L, Q, K) == want
+    # keys, words, stash, <= 8 entries per sample, 3 tile arrays of B*G*S+1 words, the work
+    # counters, the split scratch, the bucketing matrix (64 blocks x S/16+64 tiles per head),
+    # head-major copies of value and grad_output; no split scratch at c4 (at least
+    # B*G*S/128 = 4608 tiles)
+    def want(B, S, G, D, L, Q, K, split_slots):
+        n = B * Q * G * L * K
+        return (2 * al(4 * n) + al(16 * n) + al(32 * n) + 3 * al(4 * (B * G * S + 1)) + 256
+                + al(split_slots * 128 * D * 4)
+                + al(4 * B * G * 64 * (S // 16 + 64)) + al(B * S * G * D * 2) + al(B * Q * G * D * 2))
+    assert lib.ops3d_fda_backward_workspace_bytes(2, B, S, G, D, L, Q, K) == want(B, S, G, D, L, Q, K, 0)
     assert lib.ops3d_fda_backward_workspace_bytes(9, B, S, G, D, L, Q, K) == 0
+    # c2: at least 8 * 4608/128 = 288 tiles (< 2048): 4096 scratch tiles for split tiles
+    c2 = (1, 4608, 8, 32, 2, 4608, 4)
+    assert lib.ops3d_fda_backward_workspace_bytes(2, *c2) == want(*c2, 4096)
 
 
 def _fwd(lib, **kw):
