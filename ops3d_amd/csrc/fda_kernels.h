@@ -38,6 +38,15 @@
 #define OPS3D_FDA_TILE_QUEUE 1
 #endif
 
+// Tile splitting (tile kernel): parts per tile aim at SPLIT_TARGET jobs per block, at most
+// SPLIT_MAX parts per tile.
+#ifndef OPS3D_FDA_SPLIT_TARGET
+#define OPS3D_FDA_SPLIT_TARGET 2u
+#endif
+#ifndef OPS3D_FDA_SPLIT_MAX
+#define OPS3D_FDA_SPLIT_MAX 8u
+#endif
+
 // Occupancy hint of the backward query pair kernel (waves per SIMD it is compiled for; 0: none).
 // Left to itself the compiler takes 107 VGPRs (4 waves); 5 waves fit without spills.
 #ifndef OPS3D_FDA_QUERY_WPE
@@ -734,7 +743,7 @@ void fda_bwd_tile_kernel(const Args a) {
   const uint32_t ngroups = a.tile_affinity ? 8u : 1u;
   uint32_t F = 1;
   if (a.split_slots > 0 && total > 0 && total < 2u * (uint32_t)nbx) {
-    F = min((2u * (uint32_t)nbx + total - 1u) / total, 8u);
+    F = min((OPS3D_FDA_SPLIT_TARGET * (uint32_t)nbx + total - 1u) / total, (uint32_t)OPS3D_FDA_SPLIT_MAX);
     F = min(F, a.split_slots / ngroups / total);
     if (F < 1) F = 1;
   }
