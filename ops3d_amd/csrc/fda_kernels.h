@@ -651,17 +651,21 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
 // Backward phase 3, tile-major: grad_value of one tile = for every voxel v of the tile, the sum of
 // attn * w_corner * grad_out over the tile's entries (samples) with a corner at v.  A block of
 // tile_threads(LPU) threads owns the tile: LPU lanes own an x-pair of voxels (x0, x0+1) and CPL channels,
-// and keep their sums in registers.  The tile's entries are processed in chunks:
-//   1. stage each entry's stash (fx, fy, fz, attn) and grad_output row in LDS, and count the
-//      entries of each local bin (base corner in [-1,tx) x [-1,ty) x [-1,tz), LDS atomics),
+// and keep their sums in registers.  The tile's entries (sample indices) are processed in chunks:
+//   1. each thread takes kTileKPT entries and their stash (pixel coordinates, attention weight),
+//      finds the local bin of the base corner (in [-1,tx) x [-1,ty) x [-1,tz)) and counts it
+//      (LDS atomics),
 //   2. exclusive scan of the bin counts,
-//   3. counting-sort the chunk by bin (LDS atomics),
+//   3. counting sort: each entry's weights (fx, attn*fy, attn*(1-fy), fz) and grad_output row
+//      index go to its sorted position in LDS, then the rows are loaded straight into LDS in
+//      that order,
 //   4. each owner walks the entries of the bins with a corner on its voxels -- for each (dz, dy)
 //      the three contiguous bins of base x0-1, x0, x0+1 -- reading only LDS.
-// Every grad_value row of the tile is written once, in T (or added to an fp32 buffer): no
-// zero-fill, no global atomics.  Tiles are scheduled coarse levels first (their tiles hold the
-// most entries), and with G % 8 == 0 the tiles of head g run on XCD g % 8, whose L2 then holds
-// that head's grad_output rows.
+// The next chunk's entries and stash are loaded during the current chunk.  Every grad_value row
+// of the tile is written once, in T (or added to an fp32 buffer): no zero-fill, no global
+// atomics; split tiles (small volumes) write fp32 partials that a combine kernel adds.  Tiles
+// are scheduled coarse levels first (their tiles hold the most entries), and with G % 8 == 0
+// the tiles of head g run on XCD g % 8, whose L2 then holds that head's grad_output rows.
 
 // Exclusive scan across the NT threads of a block; tmp holds NT/64 words.
 template <int NT>
