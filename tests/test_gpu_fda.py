@@ -144,6 +144,31 @@ def test_all_samples_outside_volume(gpu_device):
     _check("all outside fp32", inp, gpu_device, torch.float32)
 
 
+# --- seeded random configurations ------------------------------------------------------------
+def _random_config(seed):
+    """A small random problem: 1-4 levels of 1-24 voxels per axis, B 1-3, Q 1-400, G in
+    {1, 2, 4, 8, 16}, D in {16, 32, 48}, K 1-8, some samples outside the volume.  Across the
+    seeds this mixes split and unsplit tile launches, both tile orders and all XCD mappings."""
+    r = np.random.default_rng(1000 + seed)
+    L = int(r.integers(1, 5))
+    shapes = [tuple(int(x) for x in r.integers(1, 25, size=3)) for _ in range(L)]
+    B = int(r.integers(1, 4))
+    Q = int(r.integers(1, 401))
+    G = int(r.choice([1, 2, 4, 8, 16]))
+    D = int(r.choice([16, 32, 48]))
+    K = int(r.integers(1, 9))
+    dt = torch.float32 if seed % 2 == 0 else torch.bfloat16
+    return shapes, B, Q, G, D, K, dt
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_configs(gpu_device, seed):
+    shapes, B, Q, G, D, K, dt = _random_config(seed)
+    inp = random_inputs(shapes, B, Q, G, D, K, dt, seed=seed, lo=-0.1, hi=1.1)
+    _check(f"random #{seed}: L={len(shapes)} B={B} Q={Q} G={G} D={D} K={K}", inp, gpu_device, dt,
+           im2col_step=B)
+
+
 # --- head widths, head counts (XCD mappings), dtypes ---------------------------------------
 @pytest.mark.parametrize("D", [8, 16, 24, 32, 48, 64, 96, 128])
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16])
