@@ -835,6 +835,7 @@ void fda_bwd_tile_kernel(const Args a) {
       hp_pend = k2 % F;
     }
   }
+  for (int i = tid; i < NBX; i += NT) cur_l[i] = 0u;   // bin counters of the first chunk
   __syncthreads();
   uint32_t pos = 0;   // position of the current tile in the block's sequence
   // the work counter's value claimed for the current tile (thread 0; declared outside the tile
@@ -904,8 +905,7 @@ void fda_bwd_tile_kernel(const Args a) {
       const uint32_t nc0 = nxt_here ? c0 + (uint32_t)CH : ns;
       const uint32_t nn = nxt_here ? min((uint32_t)CH, e1 - nc0) : min((uint32_t)CH, nc);
       const bool npf = nxt_here || (k1 < njobs && nc > 0);
-      for (int i = tid; i < nb; i += NT) cur_l[i] = 0u;
-      __syncthreads();
+      // (the bin counters are zero here: cleared at the start and after every owner phase)
       TILE_MARK(0);
       // 1a. local bin of each entry's base corner, grad_output row index, bin counts.  The stash
       // holds the pixel coordinates: base corner = floor, fraction = coordinate - floor (exact).
@@ -1021,6 +1021,8 @@ void fda_bwd_tile_kernel(const Args a) {
           }
         }
       }
+      // the owners do not read the bin counters: clear them for the next chunk before the barrier
+      for (int i = tid; i < NBX; i += NT) cur_l[i] = 0u;
       if (tid == 0) {
         grab_l[pos & 3u] = claimed ? taken : ~0u;
         uint32_t hs, hc;
