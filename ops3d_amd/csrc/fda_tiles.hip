@@ -64,22 +64,22 @@ __device__ __forceinline__ void level_grids(const BucketArgs &a, LevelGrid *lg) 
   }
 }
 
-// Calls f(tile id, tile-local word) for each entry of sample (key, word).
+// Calls f(tile id, tile-local word) for each entry of sample (key, word): the home tile, then
+// each of the 7 neighbour combinations (x, y, z bits of c) whose flags are all set.  Straight-line
+// predicated calls: with 64 lanes every combination is taken by some lane, so a per-lane loop
+// would run all 8 rounds anyway, with loop control on top.
 template <typename F>
 __device__ __forceinline__ void for_each_entry(uint32_t key, uint32_t word, const LevelGrid *lg, F &&f) {
-  const uint32_t ex = (word >> 15) & 1u, ey = (word >> 16) & 1u, ez = (word >> 17) & 1u;
+  const uint32_t fl = (word >> 15) & 7u;   // bit 0: next x tile, bit 1: y, bit 2: z
   const LevelGrid g = lg[word >> 18];
   const uint32_t base = word & 0x7fffu;
-  for (uint32_t dz = 0; dz <= ez; ++dz)
-    for (uint32_t dy = 0; dy <= ey; ++dy)
-      for (uint32_t dx = 0; dx <= ex; ++dx) {
-        // in the next tile along an axis the base corner is at local -1 (stored as 0)
-        uint32_t w = base;
-        if (dx) w &= ~0x1fu;
-        if (dy) w &= ~(0x1fu << 5);
-        if (dz) w &= ~(0x1fu << 10);
-        f(key + dx + dy * g.sy + dz * g.sz, w);
-      }
+  f(key, base);
+  static_for<7>([&](auto cc) {
+    constexpr uint32_t c = decltype(cc)::value + 1;
+    // in the next tile along an axis the base corner is at local -1 (stored as 0)
+    constexpr uint32_t keep = ~(((c & 1u) ? 0x1fu : 0u) | ((c & 2u) ? 0x1fu << 5 : 0u) | ((c & 4u) ? 0x1fu << 10 : 0u));
+    if ((fl & c) == c) f(key + (c & 1u) + ((c & 2u) ? g.sy : 0u) + ((c & 4u) ? g.sz : 0u), base & keep);
+  });
 }
 
 __global__ __launch_bounds__(1024) void tile_clear_kernel(const BucketArgs a) {
