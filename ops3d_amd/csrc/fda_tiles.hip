@@ -125,23 +125,28 @@ __global__ __launch_bounds__(kBucketThreads) void tile_count_kernel(const Bucket
   const uint32_t w0 = bg * T_h;
   // batches of kCountBatch samples per thread: all their loads are issued before any is used
   constexpr int kCountBatch = 8;
-  for (uint32_t sb = s0 + threadIdx.x; sb < s1; sb += kCountBatch * kBucketThreads) {
-    uint32_t key[kCountBatch], word[kCountBatch];
+  // all_in (every tile of the head in the window) drops the global-atomic path from the code
+  const auto count_all = [&](auto all_in) {
+    for (uint32_t sb = s0 + threadIdx.x; sb < s1; sb += kCountBatch * kBucketThreads) {
+      uint32_t key[kCountBatch], word[kCountBatch];
 #pragma unroll
-    for (int i = 0; i < kCountBatch; ++i) {
-      const uint32_t s = sb + (uint32_t)i * kBucketThreads;
-      key[i] = s < s1 ? a.keys[s] : kKeyInvalid;
-      word[i] = s < s1 ? a.words[s] : 0u;
-    }
+      for (int i = 0; i < kCountBatch; ++i) {
+        const uint32_t s = sb + (uint32_t)i * kBucketThreads;
+        key[i] = s < s1 ? a.keys[s] : kKeyInvalid;
+        word[i] = s < s1 ? a.words[s] : 0u;
+      }
 #pragma unroll
-    for (int i = 0; i < kCountBatch; ++i) {
-      if (key[i] == kKeyInvalid) continue;
-      for_each_entry(key[i], word[i], lg, [&](uint32_t id, uint32_t) {
-        if (id - w0 < nw) atomicAdd(&win[id - w0], 1u);
-        else atomicAdd(&a.counts[id], 1u);
-      });
+      for (int i = 0; i < kCountBatch; ++i) {
+        if (key[i] == kKeyInvalid) continue;
+        for_each_entry(key[i], word[i], lg, [&](uint32_t id, uint32_t) {
+          if (decltype(all_in)::value || id - w0 < nw) atomicAdd(&win[id - w0], 1u);
+          else atomicAdd(&a.counts[id], 1u);
+        });
+      }
     }
-  }
+  };
+  if (nw == T_h) count_all(IntConst<1>{});
+  else count_all(IntConst<0>{});
   __syncthreads();
   if (matrix_mode(a, T_h)) {
     uint32_t hb, hc;
@@ -205,6 +210,7 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
   }
   __syncthreads();
   constexpr int SPT = kRound / kBucketThreads;
+  const bool all_in = nw == T_h;   // no tile outside the window: no global-atomic path
   const uint32_t per = (nw + kBucketThreads - 1) / kBucketThreads;   // tiles per thread in the scans
   for (uint32_t r0 = s0; r0 < s1; r0 += kRound) {
     uint32_t key[SPT], word[SPT];
@@ -215,15 +221,19 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
       word[k] = s < s1 ? a.words[s] : 0u;
     }
     // (a) the round's entries per tile; tiles outside the window take a position at once
+    const auto count_round = [&](auto all_in) {
 #pragma unroll
-    for (int k = 0; k < SPT; ++k) {
-      if (key[k] == kKeyInvalid) continue;
-      const uint32_t s = r0 + (uint32_t)(k * kBucketThreads + tid);
-      for_each_entry(key[k], word[k], lg, [&](uint32_t id, uint32_t) {
-        if (id - w0 < nw) atomicAdd(&cur[id - w0], 1u);
-        else a.entries[atomicAdd(&a.cursor[id], 1u)] = s;
-      });
-    }
+      for (int k = 0; k < SPT; ++k) {
+        if (key[k] == kKeyInvalid) continue;
+        const uint32_t s = r0 + (uint32_t)(k * kBucketThreads + tid);
+        for_each_entry(key[k], word[k], lg, [&](uint32_t id, uint32_t) {
+          if (decltype(all_in)::value || id - w0 < nw) atomicAdd(&cur[id - w0], 1u);
+          else a.entries[atomicAdd(&a.cursor[id], 1u)] = s;
+        });
+      }
+    };
+    if (all_in) count_round(IntConst<1>{});
+    else count_round(IntConst<0>{});
     __syncthreads();
     // (b) exclusive scan of the counts: cur = the tile's first staging slot; win -= that slot,
     // so that staging slot i of tile t goes to win[t] + i
@@ -262,19 +272,23 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
     __syncthreads();
     const uint32_t staged = min(scan_tmp[kBucketThreads / kWave], (uint32_t)kStage);
     // (c) placement: staging slot by tile (LDS), or the final position past the capacity
+    const auto place_round = [&](auto all_in) {
 #pragma unroll
-    for (int k = 0; k < SPT; ++k) {
-      if (key[k] == kKeyInvalid) continue;
-      const uint32_t so = (uint32_t)(k * kBucketThreads + tid);
-      for_each_entry(key[k], word[k], lg, [&](uint32_t id, uint32_t) {
-        const uint32_t t = id - w0;
-        if (t < nw) {
-          const uint32_t slot = atomicAdd(&cur[t], 1u);
-          if (slot < (uint32_t)kStage) rec[slot] = (t << kRoundBits) | so;
-          else a.entries[win[t] + slot] = r0 + so;
-        }
-      });
-    }
+      for (int k = 0; k < SPT; ++k) {
+        if (key[k] == kKeyInvalid) continue;
+        const uint32_t so = (uint32_t)(k * kBucketThreads + tid);
+        for_each_entry(key[k], word[k], lg, [&](uint32_t id, uint32_t) {
+          const uint32_t t = id - w0;
+          if (decltype(all_in)::value || t < nw) {
+            const uint32_t slot = atomicAdd(&cur[t], 1u);
+            if (slot < (uint32_t)kStage) rec[slot] = (t << kRoundBits) | so;
+            else a.entries[win[t] + slot] = r0 + so;
+          }
+        });
+      }
+    };
+    if (all_in) place_round(IntConst<1>{});
+    else place_round(IntConst<0>{});
     __syncthreads();
     // (d) the staged entries in tile order: runs of consecutive positions
     for (uint32_t i = tid; i < staged; i += kBucketThreads) {
