@@ -8,13 +8,15 @@
 // Matrix mode (the head has at most wcap = min(tcap, kWin) tiles; tcap is what the workspace
 // holds, and the LDS window is wcap tiles):
 //   tile_count:    each block writes its histogram as a row of a [head][block][tile] matrix,
-//   tile_headscan: one block per head: per tile, exclusive prefix over the head's blocks (in
-//                  place) and the tile's total; exclusive scan of the totals -> tile_start,
-//   tile_scatter:  block c's entries of tile t go to tile_start[t] + prefix[c][t] + their rank
-//                  among the block's entries of t (LDS staging, below).
+//   tile_headscan: per tile (64 tiles per block), exclusive prefix over the head's blocks (in
+//                  place) and the tile's total,
+//   tile_scatter:  every block scans its head's tile totals -> tile starts (block 0 of the
+//                  head stores them); block c's entries of tile t go to tile_start[t] +
+//                  prefix[c][t] + their rank among the block's entries of t (LDS staging).
 //   No global atomics: every position is computed.
 // Atomic mode (more tiles): the histograms are flushed with global atomics into zeroed
-// counters, and tile_scatter reserves each block's range of a tile with one global atomic on
+// counters, tile_headscan scans them per head (one block) into tile_start and the cursors,
+// and tile_scatter reserves each block's range of a tile with one global atomic on
 // the tile's cursor.  Correct for any size, slower (the atomics of all blocks contend).
 // Each head owns the entry range [bg * 8 * per_head, ...) (a sample has at most 8 entries), so
 // heads are bucketed independently; a tile's entries are [tile_start, tile_start + count).
@@ -40,7 +42,7 @@ struct BucketArgs {
   int L, BG, TX, TY, TZ;
   uint32_t *counts;            // [BG * T_h] entries per tile
   uint32_t *cursor;            // [BG * T_h]
-  const uint32_t *start;       // [BG * T_h + 1]
+  uint32_t *start;             // [BG * T_h + 1]
   uint32_t *mat;               // [BG][blocks_per_head][T_h] (matrix mode)
   uint32_t tcap;               // matrix mode when T_h <= tcap
   uint32_t wcap;               // LDS histogram window in tiles: min(tcap, kWin)
@@ -158,6 +160,47 @@ __global__ __launch_bounds__(kBucketThreads) void tile_count_kernel(const Bucket
   }
 }
 
+// Exclusive scan of cnt[0, n) (LDS) by the kBucketThreads threads of the block, thread i taking
+// the run [i * per, (i + 1) * per): f(k, prefix of k) for each k, after cnt[k] is read (f may
+// overwrite it).  Returns the total.  Starts and ends with a block barrier's worth of order:
+// cnt must be complete before the call; f's LDS writes need a barrier before others read them.
+template <typename F>
+__device__ __forceinline__ uint32_t block_scan(const uint32_t *cnt, uint32_t n, uint32_t per, uint32_t *scan_tmp,
+                                               F &&f) {
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
+  const uint32_t b0 = (uint32_t)tid * per;
+  uint32_t sum = 0;
+  for (uint32_t i = 0; i < per; ++i)
+    if (b0 + i < n) sum += cnt[b0 + i];
+  uint32_t inc = sum;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint32_t y = __shfl_up(inc, o, kWave);
+    if (lane >= o) inc += y;
+  }
+  if (lane == kWave - 1) scan_tmp[wv] = inc;
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t run = 0;
+    for (int w = 0; w < kBucketThreads / kWave; ++w) {
+      const uint32_t t = scan_tmp[w];
+      scan_tmp[w] = run;
+      run += t;
+    }
+    scan_tmp[kBucketThreads / kWave] = run;
+  }
+  __syncthreads();
+  uint32_t run = scan_tmp[wv] + inc - sum;
+  const uint32_t total = scan_tmp[kBucketThreads / kWave];
+  for (uint32_t i = 0; i < per; ++i)
+    if (b0 + i < n) {
+      const uint32_t c = cnt[b0 + i];
+      f(b0 + i, run);
+      run += c;
+    }
+  return total;
+}
+
 // Entries are staged in LDS before they are written: a round of kRound samples is counted per
 // tile, scanned, and placed in LDS grouped by tile; the writes then go out in that order, so
 // consecutive lanes write consecutive positions of a tile's run instead of one scattered word
@@ -179,7 +222,7 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
   __shared__ uint32_t scan_tmp[kBucketThreads / kWave + 1];
   const uint32_t T_h = tiles_per_head(a.shapes, a.L, a.TX, a.TY, a.TZ);
   const uint32_t nw = min(T_h, a.wcap);
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
+  const int tid = threadIdx.x;
   if (tid == 0) level_grids(a, lg);
   for (uint32_t i = tid; i < nw; i += kBucketThreads) {
     win[i] = 0u;
@@ -189,11 +232,20 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
   uint32_t bg, s0, s1;
   block_range(a, bg, s0, s1);
   const uint32_t w0 = bg * T_h;
+  const uint32_t per = (nw + kBucketThreads - 1) / kBucketThreads;   // tiles per thread in the scans
   if (matrix_mode(a, T_h)) {
-    // the block's first position in each tile: tile start + the earlier blocks' entries
+    // tile starts: the head's entry range base + exclusive scan of the tile totals; the block's
+    // first position in each tile: its tile start + the earlier blocks' entries of the tile
     uint32_t hb, hc;
     const uint32_t *row = a.mat + (size_t)block_slot(a, hb, hc) * T_h;
-    for (uint32_t i = tid; i < T_h; i += kBucketThreads) win[i] = a.start[w0 + i] + row[i];
+    for (uint32_t i = tid; i < T_h; i += kBucketThreads) cur[i] = a.counts[w0 + i];
+    __syncthreads();
+    const uint32_t hbase = bg * 8u * a.per_head;
+    block_scan(cur, nw, per, scan_tmp, [&](uint32_t i, uint32_t ex) {
+      win[i] = hbase + ex + row[i];
+      if (hc == 0) a.start[w0 + i] = hbase + ex;
+      cur[i] = 0u;
+    });
   } else {
     // counts of the window's tiles, then one reservation per touched tile
 #pragma unroll 4
@@ -211,7 +263,6 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
   __syncthreads();
   constexpr int SPT = kRound / kBucketThreads;
   const bool all_in = nw == T_h;   // no tile outside the window: no global-atomic path
-  const uint32_t per = (nw + kBucketThreads - 1) / kBucketThreads;   // tiles per thread in the scans
   for (uint32_t r0 = s0; r0 < s1; r0 += kRound) {
     uint32_t key[SPT], word[SPT];
 #pragma unroll
@@ -237,40 +288,12 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
     __syncthreads();
     // (b) exclusive scan of the counts: cur = the tile's first staging slot; win -= that slot,
     // so that staging slot i of tile t goes to win[t] + i
-    {
-      const uint32_t b0 = (uint32_t)tid * per;
-      uint32_t sum = 0;
-      for (uint32_t i = 0; i < per; ++i)
-        if (b0 + i < nw) sum += cur[b0 + i];
-      uint32_t inc = sum;
-#pragma unroll
-      for (int o = 1; o < kWave; o <<= 1) {
-        const uint32_t y = __shfl_up(inc, o, kWave);
-        if (lane >= o) inc += y;
-      }
-      if (lane == kWave - 1) scan_tmp[wv] = inc;
-      __syncthreads();
-      if (tid == 0) {
-        uint32_t run = 0;
-        for (int w = 0; w < kBucketThreads / kWave; ++w) {
-          const uint32_t t = scan_tmp[w];
-          scan_tmp[w] = run;
-          run += t;
-        }
-        scan_tmp[kBucketThreads / kWave] = run;
-      }
-      __syncthreads();
-      uint32_t run = scan_tmp[wv] + inc - sum;
-      for (uint32_t i = 0; i < per; ++i)
-        if (b0 + i < nw) {
-          const uint32_t c = cur[b0 + i];
-          cur[b0 + i] = run;
-          win[b0 + i] -= run;
-          run += c;
-        }
-    }
+    const uint32_t staged = min(block_scan(cur, nw, per, scan_tmp, [&](uint32_t i, uint32_t ex) {
+                                  cur[i] = ex;
+                                  win[i] -= ex;
+                                }),
+                                (uint32_t)kStage);
     __syncthreads();
-    const uint32_t staged = min(scan_tmp[kBucketThreads / kWave], (uint32_t)kStage);
     // (c) placement: staging slot by tile (LDS), or the final position past the capacity
     const auto place_round = [&](auto all_in) {
 #pragma unroll
@@ -306,41 +329,57 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
   }
 }
 
-// One block per head: per tile, the exclusive prefix of its counts over the head's blocks (in
-// place, matrix mode) and its total (counts); tile_start = head base + exclusive scan of the
-// totals over the head's tiles; cursor = tile_start.
-__global__ __launch_bounds__(1024) void tile_headscan_kernel(const BucketArgs a, uint32_t *start) {
-  __shared__ uint32_t tmp[16];
+constexpr int kScanThreads = 256;
+constexpr int kScanTiles = 64;        // tiles per head-scan block (matrix mode)
+
+// Matrix mode: block (head, j) takes tiles [64 j, 64 j + 64) of the head, a wave per quarter of
+// the head's block rows: per tile, the exclusive prefix of its counts over the blocks (in place)
+// and its total (counts).  The tile starts are the scatter's (each of its blocks scans the
+// totals of its head).
+// Atomic mode: block (head, 0) alone: tile_start = head base + exclusive scan of the counts over
+// the head's tiles; cursor = tile_start.
+__global__ __launch_bounds__(kScanThreads) void tile_headscan_kernel(const BucketArgs a, uint32_t nblk) {
+  __shared__ uint32_t part[kScanThreads / kWave][kScanTiles];
   const uint32_t T_h = tiles_per_head(a.shapes, a.L, a.TX, a.TY, a.TZ);
-  const bool mat = matrix_mode(a, T_h);
-  const uint32_t bg = blockIdx.x;
-  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
-  if (bg == 0 && threadIdx.x < 8) a.queue[threadIdx.x] = 0u;
-  uint32_t carry = bg * 8u * a.per_head;   // the head's entry range
-  for (uint32_t base = 0; base < T_h; base += 1024) {
-    const uint32_t t = base + threadIdx.x;
-    uint32_t x = 0;
-    if (t < T_h) {
-      if (mat) {
-        uint32_t *col = a.mat + (size_t)bg * a.blocks_per_head * T_h + t;
-        // kScanBatch loads in flight, then their prefix
-        constexpr int kScanBatch = 32;
-        for (uint32_t c0 = 0; c0 < a.blocks_per_head; c0 += kScanBatch) {
-          uint32_t v[kScanBatch];
+  const uint32_t bg = blockIdx.x / nblk, j = blockIdx.x - bg * nblk;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+  if (blockIdx.x == 0 && tid < 8) a.queue[tid] = 0u;
+  const uint32_t hbase = bg * 8u * a.per_head;   // the head's entry range
+  if (matrix_mode(a, T_h)) {
+    static_assert(kScanTiles == kWave && kScanThreads / kWave * 16 >= kBlocksPerHead, "row groups");
+    if (j * kScanTiles >= T_h) return;
+    const uint32_t t = j * kScanTiles + (uint32_t)lane;
+    const bool ok = t < T_h;
+    const uint32_t bph = a.blocks_per_head, R = (bph + 3) / 4;   // R <= 16
+    const uint32_t r0 = (uint32_t)w * R, r1 = min(r0 + R, bph);
+    uint32_t *col = a.mat + (size_t)bg * bph * T_h + t;
+    uint32_t v[16], sum = 0;
 #pragma unroll
-          for (int k = 0; k < kScanBatch; ++k)
-            v[k] = c0 + k < a.blocks_per_head ? col[(size_t)(c0 + k) * T_h] : 0u;
-#pragma unroll
-          for (int k = 0; k < kScanBatch; ++k) {
-            if (c0 + k < a.blocks_per_head) col[(size_t)(c0 + k) * T_h] = x;
-            x += v[k];
-          }
-        }
-        a.counts[bg * T_h + t] = x;
-      } else {
-        x = a.counts[bg * T_h + t];
-      }
+    for (int k = 0; k < 16; ++k) {
+      v[k] = ok && r0 + k < r1 ? col[(size_t)(r0 + k) * T_h] : 0u;
+      sum += v[k];
     }
+    part[w][lane] = sum;
+    __syncthreads();
+    uint32_t x = 0;
+    for (int g = 0; g < w; ++g) x += part[g][lane];
+    if (!ok) return;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if (r0 + k < r1) col[(size_t)(r0 + k) * T_h] = x;
+      x += v[k];
+    }
+    if (w == kScanThreads / kWave - 1) a.counts[bg * T_h + t] = x;
+    // no samples: no scatter block writes the starts
+    if (bph == 0 && w == 0) a.start[bg * T_h + t] = hbase;
+    return;
+  }
+  if (j != 0) return;
+  __shared__ uint32_t tmp[kScanThreads / kWave];
+  uint32_t carry = hbase;
+  for (uint32_t base = 0; base < T_h; base += kScanThreads) {
+    const uint32_t t = base + (uint32_t)tid;
+    const uint32_t x = t < T_h ? a.counts[bg * T_h + t] : 0u;
     uint32_t inc = x;
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) {
@@ -350,14 +389,14 @@ __global__ __launch_bounds__(1024) void tile_headscan_kernel(const BucketArgs a,
     if (lane == kWave - 1) tmp[w] = inc;
     __syncthreads();
     uint32_t wofs = 0, all = 0;
-    for (int ww = 0; ww < 16; ++ww) {
+    for (int ww = 0; ww < kScanThreads / kWave; ++ww) {
       if (ww < w) wofs += tmp[ww];
       all += tmp[ww];
     }
     __syncthreads();
     if (t < T_h) {
       const uint32_t v = carry + wofs + inc - x;
-      start[bg * T_h + t] = v;
+      a.start[bg * T_h + t] = v;
       a.cursor[bg * T_h + t] = v;
     }
     carry += all;
@@ -392,7 +431,8 @@ hipError_t launch_tile_bucketing(const uint32_t *keys, const uint32_t *words, ui
   const unsigned blocks = (unsigned)BG * a.blocks_per_head;
   if (!counts_cleared) hipLaunchKernelGGL(tile_clear_kernel, dim3(64), dim3(1024), 0, st, a);
   if (blocks > 0) hipLaunchKernelGGL(tile_count_kernel, dim3(blocks), dim3(kBucketThreads), a.wcap * 4, st, a);
-  if (BG > 0) hipLaunchKernelGGL(tile_headscan_kernel, dim3((unsigned)BG), dim3(1024), 0, st, a, start);
+  const uint32_t nblk = (a.wcap + kScanTiles - 1) / kScanTiles;   // matrix mode: T_h <= wcap
+  if (BG > 0) hipLaunchKernelGGL(tile_headscan_kernel, dim3((unsigned)BG * nblk), dim3(kScanThreads), 0, st, a, nblk);
   if (mark) mark(3, st);
   if (blocks > 0) hipLaunchKernelGGL(tile_scatter_kernel, dim3(blocks), dim3(kBucketThreads), tile_scatter_lds_bytes(a.wcap), st, a);
   return hipGetLastError();
