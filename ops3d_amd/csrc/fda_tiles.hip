@@ -205,15 +205,24 @@ __device__ __forceinline__ uint32_t block_scan(const uint32_t *cnt, uint32_t n, 
 // tile, scanned, and placed in LDS grouped by tile; the writes then go out in that order, so
 // consecutive lanes write consecutive positions of a tile's run instead of one scattered word
 // each.  An entry past the staging capacity is written directly at the same position.
-constexpr int kRound = 4096;        // samples per staging round (kRound / kBucketThreads per thread)
-constexpr int kStage = 8192;        // staged entries per round (a round holds 1.5-1.8 per sample
-                                    // on average, at most 8)
-constexpr int kRoundBits = 12;      // kRound == 1 << kRoundBits
+// Rounds of 4096 samples (8192 staged entries) keep two blocks on a CU for windows up to
+// about 6000 tiles; a larger window leaves room for one block only, which then takes rounds of
+// 8192 samples: half the per-round tile scans over the window.
+constexpr int kRoundBitsSmall = 12, kRoundBitsLarge = 13;
 
-size_t tile_scatter_lds_bytes(uint32_t wcap) { return (size_t)kStage * 4 + (size_t)2 * (wcap + 1) * 4; }
+size_t tile_scatter_lds_bytes(int round_bits, uint32_t wcap) {
+  return (size_t)(2u << round_bits) * 4 + (size_t)2 * (wcap + 1) * 4;
+}
 
+int tile_scatter_round_bits(uint32_t wcap) {
+  return tile_scatter_lds_bytes(kRoundBitsSmall, wcap) + 1024 <= 80 * 1024 ? kRoundBitsSmall : kRoundBitsLarge;
+}
+
+template <int kRoundBits>
 __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const BucketArgs a) {
-  static_assert(kRound == (1 << kRoundBits), "round size");
+  constexpr int kRound = 1 << kRoundBits;   // samples per staging round (kRound / kBucketThreads per thread)
+  constexpr int kStage = 2 * kRound;        // staged entries per round (a round holds 1.5-1.8 per
+                                            // sample on average, at most 8)
   extern __shared__ uint32_t lsm[];
   uint32_t *rec = lsm;                    // [kStage] (tile - w0) << kRoundBits | (sample - round start)
   uint32_t *win = rec + kStage;           // [wcap] next free position of the block in each tile
@@ -434,7 +443,15 @@ hipError_t launch_tile_bucketing(const uint32_t *keys, const uint32_t *words, ui
   const uint32_t nblk = (a.wcap + kScanTiles - 1) / kScanTiles;   // matrix mode: T_h <= wcap
   if (BG > 0) hipLaunchKernelGGL(tile_headscan_kernel, dim3((unsigned)BG * nblk), dim3(kScanThreads), 0, st, a, nblk);
   if (mark) mark(3, st);
-  if (blocks > 0) hipLaunchKernelGGL(tile_scatter_kernel, dim3(blocks), dim3(kBucketThreads), tile_scatter_lds_bytes(a.wcap), st, a);
+  if (blocks > 0) {
+    const int rb = tile_scatter_round_bits(a.wcap);
+    if (rb == kRoundBitsSmall)
+      hipLaunchKernelGGL(tile_scatter_kernel<kRoundBitsSmall>, dim3(blocks), dim3(kBucketThreads),
+                         tile_scatter_lds_bytes(rb, a.wcap), st, a);
+    else
+      hipLaunchKernelGGL(tile_scatter_kernel<kRoundBitsLarge>, dim3(blocks), dim3(kBucketThreads),
+                         tile_scatter_lds_bytes(rb, a.wcap), st, a);
+  }
   return hipGetLastError();
 }
 
