@@ -50,8 +50,10 @@ OPS3D_FDA_API const char *ops3d_fda_last_error(void);
 OPS3D_FDA_API int ops3d_fda_supported(int dtype, int channels);
 
 /*
- * Bytes of optional device workspace for ops3d_fda_forward: room for a head-major copy
- * [B,G,S,D] of value (0 when G == 1 or on invalid sizes).
+ * Bytes of optional device workspace for ops3d_fda_forward: room for a head-major copy of value
+ * (0 when G == 1 or on invalid sizes): [B,G] slices of S rows of D elements, or, with 64-byte
+ * rows (D * element size == 64), of 2*S + 10 rows, where levels larger than 16 MB per head are
+ * stored as aligned x-neighbour row pairs (each pair load then reads one 128-byte line).
  */
 OPS3D_FDA_API size_t ops3d_fda_forward_workspace_bytes(int dtype, int batch, int spatial_size,
                                                        int num_heads, int channels);
@@ -113,9 +115,9 @@ OPS3D_FDA_API int ops3d_fda_backward(const void *value, const int64_t *spatial_s
 
 /*
  * Backward with the head-major copy of value the forward already made.  Same as
- * ops3d_fda_backward, plus value_head_major: NULL, or the [B,G,S,D] copy of value that
- * ops3d_fda_forward left in its workspace (its first B*S*G*D elements) for the same value, so
- * the backward does not make it again.  Ignored when G == 1.  No counterpart in the reference
+ * ops3d_fda_backward, plus value_head_major: NULL, or the head-major copy of value that
+ * ops3d_fda_forward left in its workspace, for the same value, spatial_shapes and
+ * level_start_index, so the backward does not make it again.  Ignored when G == 1.  No counterpart in the reference
  * (its backward re-reads value, flash_deform_attn_cuda.cu:93-179); for autograd functions that
  * keep the forward workspace until the backward.
  */

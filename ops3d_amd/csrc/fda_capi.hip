@@ -176,7 +176,9 @@ hipError_t launch(int dtype, int which, const Geometry &g, hipStream_t st) {
 //   split scratch  : when fewer than kSplitTiles tiles can exist (at least ceil(S / tile voxels)
 //                    per head), kSplitSlots fp32 partial tiles [tile voxels][D] for the tile
 //                    kernel's split tiles; else nothing
-//   head-major copies of value and grad_output (G > 1)
+//   head-major copies of value (head slices of at most head_copy_rows_max(S) rows: large
+//   levels paired)
+//   and of grad_output (G > 1)
 constexpr uint64_t kSplitTiles = 2048, kSplitSlots = 4096;
 struct BwdLayout {
   uint64_t n, ntiles_bound;
@@ -214,7 +216,7 @@ int bwd_layout(int B, int S, int G, int D, int e, int lpu, int L, int Q, int K, 
   }
   ly.tcap = (uint32_t)(S / 16 + 64);
   ly.off_mat = o; o += align256(tile_matrix_words((uint32_t)(B * G), ly.tcap) * 4);
-  ly.off_vhm = o; o += G > 1 ? align256((size_t)B * S * G * D * e) : 0;
+  ly.off_vhm = o; o += G > 1 ? align256((size_t)B * G * (size_t)head_copy_rows_max(S, D * e) * D * e) : 0;
   ly.off_ghm = o; o += G > 1 ? align256((size_t)B * Q * G * D * e) : 0;
   ly.total = o;
   return OPS3D_FDA_OK;
@@ -245,38 +247,85 @@ int device_cus() {
   return n;
 }
 
-// [B, N, G, R words] -> [B, G, N, R words]: the head-major copy of value / grad_output, so that
-// one head's rows are contiguous (one head per XCD then keeps its slice in that XCD's L2).
-// One 16-byte chunk per thread and step when R is a multiple of 4 words, else one word.
+// [B, N, G, R words] -> [B, G, N, R words]: the head-major copy of value, so that one head's
+// rows are contiguous (one head per XCD then keeps its slice in that XCD's L2).  Head slices
+// are copy_head_rows rows apart; with 64-byte rows, levels larger than
+// kPairedLevelBytes per head are stored as x-pair lines (copy_level): each of their rows is
+// written twice.  One 16-byte chunk per thread and step when R is a multiple of 4 words, else
+// one word.
 __global__ __launch_bounds__(256) void head_major_kernel(const uint32_t *src, uint32_t *dst, int64_t B,
-                                                         int64_t N, int G, int R) {
+                                                         int64_t N, int G, int R, const int64_t *shapes,
+                                                         const int64_t *lsi, int L, int pair_levels) {
+  __shared__ int64_t lv_src[5], lv_dst[5];
+  __shared__ bool lv_pair[5];
+  __shared__ CopyLevel lv[5];
+  __shared__ int64_t head_rows;
   const bool vec = (R & 3) == 0;
   const int Rc = vec ? R / 4 : R;                  // chunks per row
   const int64_t total = B * N * G * Rc;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  if (!pair_levels) {   // no level is paired: heads N rows apart
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+      const int64_t c = i % Rc;
+      const int64_t row = i / Rc;                    // (b, n, g)
+      const int64_t g = row % G;
+      const int64_t bn = row / G;
+      const int64_t n = bn % N, b = bn / N;
+      const int64_t o = ((b * G + g) * N + n) * Rc + c;
+      if (vec)
+        reinterpret_cast<u32x4 *>(dst)[o] = reinterpret_cast<const u32x4 *>(src)[i];
+      else
+        dst[o] = src[i];
+    }
+    return;
+  }
+  if (threadIdx.x == 0) {
+    head_rows = copy_levels(shapes, lsi, L, N, R * 4, lv);
+    for (int l = 0; l < L; ++l) {
+      lv_src[l] = lsi[l];
+      lv_dst[l] = lv[l].start;
+      lv_pair[l] = lv[l].paired;
+    }
+  }
+  __syncthreads();
+  const int64_t HS = head_rows;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
     const int64_t c = i % Rc;
     const int64_t row = i / Rc;                      // (b, n, g)
     const int64_t g = row % G;
     const int64_t bn = row / G;
     const int64_t n = bn % N, b = bn / N;
-    const int64_t o = ((b * G + g) * N + n) * Rc + c;
-    if (vec)
-      reinterpret_cast<u32x4 *>(dst)[o] = reinterpret_cast<const u32x4 *>(src)[i];
-    else
-      dst[o] = src[i];
+    const int64_t head = (b * G + g) * HS;
+    int l = L - 1;
+    while (l > 0 && n < lv_src[l]) --l;              // pairing implies the standard level layout
+    const int64_t v = n - lv_src[l];
+    int64_t r0 = lv_dst[l] + v, r1 = -1;             // destination rows (r1: second copy)
+    if (lv_pair[l]) {
+      r0 = lv_dst[l] + 2 * v + 2;                    // first row of line v
+      r1 = lv_dst[l] + 2 * v + 1;                    // second row of line v - 1
+    }
+    if (vec) {
+      const u32x4 x = reinterpret_cast<const u32x4 *>(src)[i];
+      reinterpret_cast<u32x4 *>(dst)[(head + r0) * Rc + c] = x;
+      if (r1 >= 0) reinterpret_cast<u32x4 *>(dst)[(head + r1) * Rc + c] = x;
+    } else {
+      const uint32_t x = src[i];
+      dst[(head + r0) * Rc + c] = x;
+      if (r1 >= 0) dst[(head + r1) * Rc + c] = x;
+    }
   }
 }
 
 hipError_t launch_head_major(const void *src, void *dst, int64_t B, int64_t N, int G, int D, int esize,
-                             hipStream_t st) {
+                             const int64_t *shapes, const int64_t *lsi, int L, hipStream_t st) {
   const int R = D * esize / 4;
   const int64_t chunks = B * N * G * ((R & 3) == 0 ? R / 4 : R);
   int64_t blocks = (chunks + 255) / 256;
   if (blocks > 16384) blocks = 16384;
   if (blocks < 1) return hipSuccess;
   hipLaunchKernelGGL(head_major_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
-                     static_cast<const uint32_t *>(src), static_cast<uint32_t *>(dst), B, N, G, R);
+                     static_cast<const uint32_t *>(src), static_cast<uint32_t *>(dst), B, N, G, R, shapes, lsi, L,
+                     pairing_possible(N, R * 4) ? 1 : 0);
   return hipGetLastError();
 }
 
@@ -297,7 +346,7 @@ size_t ops3d_fda_forward_workspace_bytes(int dtype, int batch, int spatial_size,
                                          int channels) {
   const int e = elem_size(dtype);
   if (e == 0 || batch <= 0 || spatial_size <= 0 || num_heads <= 1 || channels <= 0) return 0;
-  return align256((size_t)batch * spatial_size * num_heads * channels * e);
+  return align256((size_t)batch * num_heads * (size_t)head_copy_rows_max(spatial_size, channels * e) * channels * e);
 }
 
 int ops3d_fda_forward(const void *value, const int64_t *spatial_shapes,
@@ -322,10 +371,11 @@ int ops3d_fda_forward(const void *value, const int64_t *spatial_shapes,
   const size_t need = ops3d_fda_forward_workspace_bytes(dtype, batch, spatial_size, num_heads, channels);
   if (need > 0 && workspace && workspace_bytes >= need) {
     hipError_t e = launch_head_major(value, workspace, batch, spatial_size, num_heads, channels,
-                                     elem_size(dtype), st);
+                                     elem_size(dtype), spatial_shapes, level_start_index, num_levels, st);
     if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "head-major copy failed: %s", hipGetErrorString(e));
     geo.a.value = workspace;
     geo.a.vhm = 1;
+    geo.a.pair_levels = pairing_possible(spatial_size, channels * elem_size(dtype)) ? 1 : 0;
   }
   geo.a.shapes = spatial_shapes;
   geo.a.lsi = level_start_index;
@@ -424,11 +474,13 @@ static int backward_impl(const void *value, const void *value_head_major, const 
     if (value_head_major) {
       a.value = value_head_major;
     } else {
-      e = launch_head_major(value, ws + ly.off_vhm, batch, spatial_size, num_heads, channels, elem_size(dtype), st);
+      e = launch_head_major(value, ws + ly.off_vhm, batch, spatial_size, num_heads, channels, elem_size(dtype),
+                            spatial_shapes, level_start_index, num_levels, st);
       if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "head-major copy failed: %s", hipGetErrorString(e));
       a.value = ws + ly.off_vhm;
     }
     a.vhm = 1;
+    a.pair_levels = pairing_possible(spatial_size, channels * elem_size(dtype)) ? 1 : 0;
     a.gout_hm = ws + ly.off_ghm;
   }
   prof_mark(1, st);

@@ -61,6 +61,8 @@ struct Args {
   int tile_affinity;          // tiles of head g run on XCD g % 8 (G % 8 == 0)
   int accumulate;             // add into an fp32 grad_value instead of overwriting
   int vhm;                    // value is head-major [B,G,S,D] (a transposed copy)
+  int pair_levels;            // head-major copy in which large levels may be paired (copy_level);
+                              // 0: every level at its level_start_index, heads S rows apart
   void *gout_hm;              // head-major copy [B,G,Q,D] of grad_out (G > 1): written by the
                               // query kernel, read by the tile kernel
   double inv_lk;              // 1.0 / (L*K), for sample -> unit
@@ -352,6 +354,108 @@ struct Sample {
 // query (host and device must agree: it sets the units per block).
 __host__ __device__ constexpr bool fwd_pairs(int cpl, int lpu, int esize) {
   return lpu == 4 && cpl * esize == 16;
+}
+
+// Paired levels.  In the head-major copy of value a level whose per-head slice is larger than
+// kPairedLevelBytes, with 64-byte rows (the x-pair kernels), is stored as x-pair lines: line u
+// (u = -1 .. n-1 for the level's n voxels) holds rows u and u+1 in 128 aligned bytes, at rows
+// 2(u+1) and 2(u+1)+1 of the level (line -1's first row and line n-1's second row are never
+// read).  Each voxel is stored twice, so a corner-pair load touches exactly one 128-byte line
+// instead of 1.5 on average: for slices far beyond the 4 MB L2 the gathers are bound by the
+// lines fetched from HBM.  Smaller levels keep one row per voxel (doubling them would push
+// them out of L2).
+constexpr int64_t kPairedLevelBytes = (int64_t)16 << 20;
+
+__host__ __device__ inline bool level_paired(int64_t voxels, int row_bytes) {
+  return row_bytes == 64 && voxels * 64 > kPairedLevelBytes;
+}
+
+// Rows of a level in the head-major copy.
+__host__ __device__ inline int64_t level_copy_rows(int64_t voxels, int row_bytes) {
+  return level_paired(voxels, row_bytes) ? 2 * voxels + 2 : voxels;
+}
+
+// Whether any level of a volume of S voxels with rows of row_bytes can be paired (host and
+// device: without it every level keeps its level_start_index and no level table is read).
+__host__ __device__ inline bool pairing_possible(int64_t S, int row_bytes) {
+  return level_paired(S, row_bytes);
+}
+
+// Rows of one head's slice of the head-major copy, at most: room for every level paired (the
+// workspace size).
+__host__ __device__ inline int64_t head_copy_rows_max(int64_t S, int row_bytes) {
+  return row_bytes == 64 ? 2 * S + 2 * 5 : S;
+}
+
+// Level l in a head's slice of the head-major copy: first row and layout.  Levels are paired
+// only when level_start_index is the exclusive sum of the level sizes and the levels cover the
+// S rows exactly (the layout every caller builds); otherwise each level stays at its
+// level_start_index, as in value.
+struct CopyLevel {
+  int64_t start;
+  bool paired;
+};
+
+__device__ inline CopyLevel copy_level(const int64_t *shapes, const int64_t *lsi, int L, int64_t S, int l,
+                                       int row_bytes) {
+  if (row_bytes != 64) return {lsi[l], false};
+  int64_t plain = 0, start = 0;
+  bool standard = true;
+  for (int i = 0; i < L; ++i) {
+    const int64_t n = shapes[3 * i] * shapes[3 * i + 1] * shapes[3 * i + 2];
+    standard = standard && lsi[i] == plain;
+    if (i < l) start += level_copy_rows(n, row_bytes);
+    plain += n;
+  }
+  if (!standard || plain != S) return {lsi[l], false};
+  return {start, level_paired(shapes[3 * l] * shapes[3 * l + 1] * shapes[3 * l + 2], row_bytes)};
+}
+
+// A block-uniform 64-bit value read from LDS, moved to scalar registers.
+__device__ __forceinline__ int64_t uniform_i64(int64_t v) {
+  const uint64_t u = (uint64_t)v;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)u);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(u >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// copy_level of every level into out[0, L); returns copy_head_rows.
+__device__ inline int64_t copy_levels(const int64_t *shapes, const int64_t *lsi, int L, int64_t S, int row_bytes,
+                                      CopyLevel *out) {
+  int64_t plain = 0;
+  bool standard = row_bytes == 64;
+  for (int i = 0; i < L; ++i) {
+    standard = standard && lsi[i] == plain;
+    plain += shapes[3 * i] * shapes[3 * i + 1] * shapes[3 * i + 2];
+  }
+  standard = standard && plain == S;
+  int64_t start = 0;
+  for (int i = 0; i < L; ++i) {
+    const int64_t n = shapes[3 * i] * shapes[3 * i + 1] * shapes[3 * i + 2];
+    out[i] = standard ? CopyLevel{start, level_paired(n, row_bytes)} : CopyLevel{lsi[i], false};
+    start += level_copy_rows(n, row_bytes);
+  }
+  return standard ? start : S;
+}
+
+// Rows of one head's slice of the head-major copy (the distance between heads): S, plus the
+// extra rows of the paired levels.
+__device__ inline int64_t copy_head_rows(const int64_t *shapes, const int64_t *lsi, int L, int64_t S,
+                                         int row_bytes) {
+  if (row_bytes != 64) return S;
+  int64_t extra = 0;
+  for (int l = 0; l < L; ++l) {
+    const CopyLevel cl = copy_level(shapes, lsi, L, S, l, row_bytes);
+    if (cl.paired) extra += shapes[3 * l] * shapes[3 * l + 1] * shapes[3 * l + 2] + 2;
+  }
+  return S + extra;
+}
+
+// Element offset, in a paired level, of the row a pair lane loads: `o` is the corner's element
+// offset in the plain layout (row * RST, or OOB_ELEM), dxl the lane's x-row of the pair.  Row r
+// is read through line r - dxl: copy row 2(r - dxl + 1) + dxl.
+__device__ __forceinline__ uint32_t paired_offset(uint32_t o, int dxl, int RST) {
+  return o == OOB_ELEM ? OOB_ELEM : 2u * o + (uint32_t)((2 - dxl) * RST);
 }
 
 // Compile-time loop: f(IntConst<0>{}), ..., f(IntConst<N-1>{}).

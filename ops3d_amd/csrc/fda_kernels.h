@@ -201,8 +201,8 @@ __global__ __launch_bounds__(kBlock) void fda_forward_kernel(const Args a) {
 // two 64-byte loads when x0 is even.  Gathers of random rows cost per distinct 128-byte line,
 // not per byte, so this halves the gather work per sample.  Each half accumulates its own x-row
 // over all samples; the halves are summed once at the end.
-template <typename T, int CPL>
-__global__ __launch_bounds__(kBlock) void fda_forward_pair_kernel(const Args a) {
+template <typename T, int CPL, bool kPairs>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8))) void fda_forward_pair_kernel(const Args a) {
   extern __shared__ float lds[];
   constexpr int LPU = 4, UL = 2 * LPU;
   constexpr int UPW = kWave / UL, UPB = kWavesPerBlock * UPW;
@@ -231,14 +231,17 @@ __global__ __launch_bounds__(kBlock) void fda_forward_pair_kernel(const Args a) 
 
   const int RST = a.vhm ? a.D : a.G * a.D;
   const uint32_t lane_elem = (uint32_t)((a.vhm ? 0 : g * a.D) + j * CPL);
+  constexpr int kRowBytes = CPL * 4 * (int)sizeof(T);   // 64
   const T *vb = static_cast<const T *>(a.value) +
-                (a.vhm ? ((int64_t)b * a.G + g) * a.S * a.D : (int64_t)b * a.S * a.G * a.D);
+                (a.vhm ? ((int64_t)b * a.G + g) * (kPairs ? copy_head_rows(a.shapes, a.lsi, L, a.S, kRowBytes) : a.S) * a.D
+                       : (int64_t)b * a.S * a.G * a.D);
   constexpr int NW = CPL * (int)sizeof(T) / 4, EPW = Elem<T>::kPerWord;
   for (int l = 0; l < L; ++l) {
     const int Dl = (int)a.shapes[3 * l], Hl = (int)a.shapes[3 * l + 1], Wl = (int)a.shapes[3 * l + 2];
-    const int64_t st = a.lsi[l];
-    const uint32_t nbytes = (uint32_t)((int64_t)Dl * Hl * Wl * RST * (int64_t)sizeof(T));
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb + st * RST, nbytes);
+    const CopyLevel cl = kPairs ? copy_level(a.shapes, a.lsi, L, a.S, l, kRowBytes) : CopyLevel{a.lsi[l], false};
+    const int64_t rows = cl.paired ? 2 * (int64_t)Dl * Hl * Wl + 2 : (int64_t)Dl * Hl * Wl;
+    const uint32_t nbytes = (uint32_t)(rows * RST * (int64_t)sizeof(T));
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb + cl.start * RST, nbytes);
     // 4 samples per step: lane (ju & 3) of each quad sets up sample k0 + (ju & 3) for its own
     // x-row (4 corner offsets and weights); its quad receives them by DPP broadcast
     for (int k0 = 0; k0 < K; k0 += 4) {
@@ -254,6 +257,7 @@ __global__ __launch_bounds__(kBlock) void fda_forward_pair_kernel(const Args a) 
 #pragma unroll
       for (int c4 = 0; c4 < 4; ++c4) {   // c4 = (dz, dy); this lane's corner c = 2*c4 + dxl
         off4[c4] = live ? (dxl ? ms.off[2 * c4 + 1] : ms.off[2 * c4]) : OOB_ELEM;
+        if (cl.paired) off4[c4] = paired_offset(off4[c4], dxl, RST);
         w4[c4] = ((wxd * ms.wy[c4 & 1]) * ms.wz[c4 >> 1]) * at_s;
       }
       static_for<4>([&](auto uc) {
@@ -295,7 +299,7 @@ __global__ __launch_bounds__(kBlock) void fda_forward_pair_kernel(const Args a) 
 // set-ups are made once per quad (lane k of a quad sets up sample k0+k) and broadcast by DPP;
 // the lane that made a set-up also records that sample's stash and base corner.  The partials
 // of grad_loc / grad_attn of a lane's x-row are summed over the unit's 8 lanes.
-template <typename T, int CPL>
+template <typename T, int CPL, bool kPairs>
 __global__ __launch_bounds__(kBlock) OPS3D_FDA_QUERY_ATTR void fda_bwd_query_pair_kernel(const Args a) {
   extern __shared__ float lds[];
   constexpr int UL = 8;
@@ -320,7 +324,10 @@ __global__ __launch_bounds__(kBlock) OPS3D_FDA_QUERY_ATTR void fda_bwd_query_pai
   const int64_t unit = ((int64_t)b * a.Q + (live ? q : 0)) * a.G + g;
   __shared__ LevelTiles lvt[5];
   __shared__ uint32_t lvbase[5];
+  __shared__ CopyLevel lvcopy[5];   // each level's place in the value rows read (copy_level)
+  __shared__ int64_t head_rows;      // rows between heads of the head-major copy
   if (threadIdx.x == 0) {
+    if (kPairs) head_rows = copy_levels(a.shapes, a.lsi, L, a.S, CPL * 4 * (int)sizeof(T), lvcopy);
     uint32_t t = (uint32_t)(b * a.G + g) * tiles_per_head(a.shapes, L, a.TX, a.TY, a.TZ);
     for (int l = 0; l < L; ++l) {
       lvt[l] = level_tiles(a.shapes, l, a.TX, a.TY, a.TZ);
@@ -353,12 +360,15 @@ __global__ __launch_bounds__(kBlock) OPS3D_FDA_QUERY_ATTR void fda_bwd_query_pai
   const int RST = a.vhm ? a.D : a.G * a.D;
   const uint32_t lane_elem = (uint32_t)((a.vhm ? 0 : g * a.D) + j * CPL);
   const T *vb = static_cast<const T *>(a.value) +
-                (a.vhm ? ((int64_t)b * a.G + g) * a.S * a.D : (int64_t)b * a.S * a.G * a.D);
+                (a.vhm ? ((int64_t)b * a.G + g) * (kPairs ? uniform_i64(head_rows) : (int64_t)a.S) * a.D
+                       : (int64_t)b * a.S * a.G * a.D);
   for (int l = 0; l < L; ++l) {
     const int Dl = (int)a.shapes[3 * l], Hl = (int)a.shapes[3 * l + 1], Wl = (int)a.shapes[3 * l + 2];
-    const int64_t st = a.lsi[l];
-    const int64_t nel = (int64_t)Dl * Hl * Wl * RST;
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb + st * RST, (uint32_t)(nel * (int64_t)sizeof(T)));
+    const CopyLevel cl = kPairs ? CopyLevel{uniform_i64(lvcopy[l].start),
+                                            __builtin_amdgcn_readfirstlane((int)lvcopy[l].paired) != 0}
+                                : CopyLevel{a.lsi[l], false};
+    const int64_t rows = cl.paired ? 2 * (int64_t)Dl * Hl * Wl + 2 : (int64_t)Dl * Hl * Wl;
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb + cl.start * RST, (uint32_t)(rows * RST * (int64_t)sizeof(T)));
     for (int k0 = 0; k0 < K; k0 += 4) {
       // lane k of each quad sets up sample k0 + k (both quads: each needs its own x-row)
       const int kq = k0 + (ju & 3);
@@ -374,8 +384,10 @@ __global__ __launch_bounds__(kBlock) OPS3D_FDA_QUERY_ATTR void fda_bwd_query_pai
       }
       uint32_t off4[4];
 #pragma unroll
-      for (int c4 = 0; c4 < 4; ++c4)   // c4 = (dz, dy); a select, not an index, keeps ms in registers
+      for (int c4 = 0; c4 < 4; ++c4) {   // c4 = (dz, dy); a select, not an index, keeps ms in registers
         off4[c4] = live ? (dxl ? ms.off[2 * c4 + 1] : ms.off[2 * c4]) : OOB_ELEM;
+        if (cl.paired) off4[c4] = paired_offset(off4[c4], dxl, RST);
+      }
       const float wv[6] = {ms.wx[0], ms.wx[1], ms.wy[0], ms.wy[1], ms.wz[0], ms.wz[1]};
       // all four set-ups are computed (past K they repeat sample K-1), so U and W stay in
       // registers; only the write-back below skips them
@@ -1184,14 +1196,22 @@ __global__ __launch_bounds__(tile_threads(LPU)) void fda_bwd_split_combine_kerne
 template <typename T, int CPL, int LPU>
 hipError_t launch_one(int which, const Args &a, unsigned grid, size_t lds, hipStream_t st) {
   if (which == 0) {
-    if constexpr (fwd_pairs(CPL, LPU, (int)sizeof(T)))
-      hipLaunchKernelGGL((fda_forward_pair_kernel<T, CPL>), dim3(grid), dim3(kBlock), lds, st, a);
+    if constexpr (fwd_pairs(CPL, LPU, (int)sizeof(T))) {
+      if (a.pair_levels)
+        hipLaunchKernelGGL((fda_forward_pair_kernel<T, CPL, true>), dim3(grid), dim3(kBlock), lds, st, a);
+      else
+        hipLaunchKernelGGL((fda_forward_pair_kernel<T, CPL, false>), dim3(grid), dim3(kBlock), lds, st, a);
+    }
     else
       hipLaunchKernelGGL((fda_forward_kernel<T, CPL, LPU>), dim3(grid), dim3(kBlock), lds, st, a);
   }
   else if (which == 1) {
-    if constexpr (fwd_pairs(CPL, LPU, (int)sizeof(T)))
-      hipLaunchKernelGGL((fda_bwd_query_pair_kernel<T, CPL>), dim3(grid), dim3(kBlock), lds, st, a);
+    if constexpr (fwd_pairs(CPL, LPU, (int)sizeof(T))) {
+      if (a.pair_levels)
+        hipLaunchKernelGGL((fda_bwd_query_pair_kernel<T, CPL, true>), dim3(grid), dim3(kBlock), lds, st, a);
+      else
+        hipLaunchKernelGGL((fda_bwd_query_pair_kernel<T, CPL, false>), dim3(grid), dim3(kBlock), lds, st, a);
+    }
     else
       hipLaunchKernelGGL((fda_bwd_query_kernel<T, CPL, LPU>), dim3(grid), dim3(kBlock), lds, st, a);
   }

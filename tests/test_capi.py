@@ -51,7 +51,11 @@ def test_abi_version_and_support_table(lib):
 
 
 def test_forward_workspace_bytes(lib):
-    assert lib.ops3d_fda_forward_workspace_bytes(2, 1, 73728, 8, 32) == 73728 * 8 * 32 * 2
+    # 64-byte rows: head slices of 2*S + 10 rows (room for levels stored as x-pair lines)
+    assert lib.ops3d_fda_forward_workspace_bytes(2, 1, 73728, 8, 32) == 8 * (2 * 73728 + 10) * 32 * 2
+    # other row sizes: S rows
+    assert lib.ops3d_fda_forward_workspace_bytes(2, 1, 73728, 8, 64) == 73728 * 8 * 64 * 2
+    assert lib.ops3d_fda_forward_workspace_bytes(0, 1, 73728, 8, 32) == 73728 * 8 * 32 * 4
     assert lib.ops3d_fda_forward_workspace_bytes(2, 1, 73728, 1, 32) == 0  # G == 1: already head-major
     assert lib.ops3d_fda_forward_workspace_bytes(7, 1, 73728, 8, 32) == 0
 
@@ -71,7 +75,7 @@ def test_workspace_bytes(lib):
         n = B * Q * G * L * K
         return (2 * al(4 * n) + al(16 * n) + al(32 * n) + 3 * al(4 * (B * G * S + 1)) + 256
                 + al(split_slots * 128 * D * 4)
-                + al(4 * B * G * 64 * (S // 16 + 64)) + al(B * S * G * D * 2) + al(B * Q * G * D * 2))
+                + al(4 * B * G * 64 * (S // 16 + 64)) + al(B * G * (2 * S + 10) * D * 2) + al(B * Q * G * D * 2))
     assert lib.ops3d_fda_backward_workspace_bytes(2, B, S, G, D, L, Q, K) == want(B, S, G, D, L, Q, K, 0)
     assert lib.ops3d_fda_backward_workspace_bytes(9, B, S, G, D, L, Q, K) == 0
     # c2: at least 8 * 4608/128 = 288 tiles (< 2048): 4096 scratch tiles for split tiles

@@ -97,6 +97,73 @@ def test_c5_query_slice(gpu_device, dt):
         assert_close("c5 grad_sla", gs[:, sel.to(gs.device)], ref[2], rtol, atol)
 
 
+def _paired_inputs(G, D, dt, Q=96, seed=7):
+    """A 32x64x256 level (33.5 MB per head with 64-byte rows: stored as x-pair lines in the
+    head-major copy) and a small one; queries 0..26 sample every corner, edge and face centre
+    of the unit cube in both levels (pixel -0.5 / size-0.5: base corners at -1 and at the last
+    voxel, so the level's first voxel is read through line -1 and the last voxel's x-neighbour
+    is outside)."""
+    from ops3d_amd.workloads import pack
+
+    shapes = [(32, 64, 256), (4, 8, 16)]
+    g = torch.Generator().manual_seed(seed)
+    S = sum(a * b * c for a, b, c in shapes)
+    v = torch.randn(1, S, G, D, generator=g)
+    loc = torch.rand(1, Q, G, 2, 4, 3, generator=g)
+    pts = torch.tensor([(x, y, z) for z in (0.0, 0.5, 1.0) for y in (0.0, 0.5, 1.0) for x in (0.0, 0.5, 1.0)])
+    loc[0, : len(pts)] = pts[:, None, None, None, :]
+    loc[0, len(pts): 2 * len(pts), :, :, 0] = pts[:, None, None, :] * 0.999   # just inside
+    lg = torch.randn(1, Q, G, 2, 4, generator=g)
+    go = torch.randn(1, Q, G * D, generator=g)
+    return {"value": v.to(dt), "sampling_loc_attn": pack(loc, lg).to(dt), "grad_output": go.to(dt),
+            "shapes": shapes, "K": 4}
+
+
+@pytest.mark.parametrize("dt,D,G", [(torch.bfloat16, 32, 8), (torch.float16, 32, 2), (torch.float32, 16, 2)])
+def test_paired_level(gpu_device, dt, D, G):
+    inp = _paired_inputs(G, D, dt)
+    _check(f"paired level {dt} D={D} G={G}", inp, gpu_device, dt)
+
+
+def test_paired_level_backward_own_copy(gpu_device):
+    """_C.flash_deform_attn_backward (no forward workspace): the backward makes the paired copy."""
+    from ops3d_amd import _C
+
+    inp = _paired_inputs(8, 32, torch.bfloat16)
+    log("[case] paired level, _C backward with its own head-major copy")
+    st, lsi = level_meta(inp["shapes"], gpu_device)
+    v = inp["value"].to(gpu_device)
+    s = inp["sampling_loc_attn"].to(gpu_device)
+    go = inp["grad_output"].to(gpu_device)
+    gv, gs = _C.flash_deform_attn_backward(v, st, lsi, s, go, 64, 4, 1, 256)
+    torch.cuda.synchronize()
+    _, rgv, rgs = run_oracle(inp)
+    assert_close("grad_value", gv, rgv, *TOL[torch.bfloat16])
+    assert_close("grad_sla", gs, rgs, *TOL[torch.bfloat16])
+
+
+def test_reordered_levels_large(gpu_device):
+    """value holding the levels in reverse order (level_start_index = [n1, 0]): not the layout
+    whose large levels are paired, so every level stays at its own start; checked against the
+    oracle on the same data in the usual order."""
+    inp = _paired_inputs(8, 32, torch.bfloat16, Q=64)
+    n0 = 32 * 64 * 256
+    log("[case] reordered levels, large volume")
+    v = inp["value"]
+    v_rev = torch.cat([v[:, n0:], v[:, :n0]], dim=1).to(gpu_device).requires_grad_(True)
+    st = torch.tensor(inp["shapes"], dtype=torch.int64, device=gpu_device)
+    lsi = torch.tensor([v.shape[1] - n0, 0], dtype=torch.int64, device=gpu_device)
+    s = inp["sampling_loc_attn"].to(gpu_device).requires_grad_(True)
+    out = FlashDeformAttnFunction.apply(v_rev, st, lsi, s, 64, 4, True)
+    out.backward(inp["grad_output"].to(gpu_device))
+    torch.cuda.synchronize()
+    ref_out, ref_gv, ref_gs = run_oracle(inp)
+    gv = torch.cat([v_rev.grad[:, -n0:], v_rev.grad[:, :-n0]], dim=1)
+    assert_close("output", out.detach(), ref_out, *TOL[torch.bfloat16])
+    assert_close("grad_value", gv, ref_gv, *TOL[torch.bfloat16])
+    assert_close("grad_sla", s.grad, ref_gs, *TOL[torch.bfloat16])
+
+
 # --- reference stress shapes (tests/test_flash_deform_attn_stress.py:47-97) ------------------
 EDGE_SHAPE_CASES = [
     (1, (1, 1, 1), 1), (1, (4, 4, 4), 1), (1, (7, 7, 7), 1), (1, (8, 8, 8), 1),
