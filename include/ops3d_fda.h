@@ -52,7 +52,7 @@ OPS3D_FDA_API int ops3d_fda_supported(int dtype, int channels);
 /*
  * Bytes of optional device workspace for ops3d_fda_forward: room for a head-major copy of value
  * (0 when G == 1 or on invalid sizes): [B,G] slices of S rows of D elements, or, with 64-byte
- * rows (D * element size == 64), of 2*S + 10 rows, where levels larger than 16 MB per head are
+ * rows (D * element size == 64), of 2*S + 10 rows, where levels larger than 8 MiB per head are
  * stored as aligned x-neighbour row pairs (each pair load then reads one 128-byte line).
  */
 OPS3D_FDA_API size_t ops3d_fda_forward_workspace_bytes(int dtype, int batch, int spatial_size,

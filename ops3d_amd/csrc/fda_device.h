@@ -364,7 +364,7 @@ __host__ __device__ constexpr bool fwd_pairs(int cpl, int lpu, int esize) {
 // instead of 1.5 on average: for slices far beyond the 4 MB L2 the gathers are bound by the
 // lines fetched from HBM.  Smaller levels keep one row per voxel (doubling them would push
 // them out of L2).
-constexpr int64_t kPairedLevelBytes = (int64_t)16 << 20;
+constexpr int64_t kPairedLevelBytes = (int64_t)8 << 20;
 
 __host__ __device__ inline bool level_paired(int64_t voxels, int row_bytes) {
   return row_bytes == 64 && voxels * 64 > kPairedLevelBytes;
