@@ -97,7 +97,7 @@ def test_c5_query_slice(gpu_device, dt):
         assert_close("c5 grad_sla", gs[:, sel.to(gs.device)], ref[2], rtol, atol)
 
 
-def _paired_inputs(G, D, dt, Q=96, seed=7):
+def _paired_inputs(G, D, dt, Q=96, seed=7, B=1):
     """A 32x64x256 level (33.5 MB per head with 64-byte rows: stored as x-pair lines in the
     head-major copy) and a small one; queries 0..26 sample every corner, edge and face centre
     of the unit cube in both levels (pixel -0.5 / size-0.5: base corners at -1 and at the last
@@ -108,21 +108,22 @@ def _paired_inputs(G, D, dt, Q=96, seed=7):
     shapes = [(32, 64, 256), (4, 8, 16)]
     g = torch.Generator().manual_seed(seed)
     S = sum(a * b * c for a, b, c in shapes)
-    v = torch.randn(1, S, G, D, generator=g)
-    loc = torch.rand(1, Q, G, 2, 4, 3, generator=g)
+    v = torch.randn(B, S, G, D, generator=g)
+    loc = torch.rand(B, Q, G, 2, 4, 3, generator=g)
     pts = torch.tensor([(x, y, z) for z in (0.0, 0.5, 1.0) for y in (0.0, 0.5, 1.0) for x in (0.0, 0.5, 1.0)])
-    loc[0, : len(pts)] = pts[:, None, None, None, :]
-    loc[0, len(pts): 2 * len(pts), :, :, 0] = pts[:, None, None, :] * 0.999   # just inside
-    lg = torch.randn(1, Q, G, 2, 4, generator=g)
-    go = torch.randn(1, Q, G * D, generator=g)
+    loc[:, : len(pts)] = pts[None, :, None, None, None, :]
+    loc[:, len(pts): 2 * len(pts), :, :, 0] = pts[None, :, None, None, :] * 0.999   # just inside
+    lg = torch.randn(B, Q, G, 2, 4, generator=g)
+    go = torch.randn(B, Q, G * D, generator=g)
     return {"value": v.to(dt), "sampling_loc_attn": pack(loc, lg).to(dt), "grad_output": go.to(dt),
             "shapes": shapes, "K": 4}
 
 
-@pytest.mark.parametrize("dt,D,G", [(torch.bfloat16, 32, 8), (torch.float16, 32, 2), (torch.float32, 16, 2)])
-def test_paired_level(gpu_device, dt, D, G):
-    inp = _paired_inputs(G, D, dt)
-    _check(f"paired level {dt} D={D} G={G}", inp, gpu_device, dt)
+@pytest.mark.parametrize("dt,D,G,B", [(torch.bfloat16, 32, 8, 1), (torch.float16, 32, 2, 1), (torch.float32, 16, 2, 1),
+                                      (torch.bfloat16, 32, 2, 2)])
+def test_paired_level(gpu_device, dt, D, G, B):
+    inp = _paired_inputs(G, D, dt, B=B)
+    _check(f"paired level {dt} D={D} G={G} B={B}", inp, gpu_device, dt)
 
 
 def test_paired_level_backward_own_copy(gpu_device):
