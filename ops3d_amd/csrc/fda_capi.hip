@@ -180,6 +180,7 @@ hipError_t launch(int dtype, int which, const Geometry &g, hipStream_t st) {
 //   levels paired)
 //   and of grad_output (G > 1)
 constexpr uint64_t kSplitTiles = 2048, kSplitSlots = 4096;
+constexpr size_t kDirectGradOutBytes = (size_t)64 << 20;
 struct BwdLayout {
   uint64_t n, ntiles_bound;
   uint32_t tcap, split_slots;
@@ -481,7 +482,12 @@ static int backward_impl(const void *value, const void *value_head_major, const 
     }
     a.vhm = 1;
     a.pair_levels = pairing_possible(spatial_size, channels * elem_size(dtype)) ? 1 : 0;
-    a.gout_hm = ws + ly.off_ghm;
+    // small grad_output (<= kDirectGradOutBytes): the tile kernel reads its rows in place
+    // (one head's rows then share lines with the other heads', but all of it stays in L2
+    // reach); larger: the query kernel writes the head-major copy the tile kernel reads
+    a.gout_hm = (size_t)batch * num_query * num_heads * channels * elem_size(dtype) > kDirectGradOutBytes
+                    ? ws + ly.off_ghm
+                    : nullptr;
   }
   prof_mark(1, st);
   if (work) {

@@ -773,7 +773,10 @@ void fda_bwd_tile_kernel(const Args a) {
     hc = hi - lo;
   };
   // grad_output rows in sample order / (L*K): the head-major copy, or grad_out itself (G == 1)
+  // grad_output rows: the head-major copy (row = sample / (L*K)), or grad_output itself
+  // ([B,Q,G,D]: the row of (b, q, g) is (b*Q + q)*G + g; the same for G == 1)
   const T *go = static_cast<const T *>(a.gout_hm ? a.gout_hm : a.grad_out);
+  const bool go_direct = a.gout_hm == nullptr;
 
 #if OPS3D_FDA_TILE_TIMING
   unsigned long long t_acc[6] = {0, 0, 0, 0, 0, 0}, t_prev = clock64();
@@ -872,6 +875,7 @@ void fda_bwd_tile_kernel(const Args a) {
     uint32_t bgi, t;
     decode(ktile, l, bgi, t);
     head_of(bgi, b, g);
+    const uint32_t row0 = ((uint32_t)b * (uint32_t)G + (uint32_t)g) * (uint32_t)a.Q;   // the head's first sample row
     const LevelTiles lt = lvt[l];
     const int itx = (int)(t % (uint32_t)lt.nt[2]);
     const int ity = (int)((t / (uint32_t)lt.nt[2]) % (uint32_t)lt.nt[1]);
@@ -933,6 +937,7 @@ void fda_bwd_tile_kernel(const Args a) {
         const float fx = st[e].x - xf, fy = st[e].y - yf, fz = st[e].z - zf, at = st[e].w;
         st[e] = make_float4(fx, at * fy, at * (1.f - fy), fz);
         ri[e] = (uint32_t)(((double)en[e] + 0.5) * a.inv_lk);   // sample / (L*K), exact
+        if (go_direct) ri[e] = ((uint32_t)b * (uint32_t)a.Q + (ri[e] - row0)) * (uint32_t)G + (uint32_t)g;
         if (tid + e * NT < n) atomicAdd(&cur_l[lb[e]], 1u);
       }
       // the next chunk's entries, issued after this chunk's stash is used (loads complete in order,
