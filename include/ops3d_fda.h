@@ -86,7 +86,8 @@ OPS3D_FDA_API int ops3d_fda_forward(const void *value, const int64_t *spatial_sh
  * stash, up to 8 four-byte tile entries; per tile (<= B*G*S) a count, a start and a cursor; 8
  * work counters; for small volumes (B*G*ceil(S/128) < 2048) fp32 partial sums of 4096 split
  * tiles; the bucketing matrix (B*G x 64 x (S/16 + 64) words); and head-major copies of value
- * and grad_output (G > 1).  The pointer passed must be 256-byte aligned.
+ * (G > 1) and of grad_output (G > 1 and grad_output larger than 64 MiB; smaller ones are read in
+ * place).  The pointer passed must be 256-byte aligned.
  */
 OPS3D_FDA_API size_t ops3d_fda_backward_workspace_bytes(int dtype, int batch, int spatial_size,
                                                         int num_heads, int channels,

@@ -176,11 +176,18 @@ hipError_t launch(int dtype, int which, const Geometry &g, hipStream_t st) {
 //   split scratch  : when fewer than kSplitTiles tiles can exist (at least ceil(S / tile voxels)
 //                    per head), kSplitSlots fp32 partial tiles [tile voxels][D] for the tile
 //                    kernel's split tiles; else nothing
-//   head-major copies of value (head slices of at most head_copy_rows_max(S) rows: large
-//   levels paired)
-//   and of grad_output (G > 1)
+//   head-major copies of value (G > 1; head slices of at most head_copy_rows_max(S) rows,
+//   large levels paired) and of grad_output (grad_out_copied)
 constexpr uint64_t kSplitTiles = 2048, kSplitSlots = 4096;
 constexpr size_t kDirectGradOutBytes = (size_t)64 << 20;
+
+// Whether the backward makes the head-major copy of grad_output for the tile kernel: for G > 1
+// and more than kDirectGradOutBytes (smaller ones are read in place: the copy would cost the
+// query kernel more than it saves the tile kernel).
+bool grad_out_copied(int B, int Q, int G, int D, int e) {
+  return G > 1 && (size_t)B * Q * G * D * e > kDirectGradOutBytes;
+}
+
 struct BwdLayout {
   uint64_t n, ntiles_bound;
   uint32_t tcap, split_slots;
@@ -218,7 +225,7 @@ int bwd_layout(int B, int S, int G, int D, int e, int lpu, int L, int Q, int K, 
   ly.tcap = (uint32_t)(S / 16 + 64);
   ly.off_mat = o; o += align256(tile_matrix_words((uint32_t)(B * G), ly.tcap) * 4);
   ly.off_vhm = o; o += G > 1 ? align256((size_t)B * G * (size_t)head_copy_rows_max(S, D * e) * D * e) : 0;
-  ly.off_ghm = o; o += G > 1 ? align256((size_t)B * Q * G * D * e) : 0;
+  ly.off_ghm = o; o += grad_out_copied(B, Q, G, D, e) ? align256((size_t)B * Q * G * D * e) : 0;
   ly.total = o;
   return OPS3D_FDA_OK;
 }
@@ -482,12 +489,7 @@ static int backward_impl(const void *value, const void *value_head_major, const 
     }
     a.vhm = 1;
     a.pair_levels = pairing_possible(spatial_size, channels * elem_size(dtype)) ? 1 : 0;
-    // small grad_output (<= kDirectGradOutBytes): the tile kernel reads its rows in place
-    // (one head's rows then share lines with the other heads', but all of it stays in L2
-    // reach); larger: the query kernel writes the head-major copy the tile kernel reads
-    a.gout_hm = (size_t)batch * num_query * num_heads * channels * elem_size(dtype) > kDirectGradOutBytes
-                    ? ws + ly.off_ghm
-                    : nullptr;
+    a.gout_hm = grad_out_copied(batch, num_query, num_heads, channels, elem_size(dtype)) ? ws + ly.off_ghm : nullptr;
   }
   prof_mark(1, st);
   if (work) {

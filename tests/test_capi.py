@@ -75,9 +75,12 @@ def test_workspace_bytes(lib):
         n = B * Q * G * L * K
         return (2 * al(4 * n) + al(16 * n) + al(32 * n) + 3 * al(4 * (B * G * S + 1)) + 256
                 + al(split_slots * 128 * D * 4)
-                + al(4 * B * G * 64 * (S // 16 + 64)) + al(B * G * (2 * S + 10) * D * 2) + al(B * Q * G * D * 2))
+                + al(4 * B * G * 64 * (S // 16 + 64)) + al(B * G * (2 * S + 10) * D * 2) + (al(B * Q * G * D * 2) if B * Q * G * D * 2 > 64 << 20 else 0))
     assert lib.ops3d_fda_backward_workspace_bytes(2, B, S, G, D, L, Q, K) == want(B, S, G, D, L, Q, K, 0)
     assert lib.ops3d_fda_backward_workspace_bytes(9, B, S, G, D, L, Q, K) == 0
+    # c5: grad_output (306 MB) gets its head-major copy
+    c5 = (1, 598016, 8, 32, 3, 598016, 4)
+    assert lib.ops3d_fda_backward_workspace_bytes(2, *c5) == want(*c5, 0)
     # c2: at least 8 * 4608/128 = 288 tiles (< 2048): 4096 scratch tiles for split tiles
     c2 = (1, 4608, 8, 32, 2, 4608, 4)
     assert lib.ops3d_fda_backward_workspace_bytes(2, *c2) == want(*c2, 4096)
