@@ -28,7 +28,8 @@
 #define OPS3D_FDA_TILE_TIMING 0   // 1: per-phase cycle counts of the tile kernel into Args::dbg
 #endif
 #ifndef OPS3D_FDA_TILE_WPE
-#define OPS3D_FDA_TILE_WPE 4    // minimum waves per SIMD the tile kernel is compiled for
+#define OPS3D_FDA_TILE_WPE 0    // minimum waves per SIMD the tile kernel is compiled for; 0: as many
+                                // as its blocks per CU give (tile_wpe)
 #endif
 
 // Tile order of the tile kernel: 1 = a per-XCD work counter after four static tiles when the
@@ -697,8 +698,15 @@ __device__ __forceinline__ uint32_t block_exclusive_scan_tile(uint32_t x, uint32
   return wofs + inc - x;
 }
 
+// Waves per SIMD the tile kernel runs at: its LDS chunk sizing puts three 256-thread blocks, two
+// 512-thread blocks or one 1024-thread block on a CU (3, 4, 4 waves per SIMD); compiling for no
+// more than that leaves the register allocator all the registers those waves can have.
+__host__ __device__ constexpr int tile_wpe(int lpu) {
+  return OPS3D_FDA_TILE_WPE > 0 ? OPS3D_FDA_TILE_WPE : (tile_threads(lpu) == 256 ? 3 : 4);
+}
+
 template <typename T, int CPL, int LPU>
-__global__ __launch_bounds__(tile_threads(LPU)) __attribute__((amdgpu_waves_per_eu(OPS3D_FDA_TILE_WPE)))
+__global__ __launch_bounds__(tile_threads(LPU)) __attribute__((amdgpu_waves_per_eu(tile_wpe(LPU))))
 void fda_bwd_tile_kernel(const Args a) {
   constexpr int NT = tile_threads(LPU);
   extern __shared__ __align__(16) unsigned char tsm[];
