@@ -27,6 +27,9 @@
 #ifndef OPS3D_FDA_TILE_TIMING
 #define OPS3D_FDA_TILE_TIMING 0   // 1: per-phase cycle counts of the tile kernel into Args::dbg
 #endif
+#ifndef OPS3D_FDA_FWD_WPE
+#define OPS3D_FDA_FWD_WPE 8     // minimum waves per SIMD the x-pair forward is compiled for
+#endif
 #ifndef OPS3D_FDA_TILE_WPE
 #define OPS3D_FDA_TILE_WPE 0    // minimum waves per SIMD the tile kernel is compiled for; 0: as many
                                 // as its blocks per CU give (tile_wpe)
@@ -203,7 +206,7 @@ __global__ __launch_bounds__(kBlock) void fda_forward_kernel(const Args a) {
 // not per byte, so this halves the gather work per sample.  Each half accumulates its own x-row
 // over all samples; the halves are summed once at the end.
 template <typename T, int CPL, bool kPairs>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8))) void fda_forward_pair_kernel(const Args a) {
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(OPS3D_FDA_FWD_WPE))) void fda_forward_pair_kernel(const Args a) {
   extern __shared__ float lds[];
   constexpr int LPU = 4, UL = 2 * LPU;
   constexpr int UPW = kWave / UL, UPB = kWavesPerBlock * UPW;
