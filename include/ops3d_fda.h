@@ -40,7 +40,8 @@ extern "C" {
 enum { OPS3D_FDA_F32 = 0, OPS3D_FDA_F16 = 1, OPS3D_FDA_BF16 = 2 };
 enum { OPS3D_FDA_OK = 0, OPS3D_FDA_EINVAL = 1, OPS3D_FDA_ERUNTIME = 2 };
 
-/* ABI version of this header (bumped on any signature change). */
+/* ABI version of this header (bumped on any change of a signature or of a workspace layout a
+ * caller can hand from one call to another). */
 OPS3D_FDA_API int ops3d_fda_abi_version(void);
 
 /* Message of the last failed call on this thread ("" if none). */

@@ -75,7 +75,7 @@ def _ptr(t: torch.Tensor | None) -> int | None:
 class _NativeFDA:
     """Host side of the flash-deform-attn extension, bound to libops3d_fda.so."""
 
-    ABI_VERSION = 3
+    ABI_VERSION = 4
 
     def __init__(self, lib: ctypes.CDLL, path: str):
         self._lib = lib
@@ -258,9 +258,13 @@ class _NativeFDA:
         return dtype in _DTYPE_CODE and bool(self._lib.ops3d_fda_supported(_DTYPE_CODE[dtype], int(channels)))
 
 
+_HANDLES: list = []   # dlopen handles this module opened (closed by reload)
+
+
 def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     """dlopen libops3d_fda.so and declare its C signatures (raises OSError if absent)."""
     lib = ctypes.CDLL(path)
+    _HANDLES.append(lib._handle)
     _declare(lib)
     return lib
 
@@ -276,9 +280,25 @@ _C = _load()
 
 
 def reload() -> None:
-    """Re-resolve ``_C`` (after building the library in this process)."""
+    """Re-resolve ``_C`` (after building the library in this process).  dlopen of a path this
+    process has open returns the open library, so the handles opened so far (including one that
+    failed the ABI check) are closed first and the rebuilt file is loaded afresh."""
     global _C
+    import _ctypes
+
+    _C = None
+    while _HANDLES:
+        try:
+            _ctypes.dlclose(_HANDLES.pop())
+        except OSError:
+            pass
     _C = _load()
+    import sys
+
     from . import flash_deform_attn as _fda
 
     _fda._C = _C
+    for name in ("ops3d_amd", "ops3d"):   # the packages re-export _C
+        mod = sys.modules.get(name)
+        if mod is not None:
+            mod._C = _C

@@ -341,7 +341,7 @@ hipError_t launch_head_major(const void *src, void *dst, int64_t B, int64_t N, i
 
 extern "C" {
 
-int ops3d_fda_abi_version(void) { return 3; }
+int ops3d_fda_abi_version(void) { return 4; }
 
 const char *ops3d_fda_last_error(void) { return g_last_error.c_str(); }
 
