@@ -120,8 +120,9 @@ OPS3D_FDA_API int ops3d_fda_backward(const void *value, const int64_t *spatial_s
  * ops3d_fda_backward, plus value_head_major: NULL, or the head-major copy of value that
  * ops3d_fda_forward left in its workspace, for the same value, spatial_shapes and
  * level_start_index, so the backward does not make it again.  (Neither call copies value when
- * the gathers read fewer rows than a head has, Q*L*K*8 < S: the forward then leaves its workspace
- * unused and the backward ignores value_head_major.)  Ignored when G == 1.  No counterpart in the reference
+ * it is smaller than 8 MiB per batch item or the gathers read fewer rows than a head has,
+ * Q*L*K*8 < S: the forward then leaves its workspace unused and the backward ignores
+ * value_head_major.)  Ignored when G == 1.  No counterpart in the reference
  * (its backward re-reads value, flash_deform_attn_cuda.cu:93-179); for autograd functions that
  * keep the forward workspace until the backward.
  */

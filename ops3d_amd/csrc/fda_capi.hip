@@ -181,11 +181,16 @@ hipError_t launch(int dtype, int which, const Geometry &g, hipStream_t st) {
 constexpr uint64_t kSplitTiles = 2048, kSplitSlots = 4096;
 constexpr size_t kDirectGradOutBytes = (size_t)64 << 20;
 
-// Whether the head-major copy of value pays: the gathers read 8 corner rows per sample, Q*L*K
-// samples per (batch, head); with fewer reads than a head's S rows (cross-attention with few
-// queries) copying the rows costs more than gathering them in place.  The forward and the
-// backward decide alike, so the backward ignores a forward workspace the forward did not fill.
-bool head_major_pays(int S, int Q, int L, int K) { return (uint64_t)Q * L * K * 8 >= (uint64_t)S; }
+// Whether the head-major copy of value pays.  It keeps one head's rows together so that the XCD
+// serving the head caches only them; a value of less than kHeadMajorMinBytes per batch item fits
+// every XCD's 4 MB L2 whole, and with fewer corner reads than a head has rows (8 per sample, Q*L*K
+// samples per batch and head: cross-attention with few queries) copying the rows costs more than
+// gathering them in place.  The forward and the backward decide alike, so the backward ignores a
+// forward workspace the forward did not fill.
+constexpr uint64_t kHeadMajorMinBytes = (uint64_t)8 << 20;
+bool head_major_pays(int S, int G, int D, int e, int Q, int L, int K) {
+  return (uint64_t)S * G * D * e >= kHeadMajorMinBytes && (uint64_t)Q * L * K * 8 >= (uint64_t)S;
+}
 
 // Whether the backward makes the head-major copy of grad_output for the tile kernel: for G > 1
 // and more than kDirectGradOutBytes (smaller ones are read in place: the copy would cost the
@@ -383,7 +388,7 @@ int ops3d_fda_forward(const void *value, const int64_t *spatial_shapes,
   geo.a.value = value;
   prof_mark(6, st);
   const size_t need = ops3d_fda_forward_workspace_bytes(dtype, batch, spatial_size, num_heads, channels);
-  if (need > 0 && workspace && workspace_bytes >= need && head_major_pays(spatial_size, num_query, num_levels, num_point)) {
+  if (need > 0 && workspace && workspace_bytes >= need && head_major_pays(spatial_size, num_heads, channels, elem_size(dtype), num_query, num_levels, num_point)) {
     hipError_t e = launch_head_major(value, workspace, batch, spatial_size, num_heads, channels,
                                      elem_size(dtype), spatial_shapes, level_start_index, num_levels, st);
     if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "head-major copy failed: %s", hipGetErrorString(e));
@@ -482,7 +487,7 @@ static int backward_impl(const void *value, const void *value_head_major, const 
   a.inv_lk = 1.0 / (double)(num_levels * num_point);
   hipError_t e;
   prof_mark(0, st);
-  if (work && num_heads > 1 && head_major_pays(spatial_size, num_query, num_levels, num_point)) {
+  if (work && num_heads > 1 && head_major_pays(spatial_size, num_heads, channels, elem_size(dtype), num_query, num_levels, num_point)) {
     // head-major value (one head's rows contiguous): the caller's copy, or made here
     if (value_head_major) {
       a.value = value_head_major;
