@@ -18,6 +18,9 @@
 // counters, tile_headscan scans them per head (one block) into tile_start and the cursors,
 // and tile_scatter reserves each block's range of a tile with one global atomic on
 // the tile's cursor.  Correct for any size, slower (the atomics of all blocks contend).
+// Heads of at most kFusedHeadSamples samples take one block each, and tile_scatter<.., true>
+// counts, scans and places them in one launch (no count or head-scan launch; its counters are
+// read past L1 in atomic mode, since other heads' blocks may have cached the same lines).
 // Each head owns the entry range [bg * 8 * per_head, ...) (a sample has at most 8 entries), so
 // heads are bucketed independently; a tile's entries are [tile_start, tile_start + count).
 // The order of entries inside a tile (the LDS ranks, and in atomic mode the order of the
@@ -30,6 +33,7 @@ namespace ops3d_fda {
 constexpr int kBucketThreads = 1024;
 constexpr int kWin = 8192;                            // LDS histogram window (tiles of one head)
 constexpr int kBlocksPerHead = 64;
+constexpr uint32_t kFusedHeadSamples = 4096;          // heads this small take one fused block
 
 struct BucketArgs {
   const uint32_t *keys;        // [N] home tile id or kKeyInvalid
@@ -48,6 +52,7 @@ struct BucketArgs {
   uint32_t wcap;               // LDS histogram window in tiles: min(tcap, kWin)
   uint32_t *entries;           // [<= 8N] sample indices
   uint32_t *queue;             // [8] the tile kernel's work counters, cleared here
+  int fused;                   // one block per head: tile_scatter<.., true> counts and scans itself
 };
 
 __device__ __forceinline__ bool matrix_mode(const BucketArgs &a, uint32_t T_h) {
@@ -218,7 +223,7 @@ int tile_scatter_round_bits(uint32_t wcap) {
   return tile_scatter_lds_bytes(kRoundBitsSmall, wcap) + 1024 <= 80 * 1024 ? kRoundBitsSmall : kRoundBitsLarge;
 }
 
-template <int kRoundBits>
+template <int kRoundBits, bool kFused>
 __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const BucketArgs a) {
   constexpr int kRound = 1 << kRoundBits;   // samples per staging round (kRound / kBucketThreads per thread)
   constexpr int kStage = 2 * kRound;        // staged entries per round (a round holds 1.5-1.8 per
@@ -242,14 +247,71 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
   block_range(a, bg, s0, s1);
   const uint32_t w0 = bg * T_h;
   const uint32_t per = (nw + kBucketThreads - 1) / kBucketThreads;   // tiles per thread in the scans
-  if (matrix_mode(a, T_h)) {
+  const uint32_t hbase = bg * 8u * a.per_head;   // the head's entry range
+  if (kFused) {
+    // the head's only block (no count or head-scan launch): count its entries, scan the tile
+    // totals, store counts and starts for the tile kernel
+    if (blockIdx.x == 0 && tid < 8) a.queue[tid] = 0u;
+    const bool mat = matrix_mode(a, T_h);
+    for (uint32_t s = s0 + tid; s < s1; s += kBucketThreads) {
+      const uint32_t key = a.keys[s];
+      if (key == kKeyInvalid) continue;
+      for_each_entry(key, a.words[s], lg, [&](uint32_t id, uint32_t) {
+        if (mat) atomicAdd(&cur[id - w0], 1u);
+        else atomicAdd(&a.counts[id], 1u);   // zeroed by the query kernel
+      });
+    }
+    if (mat) {
+      __syncthreads();
+      block_scan(cur, nw, per, scan_tmp, [&](uint32_t i, uint32_t ex) {
+        a.counts[w0 + i] = cur[i];
+        a.start[w0 + i] = hbase + ex;
+        win[i] = hbase + ex;
+        cur[i] = 0u;
+      });
+    } else {
+      // the counters were added to in L2: wait for this wave's atomics, then read them past L1
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      uint32_t carry = hbase;
+      for (uint32_t t0 = 0; t0 < T_h; t0 += kBucketThreads) {
+        const uint32_t t = t0 + (uint32_t)tid;
+        const uint32_t x = t < T_h ? __hip_atomic_load(&a.counts[w0 + t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+        uint32_t inc = x;
+        const int lane = tid & (kWave - 1), wv = tid / kWave;
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) {
+          const uint32_t y = __shfl_up(inc, o, kWave);
+          if (lane >= o) inc += y;
+        }
+        if (lane == kWave - 1) scan_tmp[wv] = inc;
+        __syncthreads();
+        uint32_t wofs = 0, all = 0;
+        for (int w = 0; w < kBucketThreads / kWave; ++w) {
+          if (w < wv) wofs += scan_tmp[w];
+          all += scan_tmp[w];
+        }
+        __syncthreads();
+        if (t < T_h) {
+          a.start[w0 + t] = carry + wofs + inc - x;
+          a.cursor[w0 + t] = carry + wofs + inc - x;
+        }
+        carry += all;
+      }
+      // the cursors are reserved below with atomics: let the stores land first
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+  }
+  if (kFused && matrix_mode(a, T_h)) {
+    // starts set above
+  } else if (matrix_mode(a, T_h)) {
     // tile starts: the head's entry range base + exclusive scan of the tile totals; the block's
     // first position in each tile: its tile start + the earlier blocks' entries of the tile
     uint32_t hb, hc;
     const uint32_t *row = a.mat + (size_t)block_slot(a, hb, hc) * T_h;
     for (uint32_t i = tid; i < T_h; i += kBucketThreads) cur[i] = a.counts[w0 + i];
     __syncthreads();
-    const uint32_t hbase = bg * 8u * a.per_head;
     block_scan(cur, nw, per, scan_tmp, [&](uint32_t i, uint32_t ex) {
       win[i] = hbase + ex + row[i];
       if (hc == 0) a.start[w0 + i] = hbase + ex;
@@ -435,10 +497,24 @@ hipError_t launch_tile_bucketing(const uint32_t *keys, const uint32_t *words, ui
   a.chunk = (per_head + kBlocksPerHead - 1) / kBlocksPerHead;
   a.chunk = (a.chunk + kBucketThreads - 1) / kBucketThreads * kBucketThreads;
   if (a.chunk == 0) a.chunk = kBucketThreads;
+  // small heads: one block per head that counts, scans and scatters in one launch
+  a.fused = n > 0 && per_head <= kFusedHeadSamples;
+  if (a.fused) a.chunk = (per_head + kBucketThreads - 1) / kBucketThreads * kBucketThreads;
   a.blocks_per_head = (per_head + a.chunk - 1) / a.chunk;
   if (n == 0) a.blocks_per_head = 0;   // every counter is zero: the head scan writes zeros
   const unsigned blocks = (unsigned)BG * a.blocks_per_head;
   if (!counts_cleared) hipLaunchKernelGGL(tile_clear_kernel, dim3(64), dim3(1024), 0, st, a);
+  if (a.fused) {
+    if (mark) mark(3, st);
+    const int rb = tile_scatter_round_bits(a.wcap);
+    if (rb == kRoundBitsSmall)
+      hipLaunchKernelGGL((tile_scatter_kernel<kRoundBitsSmall, true>), dim3(blocks), dim3(kBucketThreads),
+                         tile_scatter_lds_bytes(rb, a.wcap), st, a);
+    else
+      hipLaunchKernelGGL((tile_scatter_kernel<kRoundBitsLarge, true>), dim3(blocks), dim3(kBucketThreads),
+                         tile_scatter_lds_bytes(rb, a.wcap), st, a);
+    return hipGetLastError();
+  }
   if (blocks > 0) hipLaunchKernelGGL(tile_count_kernel, dim3(blocks), dim3(kBucketThreads), a.wcap * 4, st, a);
   const uint32_t nblk = (a.wcap + kScanTiles - 1) / kScanTiles;   // matrix mode: T_h <= wcap
   if (BG > 0) hipLaunchKernelGGL(tile_headscan_kernel, dim3((unsigned)BG * nblk), dim3(kScanThreads), 0, st, a, nblk);
@@ -446,10 +522,10 @@ hipError_t launch_tile_bucketing(const uint32_t *keys, const uint32_t *words, ui
   if (blocks > 0) {
     const int rb = tile_scatter_round_bits(a.wcap);
     if (rb == kRoundBitsSmall)
-      hipLaunchKernelGGL(tile_scatter_kernel<kRoundBitsSmall>, dim3(blocks), dim3(kBucketThreads),
+      hipLaunchKernelGGL((tile_scatter_kernel<kRoundBitsSmall, false>), dim3(blocks), dim3(kBucketThreads),
                          tile_scatter_lds_bytes(rb, a.wcap), st, a);
     else
-      hipLaunchKernelGGL(tile_scatter_kernel<kRoundBitsLarge>, dim3(blocks), dim3(kBucketThreads),
+      hipLaunchKernelGGL((tile_scatter_kernel<kRoundBitsLarge, false>), dim3(blocks), dim3(kBucketThreads),
                          tile_scatter_lds_bytes(rb, a.wcap), st, a);
   }
   return hipGetLastError();

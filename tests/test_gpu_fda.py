@@ -194,11 +194,13 @@ def test_anisotropic_multilevel(gpu_device):
 
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
-def test_thin_levels_atomic_bucketing(gpu_device, dt):
+@pytest.mark.parametrize("Q", [300, 1200])
+def test_thin_levels_atomic_bucketing(gpu_device, dt, Q):
     """Levels one voxel thick and thousands long are cut into more tiles than the bucketing
-    matrix holds (S/16 + 64 per head), so the backward buckets them with global atomics."""
-    inp = random_inputs([(1, 1, 4096), (1, 2048, 1)], 1, 300, 8, 32, 4, dt, seed=8)
-    _check(f"thin levels {dt}", inp, gpu_device, dt)
+    matrix holds (S/16 + 64 per head), so the backward buckets them with global atomics -- in
+    the one-block-per-head launch (Q = 300: 2400 samples per head) and across blocks (Q = 1200)."""
+    inp = random_inputs([(1, 1, 4096), (1, 2048, 1)], 1, Q, 8, 32, 4, dt, seed=8)
+    _check(f"thin levels {dt} Q={Q}", inp, gpu_device, dt)
 
 
 def test_out_of_volume_fp32(gpu_device):
