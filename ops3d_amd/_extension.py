@@ -248,7 +248,7 @@ class _NativeFDA:
         buf = (ctypes.c_float * 8)()
         if which == "backward":
             n = self._lib.ops3d_fda_profile_read(0, buf, 8)
-            names = ("head_major_copies", "query_kernel", "tile_count", "tile_scatter", "tile_kernel")
+            names = ("head_major_copies", "query_kernel", "tile_count", "tile_scatter", "tile_kernel", "finish_kernel")
         else:
             n = self._lib.ops3d_fda_profile_read(1, buf, 8)
             names = ("head_major_copy", "forward_kernel")

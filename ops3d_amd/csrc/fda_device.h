@@ -60,6 +60,13 @@ struct Args {
   int chunk;                  // entries per LDS chunk of the tile kernel
   int tile_affinity;          // tiles of head g run on XCD g % 8 (G % 8 == 0)
   int accumulate;             // add into an fp32 grad_value instead of overwriting
+  // tile-major backward (fda_fused.h): per-sample records live in `keys` (as uint4)
+  float4 *ures;               // [N] per-sample (grad x, y, z times attn * size, grad attn)
+  uint32_t *part;             // [B*G][bph + 2] partition of each head's entries
+  float *pslots;              // [B*G*bph][2][128 voxels][32] fp32 partial tiles
+  int bph;                    // tile-kernel blocks per head
+  uint64_t n_entries;         // entries capacity (elements)
+  uint64_t n_samples;         // N
   int vhm;                    // value is head-major [B,G,S,D] (a transposed copy)
   int pair_levels;            // head-major copy in which large levels may be paired (copy_level);
                               // 0: every level at its level_start_index, heads S rows apart

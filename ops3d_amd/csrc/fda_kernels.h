@@ -20,6 +20,8 @@
 #pragma once
 
 #include "fda_device.h"
+#include "fda_tile_mfma.h"
+#include "fda_fused.h"
 
 #ifndef OPS3D_FDA_TILE_UNROLL
 #define OPS3D_FDA_TILE_UNROLL 2   // entries in flight per owner loop step
@@ -1235,6 +1237,25 @@ hipError_t launch_one(int which, const Args &a, unsigned grid, size_t lds, hipSt
     // one block per tile of every group (`grid` = the bound on tiles times the groups)
     constexpr int TL = tile_lanes(LPU, CPL * (int)sizeof(T)), TC = CPL * LPU / TL;
     hipLaunchKernelGGL((fda_bwd_split_combine_kernel<T, TC, TL>), dim3(grid), dim3(tile_threads(TL)), 0, st, a);
+  }
+  else if (which >= 5 && which <= 8) {
+    // tile-major backward: 5 setup, 6 tile, 7 combine, 8 finish
+    if constexpr (sizeof(T) == 2 && CPL == 8 && LPU == 4) {
+      if (which == 5) {
+        hipLaunchKernelGGL((fda_bwd_setup_kernel<T>), dim3(grid), dim3(kBlock), lds, st, a);
+      } else if (which == 6) {
+        if (a.accumulate)
+          hipLaunchKernelGGL((fda_bwd_fused_tile_kernel<T, true>), dim3(grid), dim3(kFusedThreads), lds, st, a);
+        else
+          hipLaunchKernelGGL((fda_bwd_fused_tile_kernel<T, false>), dim3(grid), dim3(kFusedThreads), lds, st, a);
+      } else if (which == 7) {
+        hipLaunchKernelGGL((fda_bwd_fused_combine_kernel<T>), dim3(grid), dim3(256), 0, st, a);
+      } else {
+        hipLaunchKernelGGL((fda_bwd_finish_kernel<T>), dim3(grid), dim3(kBlock), lds, st, a);
+      }
+    } else {
+      return hipErrorInvalidValue;
+    }
   }
   else {
     // persistent: `grid` (the CU count, a multiple of 8 with XCD affinity) times the blocks that
