@@ -232,8 +232,7 @@ def summary_line(r):
         ph = r["bwd_kernel"]
         parts.append(f"bwd {bk * 1e3:7.1f} us [copy {ph['head_major_copies']['mean'] * 1e3:.1f} "
                      f"q {ph['query_kernel']['mean'] * 1e3:.1f} count {ph['tile_count']['mean'] * 1e3:.1f} "
-                     f"scatter {ph['tile_scatter']['mean'] * 1e3:.1f} tile {ph['tile_kernel']['mean'] * 1e3:.1f} "
-                     f"finish {ph.get('finish_kernel', {'mean': 0.0})['mean'] * 1e3:.1f}]")
+                     f"scatter {ph['tile_scatter']['mean'] * 1e3:.1f} tile {ph['tile_kernel']['mean'] * 1e3:.1f}]")
     parts.append(f"{samples / (s or f) / 1e6:.3g} Gsamples/s" if (s or f) else "")
     return " | ".join(parts)
 

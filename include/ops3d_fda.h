@@ -51,13 +51,18 @@ OPS3D_FDA_API const char *ops3d_fda_last_error(void);
 OPS3D_FDA_API int ops3d_fda_supported(int dtype, int channels);
 
 /*
- * Bytes of optional device workspace for ops3d_fda_forward: room for a head-major copy of value
- * (0 when G == 1 or on invalid sizes): [B,G] slices of S rows of D elements, or, with 64-byte
- * rows (D * element size == 64), of 2*S + 10 rows, where levels larger than 8 MiB per head are
- * stored as aligned x-neighbour row pairs (each pair load then reads one 128-byte line).
+ * Bytes of optional device workspace for ops3d_fda_forward: room for the head-major copy of value
+ * that the forward makes, or 0 when it makes none -- G == 1 (value is already head-major), value
+ * smaller than 8 MiB per batch item (it fits every XCD's L2), fewer corner reads than a head has
+ * rows (Q*L*K*8 < S), or invalid sizes.  The copy is [B,G] slices of S rows of D elements, or,
+ * with 64-byte rows (D * element size == 64), of 2*S + 10 rows, where levels larger than 8 MiB
+ * per head are stored as aligned x-neighbour row pairs (each pair load then reads one 128-byte
+ * line).
  */
 OPS3D_FDA_API size_t ops3d_fda_forward_workspace_bytes(int dtype, int batch, int spatial_size,
-                                                       int num_heads, int channels);
+                                                       int num_heads, int channels,
+                                                       int num_levels, int num_query,
+                                                       int num_point);
 
 /*
  * Forward.  Replaces flash_deform_attn_forward (reference csrc/flash_deform_attn.h:7-25 ->
@@ -65,9 +70,11 @@ OPS3D_FDA_API size_t ops3d_fda_forward_workspace_bytes(int dtype, int batch, int
  * ([B,Q,G*D], dtype), so the caller need not zero it.  The softmax over the L*K logits of each
  * (b,q,g) is computed in fp32 inside the kernel; trilinear sampling uses zero padding and
  * align_corners=False pixel coordinates (loc*size - 0.5).
- *   workspace:   optional (NULL/0 allowed).  With ops3d_fda_forward_workspace_bytes() bytes the
- *                library first copies value head-major, so that each head's rows are contiguous
- *                and, with heads mapped to XCDs, stay in one XCD's L2 (faster; same results).
+ *   workspace:   optional (NULL allowed).  When ops3d_fda_forward_workspace_bytes() is not 0 and
+ *                a workspace of at least that size is given, the library first copies value
+ *                head-major into it, so that each head's rows are contiguous and, with heads
+ *                mapped to XCDs, stay in one XCD's L2 (faster; same results).  A non-NULL
+ *                workspace smaller than that is an error (OPS3D_FDA_EINVAL).
  *   im2col_step: batch chunk size of the reference; min(batch, im2col_step) must divide batch
  *                (else OPS3D_FDA_ERUNTIME, as reference flash_deform_attn_cuda.cu:56-58).  Results
  *                do not depend on it.

@@ -2,7 +2,6 @@
 from ops3d_amd.flash_deform_attn import (  # noqa: F401
     FlashDeformAttnFunction,
     _C,
-    _is_power_of_2,
     factors,
     findspec,
     findspec_bwd,

@@ -58,9 +58,8 @@ def _run(cmd: list[str]) -> None:
         sys.stderr.write(err + "\n")
 
 
-def build(out_path: str = LIB_PATH, build_dir: str | None = None, extra_flags: list[str] | None = None) -> str:
-    """Compile every source for gfx950 and link ``libops3d_fda.so``; return its path.
-    ``extra_flags`` (e.g. ``-DOPS3D_FDA_TILE_WPE=8``) builds a tuning variant."""
+def build(out_path: str = LIB_PATH, build_dir: str | None = None) -> str:
+    """Compile every source for gfx950 and link ``libops3d_fda.so``; return its path."""
     hipcc = _hipcc()
     build_dir = build_dir or os.path.join(PKG_DIR, "_build")
     os.makedirs(build_dir, exist_ok=True)
@@ -69,7 +68,7 @@ def build(out_path: str = LIB_PATH, build_dir: str | None = None, extra_flags: l
     for src in SOURCES:
         obj = os.path.join(build_dir, src.replace(".hip", ".o"))
         objs.append(obj)
-        cmds.append([hipcc, *HIP_FLAGS, *(extra_flags or []), "-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append([hipcc, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
     with ThreadPoolExecutor(max_workers=min(len(cmds), os.cpu_count() or 1)) as ex:
         list(ex.map(_run, cmds))
     tmp = out_path + ".tmp"

@@ -20,8 +20,7 @@ import os
 import torch  # imported first: its HIP runtime is the one libops3d_fda.so binds to
 
 _PKG_DIR = os.path.dirname(os.path.abspath(__file__))
-# OPS3D_FDA_LIBRARY selects another build of the library (e.g. a tuning variant)
-LIB_PATH = os.environ.get("OPS3D_FDA_LIBRARY") or os.path.join(_PKG_DIR, "libops3d_fda.so")
+LIB_PATH = os.path.join(_PKG_DIR, "libops3d_fda.so")
 
 OPS3D_FDA_OK, OPS3D_FDA_EINVAL, OPS3D_FDA_ERUNTIME = 0, 1, 2
 _DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
@@ -51,7 +50,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ops3d_fda_supported.restype = _i
     lib.ops3d_fda_supported.argtypes = [_i, _i]
     lib.ops3d_fda_forward_workspace_bytes.restype = _sz
-    lib.ops3d_fda_forward_workspace_bytes.argtypes = [_i] * 5
+    lib.ops3d_fda_forward_workspace_bytes.argtypes = [_i] * 8
     lib.ops3d_fda_forward.restype = _i
     lib.ops3d_fda_forward.argtypes = [_vp] * 6 + [_sz] + [_i] * 9 + [_vp]
     lib.ops3d_fda_backward_workspace_bytes.restype = _sz
@@ -75,7 +74,7 @@ def _ptr(t: torch.Tensor | None) -> int | None:
 class _NativeFDA:
     """Host side of the flash-deform-attn extension, bound to libops3d_fda.so."""
 
-    ABI_VERSION = 4
+    ABI_VERSION = 5
 
     def __init__(self, lib: ctypes.CDLL, path: str):
         self._lib = lib
@@ -153,11 +152,11 @@ class _NativeFDA:
 
     def forward_keep_head_major(self, value, spatial_shapes, level_start_index, sampling_loc_attn, im2col_step, K):
         """Forward that also returns its workspace, which holds the head-major copy of value
-        (None when G == 1), for backward_with_head_major."""
+        (None when the forward makes no copy), for backward_with_head_major."""
         B, S, G, D, L, Q = self._common(value, spatial_shapes, level_start_index, sampling_loc_attn, K, {})
         out = torch.empty((B, Q, G * D), dtype=value.dtype, device=value.device)
         code = _DTYPE_CODE[value.dtype]
-        n = self._lib.ops3d_fda_forward_workspace_bytes(code, B, S, G, D) if B * Q > 0 else 0
+        n = self._lib.ops3d_fda_forward_workspace_bytes(code, B, S, G, D, L, Q, int(K))
         ws = torch.empty(n, dtype=torch.uint8, device=value.device) if n else None
         stream = torch.cuda.current_stream(value.device).cuda_stream
         with torch.cuda.device(value.device):
@@ -188,10 +187,12 @@ class _NativeFDA:
         )
         if grad_output.numel() != B * Q * G * D:
             raise ValueError(f"grad_output must have B*Q*G*D = {B * Q * G * D} elements, got {grad_output.numel()}")
-        if value_head_major is not None and (value_head_major.device != value.device
-                                             or value_head_major.numel() < value.numel() * value.element_size()):
-            raise ValueError("value_head_major is not a forward workspace of this value")
         code = _DTYPE_CODE[value.dtype]
+        if value_head_major is not None:
+            need = self._lib.ops3d_fda_forward_workspace_bytes(code, B, S, G, D, L, Q, int(K))
+            if (value_head_major.device != value.device or value_head_major.dtype != torch.uint8
+                    or value_head_major.numel() != need):
+                raise ValueError("value_head_major is not a forward workspace of this value")
         grad_value = torch.empty_like(value)
         grad_sla = torch.empty_like(sampling_loc_attn)
         ws, ws_bytes = self._workspace(code, B, S, G, D, L, Q, K, value.device)
@@ -248,7 +249,7 @@ class _NativeFDA:
         buf = (ctypes.c_float * 8)()
         if which == "backward":
             n = self._lib.ops3d_fda_profile_read(0, buf, 8)
-            names = ("head_major_copies", "query_kernel", "tile_count", "tile_scatter", "tile_kernel", "finish_kernel")
+            names = ("head_major_copies", "query_kernel", "tile_count", "tile_scatter", "tile_kernel")
         else:
             n = self._lib.ops3d_fda_profile_read(1, buf, 8)
             names = ("head_major_copy", "forward_kernel")
@@ -298,7 +299,7 @@ def reload() -> None:
     from . import flash_deform_attn as _fda
 
     _fda._C = _C
-    for name in ("ops3d_amd", "ops3d"):   # the packages re-export _C
+    for name in ("ops3d_amd", "ops3d", "ops3d.flash_deform_attn"):   # modules that re-export _C
         mod = sys.modules.get(name)
         if mod is not None:
             mod._C = _C

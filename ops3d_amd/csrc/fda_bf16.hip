@@ -12,14 +12,4 @@ hipError_t launch_bf16(int which, int cpl, int lpu, const Args &a, unsigned grid
   }
 }
 
-// Resident blocks per CU of the tile-major backward's tile kernel (the f16 instance has the same
-// resources).
-int fused_tile_blocks_per_cu() {
-  int occ = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fda_bwd_fused_tile_kernel<__bf16, false>, kFusedThreads,
-                                                   fused_tile_lds_bytes()) != hipSuccess)
-    return 0;
-  return occ;
-}
-
 }  // namespace ops3d_fda

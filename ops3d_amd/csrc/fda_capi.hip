@@ -22,19 +22,15 @@
 
 #include "../../include/ops3d_fda.h"
 #include "fda_device.h"
-#include "fda_tile_mfma.h"
-#include "fda_fused.h"
 
 namespace ops3d_fda {
 hipError_t launch_f32(int, int, int, const Args &, unsigned, size_t, hipStream_t);
 hipError_t launch_f16(int, int, int, const Args &, unsigned, size_t, hipStream_t);
 hipError_t launch_bf16(int, int, int, const Args &, unsigned, size_t, hipStream_t);
-hipError_t launch_tile_bucketing(const uint32_t *keys, const uint32_t *words, const void *srec, uint32_t n,
-                                 uint32_t per_head, const int64_t *shapes, int L, int BG, int TX, int TY, int TZ,
-                                 uint32_t *counts, uint32_t *start, uint32_t *cursor, uint32_t *mat, uint32_t tcap,
-                                 uint32_t *entries, uint32_t *queue, uint32_t *part, int bph, bool counts_cleared,
-                                 hipStream_t st, void (*mark)(int, hipStream_t));
-int fused_tile_blocks_per_cu();
+hipError_t launch_tile_bucketing(const uint32_t *keys, const uint32_t *words, uint32_t n, uint32_t per_head,
+                                 const int64_t *shapes, int L, int BG, int TX, int TY, int TZ, uint32_t *counts,
+                                 uint32_t *start, uint32_t *cursor, uint32_t *mat, uint32_t tcap, uint32_t *entries, uint32_t *queue,
+                                 bool counts_cleared, hipStream_t st, void (*mark)(int, hipStream_t));
 size_t tile_matrix_words(uint32_t BG, uint32_t tcap);
 uint32_t tile_window(uint32_t tcap);
 }  // namespace ops3d_fda
@@ -46,10 +42,9 @@ namespace {
 thread_local std::string g_last_error;
 
 // backward phase timing (ops3d_fda_profile_*)
-// events 0..6: backward (copies | query or setup kernel | tile count + scan | tile scatter | tile
-// kernel | finish kernel); events 7..9: forward (head-major copy | forward kernel)
-constexpr int kProfEvents = 10;
-constexpr int kProfFwd = 7;
+// events 0..5: backward (copies | query kernel | tile count + scan | tile scatter | tile kernel)
+// events 6..8: forward (head-major copy | forward kernel)
+constexpr int kProfEvents = 9;
 bool g_prof_on = false;
 bool g_prof_recorded[2] = {false, false};
 hipEvent_t g_prof_ev[kProfEvents];
@@ -240,7 +235,7 @@ int bwd_layout(int B, int S, int G, int D, int e, int lpu, int L, int Q, int K, 
   }
   ly.tcap = (uint32_t)(S / 16 + 64);
   ly.off_mat = o; o += align256(tile_matrix_words((uint32_t)(B * G), ly.tcap) * 4);
-  ly.off_vhm = o; o += G > 1 ? align256((size_t)B * G * (size_t)head_copy_rows_max(S, D * e) * D * e) : 0;
+  ly.off_vhm = o; o += G > 1 && head_major_pays(S, G, D, e, Q, L, K) ? align256((size_t)B * G * (size_t)head_copy_rows_max(S, D * e) * D * e) : 0;
   ly.off_ghm = o; o += grad_out_copied(B, Q, G, D, e) ? align256((size_t)B * Q * G * D * e) : 0;
   ly.total = o;
   return OPS3D_FDA_OK;
@@ -253,10 +248,7 @@ int tile_chunk(int D, int e, int lpu) {
   const int rb = D * e;
   const int nt = tile_threads(lpu);
   const size_t bins = tile_kernel_lds_bytes(0, rb, lpu);
-#ifndef OPS3D_FDA_TILE_LDS_KB_256
-#define OPS3D_FDA_TILE_LDS_KB_256 50
-#endif
-  const size_t budget = (nt >= 1024 ? 150 : (nt >= 512 ? 76 : OPS3D_FDA_TILE_LDS_KB_256)) * (size_t)1024;
+  const size_t budget = (nt >= 1024 ? 150 : (nt >= 512 ? 76 : 50)) * (size_t)1024;
   if (budget <= bins) return 0;
   int ch = (int)((budget - bins) / (size_t)(rb + 20));
   ch = ch > kTileKPT * nt ? kTileKPT * nt : ch;
@@ -341,7 +333,7 @@ __global__ __launch_bounds__(256) void head_major_kernel(const uint32_t *src, ui
 }
 
 hipError_t launch_head_major(const void *src, void *dst, int64_t B, int64_t N, int G, int D, int esize,
-                             const int64_t *shapes, const int64_t *lsi, int L, hipStream_t st, bool allow_pairs = true) {
+                             const int64_t *shapes, const int64_t *lsi, int L, hipStream_t st) {
   const int R = D * esize / 4;
   const int64_t chunks = B * N * G * ((R & 3) == 0 ? R / 4 : R);
   int64_t blocks = (chunks + 255) / 256;
@@ -349,81 +341,15 @@ hipError_t launch_head_major(const void *src, void *dst, int64_t B, int64_t N, i
   if (blocks < 1) return hipSuccess;
   hipLaunchKernelGGL(head_major_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
                      static_cast<const uint32_t *>(src), static_cast<uint32_t *>(dst), B, N, G, R, shapes, lsi, L,
-                     allow_pairs && pairing_possible(N, R * 4) ? 1 : 0);
+                     pairing_possible(N, R * 4) ? 1 : 0);
   return hipGetLastError();
-}
-
-// ---------------------------------------------------------------------------------------------
-// Tile-major backward (fda_fused.h): 16-bit types with D = 32.  The tile kernel is persistent with
-// an equal share of a head's entries per block: bph blocks per head, and with G % 8 == 0 the
-// blocks of the heads with g % 8 == x on XCD x.
-struct FusedPlan {
-  bool on;
-  int bph;
-  unsigned grid;   // tile and combine kernel blocks
-};
-
-// The tile-major backward is selected only where it is measured faster than the gather backward
-// (query kernel + VALU tile kernel); so far it is not, at any configuration.
-constexpr bool kFusedBackward = false;
-
-FusedPlan fused_plan(int dtype, int B, int S, int G, int D, int L, int Q, int K) {
-  FusedPlan p{false, 0, 0};
-  if (!kFusedBackward || elem_size(dtype) != 2 || D != 32 || B <= 0 || Q <= 0 || S <= 0) return p;
-  // entry offsets of a head (8 per sample) and its samples' records stay below 2^32 bytes
-  const uint64_t per_head = (uint64_t)Q * L * K;
-  if (per_head * 8u * 4u >= 0xfff00000ull || (uint64_t)B * G * per_head >= 0x0fffffffull) return p;
-  static int occ = -1;
-  if (occ < 0) occ = fused_tile_blocks_per_cu();
-  if (occ <= 0) return p;
-  const int slots = device_cus() * occ;
-  if (G % 8 == 0) {
-    const int nbg = B * G / 8, nbx = slots / 8;
-    p.bph = nbx / nbg;
-    p.grid = (unsigned)(8 * nbg * p.bph);
-  } else {
-    const int nbg = B * G;
-    p.bph = slots / nbg;
-    p.grid = (unsigned)(nbg * p.bph);
-  }
-  p.on = p.bph >= 1;
-  return p;
-}
-
-struct FusedLayout {
-  uint64_t n;
-  uint32_t tcap;
-  size_t off_srec, off_ures, off_entries, off_counts, off_start, off_cursor, off_queue, off_part, off_pslots, off_mat,
-      off_ghm, total;
-};
-
-FusedLayout fused_layout(int B, int S, int G, int D, int e, int L, int Q, int K, int bph) {
-  FusedLayout f{};
-  f.n = (uint64_t)B * Q * G * L * K;
-  const uint64_t ntiles = (uint64_t)B * G * (uint64_t)S;
-  const size_t t4 = align256((ntiles + 1) * 4);
-  size_t o = 0;
-  f.off_srec = o; o += align256(f.n * 16);
-  f.off_ures = o; o += align256(f.n * 16);
-  f.off_entries = o; o += align256(f.n * 8 * 4);
-  f.off_counts = o; o += t4;
-  f.off_start = o; o += t4;
-  f.off_cursor = o; o += t4;
-  f.off_queue = o; o += 256;
-  f.off_part = o; o += align256((size_t)B * G * (bph + 2) * 4);
-  f.off_pslots = o; o += align256((size_t)B * G * bph * 2 * 4096 * 4);
-  f.tcap = (uint32_t)(S / 16 + 64);
-  f.off_mat = o; o += align256(tile_matrix_words((uint32_t)(B * G), f.tcap) * 4);
-  f.off_ghm = o; o += grad_out_copied(B, Q, G, D, e) ? align256((size_t)B * Q * G * D * e) : 0;
-  f.total = o;
-  return f;
 }
 
 }  // namespace
 
 extern "C" {
 
-int ops3d_fda_abi_version(void) { return 4; }
+int ops3d_fda_abi_version(void) { return 5; }
 
 const char *ops3d_fda_last_error(void) { return g_last_error.c_str(); }
 
@@ -433,9 +359,12 @@ int ops3d_fda_supported(int dtype, int channels) {
 }
 
 size_t ops3d_fda_forward_workspace_bytes(int dtype, int batch, int spatial_size, int num_heads,
-                                         int channels) {
+                                         int channels, int num_levels, int num_query, int num_point) {
   const int e = elem_size(dtype);
-  if (e == 0 || batch <= 0 || spatial_size <= 0 || num_heads <= 1 || channels <= 0) return 0;
+  if (e == 0 || batch <= 0 || spatial_size <= 0 || num_heads <= 1 || channels <= 0 || num_levels < 1 ||
+      num_query <= 0 || num_point < 1)
+    return 0;
+  if (!head_major_pays(spatial_size, num_heads, channels, e, num_query, num_levels, num_point)) return 0;
   return align256((size_t)batch * num_heads * (size_t)head_copy_rows_max(spatial_size, channels * e) * channels * e);
 }
 
@@ -457,9 +386,12 @@ int ops3d_fda_forward(const void *value, const int64_t *spatial_shapes,
     return fail(OPS3D_FDA_EINVAL, "tensor data pointers must be 4-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
   geo.a.value = value;
-  prof_mark(kProfFwd, st);
-  const size_t need = ops3d_fda_forward_workspace_bytes(dtype, batch, spatial_size, num_heads, channels);
-  if (need > 0 && workspace && workspace_bytes >= need && head_major_pays(spatial_size, num_heads, channels, elem_size(dtype), num_query, num_levels, num_point)) {
+  prof_mark(6, st);
+  const size_t need = ops3d_fda_forward_workspace_bytes(dtype, batch, spatial_size, num_heads, channels,
+                                                        num_levels, num_query, num_point);
+  if (workspace && need > 0 && workspace_bytes < need)
+    return fail(OPS3D_FDA_EINVAL, "forward workspace too small: %zu bytes given, %zu needed", workspace_bytes, need);
+  if (workspace && need > 0) {
     hipError_t e = launch_head_major(value, workspace, batch, spatial_size, num_heads, channels,
                                      elem_size(dtype), spatial_shapes, level_start_index, num_levels, st);
     if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "head-major copy failed: %s", hipGetErrorString(e));
@@ -471,12 +403,12 @@ int ops3d_fda_forward(const void *value, const int64_t *spatial_shapes,
   geo.a.lsi = level_start_index;
   geo.a.loc_attn = sampling_loc_attn;
   geo.a.out = output;
-  prof_mark(kProfFwd + 1, st);
+  prof_mark(7, st);
   hipError_t e = launch(dtype, 0, geo, st);
   if (e != hipSuccess)
     return fail(OPS3D_FDA_ERUNTIME, "forward kernel launch failed: %s (grid=%u, lds=%zu)",
                 hipGetErrorString(e), geo.grid, geo.lds);
-  prof_mark(kProfFwd + 2, st);
+  prof_mark(8, st);
   if (g_prof_on) g_prof_recorded[1] = true;
   return OPS3D_FDA_OK;
 }
@@ -489,10 +421,6 @@ size_t ops3d_fda_backward_workspace_bytes(int dtype, int batch, int spatial_size
   BwdLayout ly;
   int cpl = 0, lpu = 0;
   if (!pick_config(dtype, channels, cpl, lpu)) return 0;
-  const FusedPlan plan = fused_plan(dtype, batch, spatial_size, num_heads, channels, num_levels, num_query, num_point);
-  if (plan.on)
-    return fused_layout(batch, spatial_size, num_heads, channels, elem_size(dtype), num_levels, num_query, num_point,
-                        plan.bph).total;
   if (bwd_layout(batch, spatial_size, num_heads, channels, elem_size(dtype), tile_lanes(lpu, cpl * elem_size(dtype)),
                  num_levels, num_query, num_point, ly))
     return 0;
@@ -523,116 +451,13 @@ static int backward_impl(const void *value, const void *value_head_major, const 
   if (!spatial_shapes || !level_start_index) return fail(OPS3D_FDA_EINVAL, "NULL pointer argument");
   if (work && (!sampling_loc_attn || !grad_output || !grad_sampling_loc_attn || (!value && spatial_size > 0)))
     return fail(OPS3D_FDA_EINVAL, "NULL pointer argument");
+  if (!workspace || workspace_bytes < ly.total)
+    return fail(OPS3D_FDA_EINVAL, "workspace too small: %zu bytes given, %zu needed", workspace_bytes, ly.total);
   if (misaligned(value) || misaligned(sampling_loc_attn) || misaligned(grad_output) ||
       misaligned(grad_sampling_loc_attn) || misaligned(grad_value))
     return fail(OPS3D_FDA_EINVAL, "tensor data pointers must be 4-byte aligned");
-  if (workspace && (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
     return fail(OPS3D_FDA_EINVAL, "workspace must be 256-byte aligned");
-  const FusedPlan plan = fused_plan(dtype, batch, spatial_size, num_heads, channels, num_levels, num_query, num_point);
-  if (plan.on) {
-    const FusedLayout fl = fused_layout(batch, spatial_size, num_heads, channels, elem_size(dtype), num_levels,
-                                        num_query, num_point, plan.bph);
-    if (!workspace || workspace_bytes < fl.total)
-      return fail(OPS3D_FDA_EINVAL, "workspace too small: %zu bytes given, %zu needed", workspace_bytes, fl.total);
-    char *ws = static_cast<char *>(workspace);
-    Args &a = geo.a;
-    a.value = value;
-    a.shapes = spatial_shapes;
-    a.lsi = level_start_index;
-    a.loc_attn = sampling_loc_attn;
-    a.grad_out = grad_output;
-    a.grad_loc_attn = grad_sampling_loc_attn;
-    a.out = grad_value;
-    a.accumulate = out_f32_accumulate ? 1 : 0;
-    a.keys = reinterpret_cast<uint32_t *>(ws + fl.off_srec);
-    a.ures = reinterpret_cast<float4 *>(ws + fl.off_ures);
-    a.entries = reinterpret_cast<uint32_t *>(ws + fl.off_entries);
-    a.tile_counts = reinterpret_cast<uint32_t *>(ws + fl.off_counts);
-    a.tile_start = reinterpret_cast<uint32_t *>(ws + fl.off_start);
-    a.tile_cursor = reinterpret_cast<uint32_t *>(ws + fl.off_cursor);
-    a.tile_queue = reinterpret_cast<uint32_t *>(ws + fl.off_queue);
-    a.part = reinterpret_cast<uint32_t *>(ws + fl.off_part);
-    a.pslots = reinterpret_cast<float *>(ws + fl.off_pslots);
-    a.bph = plan.bph;
-    a.n_entries = fl.n * 8u;
-    a.n_samples = fl.n;
-    a.count_clear_wcap = tile_window(fl.tcap);
-    a.TX = 8; a.TY = 4; a.TZ = 4;
-    a.inv_lk = 1.0 / (double)(num_levels * num_point);
-    a.tile_affinity = num_heads % 8 == 0;
-    a.gout_hm = grad_out_copied(batch, num_query, num_heads, channels, elem_size(dtype)) ? ws + fl.off_ghm : nullptr;
-    hipError_t e;
-    prof_mark(0, st);
-    if (a.gout_hm) {
-      e = launch_head_major(grad_output, a.gout_hm, batch, num_query, num_heads, channels, elem_size(dtype),
-                            spatial_shapes, level_start_index, num_levels, st, false);
-      if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "grad_output copy failed: %s", hipGetErrorString(e));
-    }
-    prof_mark(1, st);
-    {   // setup: 32 units of one (b, g) per block
-      Geometry gs = geo;
-      gs.a.nqb = (num_query + kSetupUnits - 1) / kSetupUnits;
-      gs.a.ncol = batch * gs.a.nqb;
-      int64_t grid;
-      if (gs.a.xcd_mode == 0) grid = (int64_t)num_heads * gs.a.ncol;
-      else if (gs.a.xcd_mode == 1) grid = 8 * (((int64_t)gs.a.ncol + gs.a.xpg - 1) / gs.a.xpg);
-      else grid = (int64_t)num_heads * gs.a.ncol;
-      gs.grid = (unsigned)grid;
-      gs.lds = (size_t)kSetupUnits * (size_t)(geo.a.P + 1) * sizeof(float);
-      e = launch(dtype, 5, gs, st);
-      if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "setup kernel launch failed: %s", hipGetErrorString(e));
-    }
-    prof_mark(2, st);
-    e = launch_tile_bucketing(nullptr, nullptr, a.keys, (uint32_t)fl.n,
-                              (uint32_t)num_query * (uint32_t)(num_levels * num_point), spatial_shapes, num_levels,
-                              batch * num_heads, 8, 4, 4, a.tile_counts, a.tile_start, a.tile_cursor,
-                              reinterpret_cast<uint32_t *>(ws + fl.off_mat), fl.tcap, a.entries, a.tile_queue, a.part,
-                              plan.bph, true, st, g_prof_on ? prof_mark : nullptr);
-    if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "tile bucketing failed: %s", hipGetErrorString(e));
-    prof_mark(4, st);
-    {
-      Geometry gt = geo;
-      gt.grid = plan.grid;
-      gt.lds = fused_tile_lds_bytes();
-#ifdef FUSED_TIMING
-      static unsigned long long *dbg = nullptr;
-      if (!dbg && hipMalloc(&dbg, 32 * sizeof(unsigned long long)) != hipSuccess) dbg = nullptr;
-      if (dbg) (void)hipMemsetAsync(dbg, 0, 32 * sizeof(unsigned long long), st);
-      gt.a.dbg = dbg;
-#endif
-      e = launch(dtype, 6, gt, st);
-#ifdef FUSED_TIMING
-      if (dbg) {
-        unsigned long long h[32];
-        if (hipMemcpyAsync(h, dbg, sizeof(h), hipMemcpyDeviceToHost, st) == hipSuccess && hipStreamSynchronize(st) == hipSuccess)
-          for (int w = 0; w < 4; ++w) {
-            unsigned long long tot = 0;
-            for (int i = 0; i < 8; ++i) tot += h[8 * w + i];
-            fprintf(stderr, "[fused w%d] wait %.1f%% derive %.1f%% bar %.1f%% place+issue %.1f%% U %.1f%% mfma %.1f%% flush %.1f%% loop %.1f%% (%.3g Mcyc/block, grid %u)\n", w,
-                    100.0 * h[8*w+0] / tot, 100.0 * h[8*w+1] / tot, 100.0 * h[8*w+2] / tot, 100.0 * h[8*w+3] / tot, 100.0 * h[8*w+4] / tot,
-                    100.0 * h[8*w+5] / tot, 100.0 * h[8*w+6] / tot, 100.0 * h[8*w+7] / tot, tot / 1e6 / gt.grid, gt.grid);
-          }
-      }
-#endif
-      if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "tile kernel launch failed: %s", hipGetErrorString(e));
-      e = launch(dtype, 7, gt, st);
-      if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "combine kernel launch failed: %s", hipGetErrorString(e));
-    }
-    prof_mark(5, st);
-    {
-      Geometry gf = geo;
-      const int64_t units = (int64_t)batch * num_query * num_heads;
-      gf.grid = (unsigned)((units + kSetupUnits - 1) / kSetupUnits);
-      gf.lds = (size_t)kSetupUnits * (size_t)(geo.a.P + 1) * sizeof(float);
-      e = launch(dtype, 8, gf, st);
-      if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "finish kernel launch failed: %s", hipGetErrorString(e));
-    }
-    prof_mark(6, st);
-    if (g_prof_on) g_prof_recorded[0] = true;
-    return OPS3D_FDA_OK;
-  }
-  if (!workspace || workspace_bytes < ly.total)
-    return fail(OPS3D_FDA_EINVAL, "workspace too small: %zu bytes given, %zu needed", workspace_bytes, ly.total);
 
   char *ws = static_cast<char *>(workspace);
   uint32_t *keys = reinterpret_cast<uint32_t *>(ws + ly.off_keys);
@@ -691,11 +516,11 @@ static int backward_impl(const void *value, const void *value_head_major, const 
   prof_mark(2, st);
   // phase 2: entries grouped by tile (counters are cleared even without samples: the tile
   // kernel reads the tile ranges of every tile)
-  e = launch_tile_bucketing(keys, words, nullptr, work ? (uint32_t)ly.n : 0u,
+  e = launch_tile_bucketing(keys, words, work ? (uint32_t)ly.n : 0u,
                             (uint32_t)num_query * (uint32_t)(num_levels * num_point), spatial_shapes, num_levels,
                             batch * num_heads, a.TX, a.TY, a.TZ, counts, tstart, cursor,
                             reinterpret_cast<uint32_t *>(ws + ly.off_mat), ly.tcap, entries,
-                            reinterpret_cast<uint32_t *>(ws + ly.off_queue), nullptr, 0, work, st,
+                            reinterpret_cast<uint32_t *>(ws + ly.off_queue), work, st,
                             g_prof_on ? prof_mark : nullptr);
   if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "tile bucketing failed: %s", hipGetErrorString(e));
   prof_mark(4, st);
@@ -712,46 +537,10 @@ static int backward_impl(const void *value, const void *value_head_major, const 
     if (g3.a.tile_affinity) g3.grid = (g3.grid + 7) & ~7u;
     if (g3.a.chunk < 64 || g3.lds > 160 * 1024)
       return fail(OPS3D_FDA_EINVAL, "channels per head D=%d too large for the backward tile kernel", channels);
-#ifdef MFMA_TIMING
-    static unsigned long long *dbg = nullptr;
-    if (!dbg && hipMalloc(&dbg, 32 * sizeof(unsigned long long)) != hipSuccess) dbg = nullptr;
-    if (dbg) (void)hipMemsetAsync(dbg, 0, 32 * sizeof(unsigned long long), st);
-    g3.a.dbg = dbg;
-#endif
     e = launch(dtype, 2, g3, st);
     if (e != hipSuccess)
       return fail(OPS3D_FDA_ERUNTIME, "backward tile kernel launch failed: %s (grid=%u, lds=%zu)",
                   hipGetErrorString(e), g3.grid, g3.lds);
-#ifdef MFMA_TIMING
-    if (dbg) {
-      unsigned long long h[32];
-      if (hipMemcpyAsync(h, dbg, sizeof(h), hipMemcpyDeviceToHost, st) == hipSuccess &&
-          hipStreamSynchronize(st) == hipSuccess) {
-        int occ = 0;
-        (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fda_bwd_tile_mfma_kernel<__bf16>, 256, g3.lds);
-        for (int w = 0; w < 4; ++w) {
-          unsigned long long tot = 0;
-          for (int i = 0; i < 8; ++i) tot += h[8 * w + i];
-          fprintf(stderr, "[mfma w%d occ %d] wait %.1f%% sort %.1f%% place %.1f%% half0 %.1f%% pref %.1f%% half1 %.1f%% endbar %.1f%% tile %.1f%% (%.3g Mcyc/block)\n", w, occ,
-                  100.0 * h[8*w+0] / tot, 100.0 * h[8*w+1] / tot, 100.0 * h[8*w+2] / tot, 100.0 * h[8*w+3] / tot, 100.0 * h[8*w+4] / tot,
-                  100.0 * h[8*w+5] / tot, 100.0 * h[8*w+6] / tot, 100.0 * h[8*w+7] / tot, tot / 1e6 / (g3.grid * occ));
-        }
-      }
-    }
-#endif
-#if 0
-    if (dbg) {
-      unsigned long long h[6];
-      if (hipMemcpyAsync(h, dbg, sizeof(h), hipMemcpyDeviceToHost, st) == hipSuccess &&
-          hipStreamSynchronize(st) == hipSuccess) {
-        unsigned long long tot = 0;
-        for (int i = 0; i < 6; ++i) tot += h[i];
-        fprintf(stderr, "[tile timing] clear %.1f%% stage %.1f%% rows+scan %.1f%% sort %.1f%% owners %.1f%% tile %.1f%% (%.3g Mcyc/block)\n",
-                100.0 * h[0] / tot, 100.0 * h[1] / tot, 100.0 * h[2] / tot, 100.0 * h[3] / tot, 100.0 * h[4] / tot,
-                100.0 * h[5] / tot, tot / 1e6 / g3.grid);
-      }
-    }
-#endif
     if (ly.split_slots > 0) {
       // split tiles: add the parts' partial sums (a split needs at least 2 parts per tile, so a
       // group has at most slots / (2 * groups) tiles; the kernel exits when nothing was split)
@@ -764,7 +553,6 @@ static int backward_impl(const void *value, const void *value_head_major, const 
     }
   }
   prof_mark(5, st);
-  prof_mark(6, st);
   if (g_prof_on) g_prof_recorded[0] = true;
   return OPS3D_FDA_OK;
 }
@@ -782,7 +570,7 @@ int ops3d_fda_profile_enable(int on) {
 
 int ops3d_fda_profile_read(int which, float *ms, int n) {
   if (which < 0 || which > 1 || !g_prof_recorded[which] || !ms) return 0;
-  const int first = which == 0 ? 0 : kProfFwd, last = which == 0 ? kProfFwd - 1 : kProfFwd + 2;
+  const int first = which == 0 ? 0 : 6, last = which == 0 ? 5 : 8;
   if (hipEventSynchronize(g_prof_ev[last]) != hipSuccess) return 0;
   int k = 0;
   for (int i = first; i < last && k < n; ++i, ++k)

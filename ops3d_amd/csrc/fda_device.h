@@ -60,20 +60,12 @@ struct Args {
   int chunk;                  // entries per LDS chunk of the tile kernel
   int tile_affinity;          // tiles of head g run on XCD g % 8 (G % 8 == 0)
   int accumulate;             // add into an fp32 grad_value instead of overwriting
-  // tile-major backward (fda_fused.h): per-sample records live in `keys` (as uint4)
-  float4 *ures;               // [N] per-sample (grad x, y, z times attn * size, grad attn)
-  uint32_t *part;             // [B*G][bph + 2] partition of each head's entries
-  float *pslots;              // [B*G*bph][2][128 voxels][32] fp32 partial tiles
-  int bph;                    // tile-kernel blocks per head
-  uint64_t n_entries;         // entries capacity (elements)
-  uint64_t n_samples;         // N
   int vhm;                    // value is head-major [B,G,S,D] (a transposed copy)
   int pair_levels;            // head-major copy in which large levels may be paired (copy_level);
                               // 0: every level at its level_start_index, heads S rows apart
   void *gout_hm;              // head-major copy [B,G,Q,D] of grad_out (G > 1): written by the
                               // query kernel, read by the tile kernel
   double inv_lk;              // 1.0 / (L*K), for sample -> unit
-  unsigned long long *dbg;    // tile kernel phase cycles (OPS3D_FDA_TILE_TIMING builds only)
   int B, S, G, D, L, K, Q, P;
   int nqb;                    // query blocks per batch = ceil(Q / UPB)
   int ncol;                   // B * nqb
@@ -614,10 +606,7 @@ __device__ __forceinline__ uint32_t sample_index(int b, int g, int q, int s, int
 __host__ __device__ constexpr int tile_threads(int lpu) {
   return lpu <= 4 ? 256 : (lpu >= 16 ? 1024 : 64 * lpu);
 }
-#ifndef OPS3D_FDA_TILE_KPT
-#define OPS3D_FDA_TILE_KPT 2
-#endif
-constexpr int kTileKPT = OPS3D_FDA_TILE_KPT;   // entries per thread and chunk (chunk <= KPT * threads)
+constexpr int kTileKPT = 2;   // entries per thread and chunk (chunk <= KPT * threads)
 constexpr uint32_t kKeyInvalid = 0xffffffffu;
 
 // Lanes per x-pair of voxels in the tile kernel (lane_bytes = CPL * sizeof(T) of the query

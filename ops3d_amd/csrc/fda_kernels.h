@@ -20,51 +20,16 @@
 #pragma once
 
 #include "fda_device.h"
-#include "fda_tile_mfma.h"
-#include "fda_fused.h"
-
-#ifndef OPS3D_FDA_TILE_UNROLL
-#define OPS3D_FDA_TILE_UNROLL 2   // entries in flight per owner loop step
-#endif
-#ifndef OPS3D_FDA_TILE_TIMING
-#define OPS3D_FDA_TILE_TIMING 0   // 1: per-phase cycle counts of the tile kernel into Args::dbg
-#endif
-#ifndef OPS3D_FDA_FWD_WPE
-#define OPS3D_FDA_FWD_WPE 8     // minimum waves per SIMD the x-pair forward is compiled for
-#endif
-#ifndef OPS3D_FDA_TILE_WPE
-#define OPS3D_FDA_TILE_WPE 0    // minimum waves per SIMD the tile kernel is compiled for; 0: as many
-                                // as its blocks per CU give (tile_wpe)
-#endif
-
-// Tile order of the tile kernel: 1 = a per-XCD work counter after four static tiles when the
-// tiles hold at least a chunk of entries on average (else the static snake order, whose blocks
-// pay no claim per tiny tile); 0 = always the static snake order (no atomics).
-#ifndef OPS3D_FDA_TILE_QUEUE
-#define OPS3D_FDA_TILE_QUEUE 1
-#endif
-
-// Tile splitting (tile kernel): parts per tile aim at SPLIT_TARGET jobs per block, at most
-// SPLIT_MAX parts per tile.
-#ifndef OPS3D_FDA_SPLIT_TARGET
-#define OPS3D_FDA_SPLIT_TARGET 2u
-#endif
-#ifndef OPS3D_FDA_SPLIT_MAX
-#define OPS3D_FDA_SPLIT_MAX 8u
-#endif
-
-// Occupancy hint of the backward query pair kernel (waves per SIMD it is compiled for; 0: none).
-// Left to itself the compiler takes 107 VGPRs (4 waves); 5 waves fit without spills.
-#ifndef OPS3D_FDA_QUERY_WPE
-#define OPS3D_FDA_QUERY_WPE 5
-#endif
-#if OPS3D_FDA_QUERY_WPE > 0
-#define OPS3D_FDA_QUERY_ATTR __attribute__((amdgpu_waves_per_eu(OPS3D_FDA_QUERY_WPE)))
-#else
-#define OPS3D_FDA_QUERY_ATTR
-#endif
 
 namespace ops3d_fda {
+
+constexpr int kFwdWavesPerEU = 8;     // minimum waves per SIMD the x-pair forward is compiled for
+// Backward query pair kernel: left to itself the compiler takes 107 VGPRs (4 waves per SIMD);
+// 5 waves fit without spills.
+constexpr int kQueryWavesPerEU = 5;
+// Tile splitting (tile kernel): parts per tile aim at kSplitTarget jobs per block, at most
+// kSplitMax parts per tile.
+constexpr uint32_t kSplitTarget = 2u, kSplitMax = 8u;
 
 // NW raw words from a plain global pointer (aligned to 16 bytes when NW % 4 == 0).
 template <int NW>
@@ -208,7 +173,7 @@ __global__ __launch_bounds__(kBlock) void fda_forward_kernel(const Args a) {
 // not per byte, so this halves the gather work per sample.  Each half accumulates its own x-row
 // over all samples; the halves are summed once at the end.
 template <typename T, int CPL, bool kPairs>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(OPS3D_FDA_FWD_WPE))) void fda_forward_pair_kernel(const Args a) {
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kFwdWavesPerEU))) void fda_forward_pair_kernel(const Args a) {
   extern __shared__ float lds[];
   constexpr int LPU = 4, UL = 2 * LPU;
   constexpr int UPW = kWave / UL, UPB = kWavesPerBlock * UPW;
@@ -306,7 +271,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(OPS3D_FD
 // the lane that made a set-up also records that sample's stash and base corner.  The partials
 // of grad_loc / grad_attn of a lane's x-row are summed over the unit's 8 lanes.
 template <typename T, int CPL, bool kPairs>
-__global__ __launch_bounds__(kBlock) OPS3D_FDA_QUERY_ATTR void fda_bwd_query_pair_kernel(const Args a) {
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kQueryWavesPerEU))) void fda_bwd_query_pair_kernel(const Args a) {
   extern __shared__ float lds[];
   constexpr int UL = 8;
   constexpr int UPW = kWave / UL, UPB = kWavesPerBlock * UPW;
@@ -707,7 +672,7 @@ __device__ __forceinline__ uint32_t block_exclusive_scan_tile(uint32_t x, uint32
 // 512-thread blocks or one 1024-thread block on a CU (3, 4, 4 waves per SIMD); compiling for no
 // more than that leaves the register allocator all the registers those waves can have.
 __host__ __device__ constexpr int tile_wpe(int lpu) {
-  return OPS3D_FDA_TILE_WPE > 0 ? OPS3D_FDA_TILE_WPE : (tile_threads(lpu) == 256 ? 3 : 4);
+  return tile_threads(lpu) == 256 ? 3 : 4;
 }
 
 template <typename T, int CPL, int LPU>
@@ -749,10 +714,12 @@ void fda_bwd_tile_kernel(const Args a) {
       t += lvt[u].count;
     }
     lvbase[L] = t;
-    // work counter or static order: from the first head's entries per tile (same in every block)
+    // tile order: a per-XCD work counter after four static tiles when the tiles hold at least a
+    // chunk of entries on average, else the static snake order, whose blocks pay no claim per
+    // tiny tile (from the first head's entries per tile: the same in every block)
     const uint32_t last = t > 0 ? t - 1 : 0;
     const uint32_t ent = t > 0 ? a.tile_start[last] + a.tile_counts[last] - a.tile_start[0] : 0u;
-    queue_l = OPS3D_FDA_TILE_QUEUE && (uint64_t)ent >= (uint64_t)a.chunk * t;
+    queue_l = (uint64_t)ent >= (uint64_t)a.chunk * t;
   }
   __syncthreads();
   const uint32_t T_h = lvbase[L];
@@ -772,7 +739,7 @@ void fda_bwd_tile_kernel(const Args a) {
   const uint32_t ngroups = a.tile_affinity ? 8u : 1u;
   uint32_t F = 1;
   if (a.split_slots > 0 && total > 0 && total < 2u * (uint32_t)nbx) {
-    F = min((OPS3D_FDA_SPLIT_TARGET * (uint32_t)nbx + total - 1u) / total, (uint32_t)OPS3D_FDA_SPLIT_MAX);
+    F = min((kSplitTarget * (uint32_t)nbx + total - 1u) / total, kSplitMax);
     F = min(F, a.split_slots / ngroups / total);
     if (F < 1) F = 1;
   }
@@ -791,17 +758,6 @@ void fda_bwd_tile_kernel(const Args a) {
   const T *go = static_cast<const T *>(a.gout_hm ? a.gout_hm : a.grad_out);
   const bool go_direct = a.gout_hm == nullptr;
 
-#if OPS3D_FDA_TILE_TIMING
-  unsigned long long t_acc[6] = {0, 0, 0, 0, 0, 0}, t_prev = clock64();
-#define TILE_MARK(i)                                        \
-  do {                                                      \
-    const unsigned long long t_now = clock64();             \
-    t_acc[i] += t_now - t_prev;                             \
-    t_prev = t_now;                                         \
-  } while (0)
-#else
-#define TILE_MARK(i) ((void)0)
-#endif
   // k -> (level, head, tile), coarse (last) levels first
   const auto decode = [&](uint32_t k, int &l, uint32_t &bgi, uint32_t &t) {
     uint32_t rem = k;
@@ -935,7 +891,6 @@ void fda_bwd_tile_kernel(const Args a) {
       const uint32_t nn = nxt_here ? min((uint32_t)CH, e1 - nc0) : min((uint32_t)CH, nc);
       const bool npf = nxt_here || (k1 < njobs && nc > 0);
       // (the bin counters are zero here: cleared at the start and after every owner phase)
-      TILE_MARK(0);
       // 1a. local bin of each entry's base corner, grad_output row index, bin counts.  The stash
       // holds the pixel coordinates: base corner = floor, fraction = coordinate - floor (exact).
       const int ox = itx * tx - 1, oy = ity * ty - 1, oz = itz * tz - 1;   // bin 0 = local -1
@@ -962,7 +917,6 @@ void fda_bwd_tile_kernel(const Args a) {
           pE[e] = a.entries[nc0 + ((uint32_t)(tid + e * NT) < nn ? (uint32_t)(tid + e * NT) : 0u)];
       }
       __syncthreads();
-      TILE_MARK(1);
       // 2. bin starts: thread tid scans bins [tid*per, (tid+1)*per)
       {
         const int per = (nb + NT - 1) / NT;
@@ -981,7 +935,6 @@ void fda_bwd_tile_kernel(const Args a) {
         if (tid == NT - 1) start_l[nb] = (uint32_t)n;
       }
       __syncthreads();
-      TILE_MARK(2);
       // 3. counting sort by bin: each entry's stash and row index go to its sorted position
 #pragma unroll
       for (int e = 0; e < KPT; ++e)
@@ -1015,7 +968,6 @@ void fda_bwd_tile_kernel(const Args a) {
         __builtin_amdgcn_s_waitcnt(0);   // the pieces are in LDS before the barrier below
       }
       __syncthreads();
-      TILE_MARK(3);
       // 4. owners gather from LDS
       if (live) {
 #pragma unroll
@@ -1025,7 +977,7 @@ void fda_bwd_tile_kernel(const Args a) {
           const int rb = ((pz - dz + 1) * TYp + (py - dy + 1)) * TXp + 2 * px;
           const uint32_t s0 = start_l[rb], m1 = start_l[rb + 1], m2 = start_l[rb + 2];
           const uint32_t s3 = two ? start_l[rb + 3] : m2;
-#pragma unroll OPS3D_FDA_TILE_UNROLL
+#pragma unroll 2
           for (uint32_t i = s0; i < s3; ++i) {
             const float4 st = st_l[i];
             uint32_t wv[NW];
@@ -1061,7 +1013,6 @@ void fda_bwd_tile_kernel(const Args a) {
         hdr_l[(pos + 2u) & 3u][1] = hc;
       }
       __syncthreads();
-      TILE_MARK(4);
     }
     if (F > 1) {
       // this part's sums go to its scratch slot (voxels of the nominal tile: pair p, x-half h);
@@ -1094,7 +1045,6 @@ void fda_bwd_tile_kernel(const Args a) {
         }
       }
     }
-    TILE_MARK(5);
     if (e0 == e1) {   // no chunk: publish the claim here
       if (tid == 0) {
         grab_l[pos & 3u] = claimed ? taken : ~0u;
@@ -1128,11 +1078,6 @@ void fda_bwd_tile_kernel(const Args a) {
     k = k1; k1 = k2; k2 = k3;
     ++pos;
   }
-#if OPS3D_FDA_TILE_TIMING
-  if (tid == 0 && a.dbg)
-    for (int i = 0; i < 6; ++i) atomicAdd(a.dbg + i, t_acc[i]);
-#endif
-#undef TILE_MARK
 }
 
 // Split tiles (see the tile kernel): one block per tile of every group adds the F parts'
@@ -1237,25 +1182,6 @@ hipError_t launch_one(int which, const Args &a, unsigned grid, size_t lds, hipSt
     // one block per tile of every group (`grid` = the bound on tiles times the groups)
     constexpr int TL = tile_lanes(LPU, CPL * (int)sizeof(T)), TC = CPL * LPU / TL;
     hipLaunchKernelGGL((fda_bwd_split_combine_kernel<T, TC, TL>), dim3(grid), dim3(tile_threads(TL)), 0, st, a);
-  }
-  else if (which >= 5 && which <= 8) {
-    // tile-major backward: 5 setup, 6 tile, 7 combine, 8 finish
-    if constexpr (sizeof(T) == 2 && CPL == 8 && LPU == 4) {
-      if (which == 5) {
-        hipLaunchKernelGGL((fda_bwd_setup_kernel<T>), dim3(grid), dim3(kBlock), lds, st, a);
-      } else if (which == 6) {
-        if (a.accumulate)
-          hipLaunchKernelGGL((fda_bwd_fused_tile_kernel<T, true>), dim3(grid), dim3(kFusedThreads), lds, st, a);
-        else
-          hipLaunchKernelGGL((fda_bwd_fused_tile_kernel<T, false>), dim3(grid), dim3(kFusedThreads), lds, st, a);
-      } else if (which == 7) {
-        hipLaunchKernelGGL((fda_bwd_fused_combine_kernel<T>), dim3(grid), dim3(256), 0, st, a);
-      } else {
-        hipLaunchKernelGGL((fda_bwd_finish_kernel<T>), dim3(grid), dim3(kBlock), lds, st, a);
-      }
-    } else {
-      return hipErrorInvalidValue;
-    }
   }
   else {
     // persistent: `grid` (the CU count, a multiple of 8 with XCD affinity) times the blocks that

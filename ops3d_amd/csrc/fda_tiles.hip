@@ -27,7 +27,6 @@
 // reservations) decides the order of the tile kernel's fp32 sums, so grad_value can differ
 // between runs at the rounding level.
 #include "fda_device.h"
-#include "fda_fused.h"
 
 namespace ops3d_fda {
 
@@ -54,43 +53,7 @@ struct BucketArgs {
   uint32_t *entries;           // [<= 8N] sample indices
   uint32_t *queue;             // [8] the tile kernel's work counters, cleared here
   int fused;                   // one block per head: tile_scatter<.., true> counts and scans itself
-  const uint4 *srec;           // [N] per-sample records of the tile-major backward (fda_fused.h), or
-                               // nullptr: keys / words
-  uint32_t *part;              // [BG][bph + 2] partition of each head's entries for the tile kernel
-                               // (fda_fused.h), or nullptr
-  int bph;                     // tile-kernel blocks per head
 };
-
-// Home tile and bucketing word of sample s.
-__device__ __forceinline__ void load_key_word(const BucketArgs &a, uint32_t s, uint32_t &key, uint32_t &word) {
-  if (a.srec) {
-    const uint2 v = reinterpret_cast<const uint2 *>(a.srec)[2 * (size_t)s];
-    key = v.x;
-    word = fused_word_expand(v.y & 0xffffu);
-  } else {
-    key = a.keys[s];
-    word = a.words[s];
-  }
-}
-
-// Partition of head bg's entries [hbase, hbase + E) into bph equal ranges, bound j = hbase +
-// floor(j E / bph): part[j] = the first tile whose start is at least bound j (j = 0 .. bph),
-// part[bph + 1] = E.  `st` holds the head's tile starts (LDS or global, ascending).
-__device__ __forceinline__ void write_partition(const BucketArgs &a, uint32_t bg, uint32_t hbase, uint32_t E,
-                                                const uint32_t *st, uint32_t T_h) {
-  uint32_t *part = a.part + (size_t)bg * (a.bph + 2);
-  for (int j = threadIdx.x; j <= a.bph; j += blockDim.x) {
-    const uint32_t bnd = hbase + (uint32_t)((uint64_t)j * E / (uint32_t)a.bph);
-    uint32_t lo = 0, hi = T_h;
-    while (lo < hi) {
-      const uint32_t mid = (lo + hi) >> 1;
-      if (st[mid] >= bnd) hi = mid;
-      else lo = mid + 1;
-    }
-    part[j] = lo;
-  }
-  if (threadIdx.x == 0) part[a.bph + 1] = E;
-}
 
 __device__ __forceinline__ bool matrix_mode(const BucketArgs &a, uint32_t T_h) {
   return T_h <= a.wcap;
@@ -176,9 +139,8 @@ __global__ __launch_bounds__(kBucketThreads) void tile_count_kernel(const Bucket
 #pragma unroll
       for (int i = 0; i < kCountBatch; ++i) {
         const uint32_t s = sb + (uint32_t)i * kBucketThreads;
-        key[i] = kKeyInvalid;
-        word[i] = 0u;
-        if (s < s1) load_key_word(a, s, key[i], word[i]);
+        key[i] = s < s1 ? a.keys[s] : kKeyInvalid;
+        word[i] = s < s1 ? a.words[s] : 0u;
       }
 #pragma unroll
       for (int i = 0; i < kCountBatch; ++i) {
@@ -292,26 +254,21 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
     if (blockIdx.x == 0 && tid < 8) a.queue[tid] = 0u;
     const bool mat = matrix_mode(a, T_h);
     for (uint32_t s = s0 + tid; s < s1; s += kBucketThreads) {
-      uint32_t key, word;
-      load_key_word(a, s, key, word);
+      const uint32_t key = a.keys[s];
       if (key == kKeyInvalid) continue;
-      for_each_entry(key, word, lg, [&](uint32_t id, uint32_t) {
+      for_each_entry(key, a.words[s], lg, [&](uint32_t id, uint32_t) {
         if (mat) atomicAdd(&cur[id - w0], 1u);
         else atomicAdd(&a.counts[id], 1u);   // zeroed by the query kernel
       });
     }
     if (mat) {
       __syncthreads();
-      const uint32_t E = block_scan(cur, nw, per, scan_tmp, [&](uint32_t i, uint32_t ex) {
+      block_scan(cur, nw, per, scan_tmp, [&](uint32_t i, uint32_t ex) {
         a.counts[w0 + i] = cur[i];
         a.start[w0 + i] = hbase + ex;
         win[i] = hbase + ex;
         cur[i] = 0u;
       });
-      if (a.part) {
-        __syncthreads();
-        write_partition(a, bg, hbase, E, win, T_h);
-      }
     } else {
       // the counters were added to in L2: wait for this wave's atomics, then read them past L1
       __builtin_amdgcn_s_waitcnt(0);
@@ -344,11 +301,6 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
       // the cursors are reserved below with atomics: let the stores land first
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
-      if (a.part) {
-        __threadfence_block();
-        write_partition(a, bg, hbase, carry - hbase, a.start + w0, T_h);
-        __syncthreads();
-      }
     }
   }
   if (kFused && matrix_mode(a, T_h)) {
@@ -360,23 +312,18 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
     const uint32_t *row = a.mat + (size_t)block_slot(a, hb, hc) * T_h;
     for (uint32_t i = tid; i < T_h; i += kBucketThreads) cur[i] = a.counts[w0 + i];
     __syncthreads();
-    const uint32_t E = block_scan(cur, nw, per, scan_tmp, [&](uint32_t i, uint32_t ex) {
+    block_scan(cur, nw, per, scan_tmp, [&](uint32_t i, uint32_t ex) {
       win[i] = hbase + ex + row[i];
       if (hc == 0) a.start[w0 + i] = hbase + ex;
       cur[i] = 0u;
     });
-    if (a.part && hc == 0) {   // block 0 of the head: row[] is 0, win[] holds the tile starts
-      __syncthreads();
-      write_partition(a, bg, hbase, E, win, T_h);
-    }
   } else {
     // counts of the window's tiles, then one reservation per touched tile
 #pragma unroll 4
     for (uint32_t s = s0 + tid; s < s1; s += kBucketThreads) {
-      uint32_t key, word;
-      load_key_word(a, s, key, word);
+      const uint32_t key = a.keys[s];
       if (key == kKeyInvalid) continue;
-      for_each_entry(key, word, lg, [&](uint32_t id, uint32_t) {
+      for_each_entry(key, a.words[s], lg, [&](uint32_t id, uint32_t) {
         if (id - w0 < nw) atomicAdd(&win[id - w0], 1u);
       });
     }
@@ -392,9 +339,8 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
 #pragma unroll
     for (int k = 0; k < SPT; ++k) {
       const uint32_t s = r0 + (uint32_t)(k * kBucketThreads + tid);
-      key[k] = kKeyInvalid;
-      word[k] = 0u;
-      if (s < s1) load_key_word(a, s, key[k], word[k]);
+      key[k] = s < s1 ? a.keys[s] : kKeyInvalid;
+      word[k] = s < s1 ? a.words[s] : 0u;
     }
     // (a) the round's entries per tile; tiles outside the window take a position at once
     const auto count_round = [&](auto all_in) {
@@ -526,11 +472,6 @@ __global__ __launch_bounds__(kScanThreads) void tile_headscan_kernel(const Bucke
     }
     carry += all;
   }
-  if (a.part) {   // the starts this block wrote: visible to it after the fence and barrier
-    __threadfence_block();
-    __syncthreads();
-    write_partition(a, bg, hbase, carry - hbase, a.start + bg * T_h, T_h);
-  }
 }
 
 // LDS histogram window (tiles) of the bucketing kernels for a workspace matrix of tcap tiles; a
@@ -541,14 +482,12 @@ uint32_t tile_window(uint32_t tcap) { return tcap < (uint32_t)kWin ? (tcap > 0 ?
 // to tcap tiles.
 size_t tile_matrix_words(uint32_t BG, uint32_t tcap) { return (size_t)BG * kBlocksPerHead * tcap; }
 
-hipError_t launch_tile_bucketing(const uint32_t *keys, const uint32_t *words, const void *srec, uint32_t n,
-                                 uint32_t per_head, const int64_t *shapes, int L, int BG, int TX, int TY, int TZ,
-                                 uint32_t *counts, uint32_t *start, uint32_t *cursor, uint32_t *mat, uint32_t tcap,
-                                 uint32_t *entries, uint32_t *queue, uint32_t *part, int bph, bool counts_cleared,
-                                 hipStream_t st, void (*mark)(int, hipStream_t)) {
+hipError_t launch_tile_bucketing(const uint32_t *keys, const uint32_t *words, uint32_t n, uint32_t per_head,
+                                 const int64_t *shapes, int L, int BG, int TX, int TY, int TZ, uint32_t *counts,
+                                 uint32_t *start, uint32_t *cursor, uint32_t *mat, uint32_t tcap, uint32_t *entries, uint32_t *queue,
+                                 bool counts_cleared, hipStream_t st, void (*mark)(int, hipStream_t)) {
   BucketArgs a{};
   a.keys = keys; a.words = words; a.n = n; a.per_head = per_head; a.shapes = shapes;
-  a.srec = static_cast<const uint4 *>(srec); a.part = part; a.bph = bph;
   a.L = L; a.BG = BG; a.TX = TX; a.TY = TY; a.TZ = TZ;
   a.counts = counts; a.cursor = cursor; a.start = start; a.mat = mat; a.tcap = tcap; a.entries = entries; a.queue = queue;
   // LDS sized to what the matrix can hold (tiles past the window take the global-atomic path),

@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_support_table(lib):
-    assert lib.ops3d_fda_abi_version() == 4
+    assert lib.ops3d_fda_abi_version() == 5
     F32, F16, BF16 = 0, 1, 2
     for d in (8, 16, 24, 32, 48, 64, 96, 128, 192, 256):
         assert lib.ops3d_fda_supported(BF16, d) == 1, d
@@ -51,13 +51,25 @@ def test_abi_version_and_support_table(lib):
 
 
 def test_forward_workspace_bytes(lib):
+    c4 = (1, 73728, 8, 32, 2, 73728, 4)   # B, S, G, D, L, Q, K
+
+    def fw(dtype, B, S, G, D, L, Q, K):
+        return lib.ops3d_fda_forward_workspace_bytes(dtype, B, S, G, D, L, Q, K)
+
     # 64-byte rows: head slices of 2*S + 10 rows (room for levels stored as x-pair lines)
-    assert lib.ops3d_fda_forward_workspace_bytes(2, 1, 73728, 8, 32) == 8 * (2 * 73728 + 10) * 32 * 2
+    assert fw(2, *c4) == 8 * (2 * 73728 + 10) * 32 * 2
     # other row sizes: S rows
-    assert lib.ops3d_fda_forward_workspace_bytes(2, 1, 73728, 8, 64) == 73728 * 8 * 64 * 2
-    assert lib.ops3d_fda_forward_workspace_bytes(0, 1, 73728, 8, 32) == 73728 * 8 * 32 * 4
-    assert lib.ops3d_fda_forward_workspace_bytes(2, 1, 73728, 1, 32) == 0  # G == 1: already head-major
-    assert lib.ops3d_fda_forward_workspace_bytes(7, 1, 73728, 8, 32) == 0
+    assert fw(2, 1, 73728, 8, 64, 2, 73728, 4) == 73728 * 8 * 64 * 2
+    assert fw(0, *c4) == 73728 * 8 * 32 * 4
+    assert fw(2, 1, 73728, 1, 32, 2, 73728, 4) == 0   # G == 1: already head-major
+    assert fw(7, *c4) == 0
+    # no copy, so no workspace: value under 8 MiB per batch item (c1, c2) ...
+    assert fw(0, 1, 576, 8, 32, 2, 576, 4) == 0       # c1 (fp32)
+    assert fw(2, 1, 4608, 8, 32, 2, 4608, 4) == 0     # c2
+    # ... or fewer corner reads than a head has rows (cross-attention with few queries)
+    assert fw(2, 1, 73728, 8, 32, 2, 1000, 4) == 0
+    assert fw(2, 1, 73728, 8, 32, 2, 1152, 4) > 0     # Q*L*K*8 == S
+    assert fw(2, 1, 73728, 8, 32, 2, 0, 4) == 0
 
 
 def test_workspace_bytes(lib):
@@ -71,25 +83,26 @@ def test_workspace_bytes(lib):
     # counters, the split scratch, the bucketing matrix (64 blocks x S/16+64 tiles per head),
     # head-major copies of value and grad_output; no split scratch at c4 (at least
     # B*G*S/128 = 4608 tiles)
-    def want(B, S, G, D, L, Q, K, split_slots):
+    def want(B, S, G, D, L, Q, K, split_slots, value_copy=True):
         n = B * Q * G * L * K
         return (2 * al(4 * n) + al(16 * n) + al(32 * n) + 3 * al(4 * (B * G * S + 1)) + 256
                 + al(split_slots * 128 * D * 4)
-                + al(4 * B * G * 64 * (S // 16 + 64)) + al(B * G * (2 * S + 10) * D * 2) + (al(B * Q * G * D * 2) if B * Q * G * D * 2 > 64 << 20 else 0))
+                + al(4 * B * G * 64 * (S // 16 + 64)) + (al(B * G * (2 * S + 10) * D * 2) if value_copy else 0) + (al(B * Q * G * D * 2) if B * Q * G * D * 2 > 64 << 20 else 0))
     assert lib.ops3d_fda_backward_workspace_bytes(2, B, S, G, D, L, Q, K) == want(B, S, G, D, L, Q, K, 0)
     assert lib.ops3d_fda_backward_workspace_bytes(9, B, S, G, D, L, Q, K) == 0
     # c5: grad_output (306 MB) gets its head-major copy
     c5 = (1, 598016, 8, 32, 3, 598016, 4)
     assert lib.ops3d_fda_backward_workspace_bytes(2, *c5) == want(*c5, 0)
-    # c2: at least 8 * 4608/128 = 288 tiles (< 2048): 4096 scratch tiles for split tiles
+    # c2: at least 8 * 4608/128 = 288 tiles (< 2048): 4096 scratch tiles for split tiles; value
+    # (2.4 MB) under 8 MiB: no head-major copy
     c2 = (1, 4608, 8, 32, 2, 4608, 4)
-    assert lib.ops3d_fda_backward_workspace_bytes(2, *c2) == want(*c2, 4096)
+    assert lib.ops3d_fda_backward_workspace_bytes(2, *c2) == want(*c2, 4096, value_copy=False)
 
 
-def _fwd(lib, **kw):
+def _fwd(lib, ptr=None, ws=None, ws_bytes=0, **kw):
     a = dict(dtype=2, B=1, S=576, G=8, D=32, L=2, Q=576, K=4, step=64)
     a.update(kw)
-    return lib.ops3d_fda_forward(None, None, None, None, None, None, 0, a["dtype"], a["B"], a["S"], a["G"],
+    return lib.ops3d_fda_forward(ptr, ptr, ptr, ptr, ptr, ws, ws_bytes, a["dtype"], a["B"], a["S"], a["G"],
                                  a["D"], a["L"], a["Q"], a["K"], a["step"], None)
 
 
@@ -106,6 +119,14 @@ def test_argument_errors_before_device_work(lib):
     assert _fwd(lib) == 1 and b"NULL" in lib.ops3d_fda_last_error()
     # nothing to do: B*Q == 0 succeeds without touching any pointer
     assert _fwd(lib, Q=0) == 0
+
+
+def test_forward_workspace_too_small(lib):
+    p = ctypes.c_void_p(256)
+    c4 = dict(S=73728, Q=73728)
+    need = lib.ops3d_fda_forward_workspace_bytes(2, 1, 73728, 8, 32, 2, 73728, 4)
+    # a non-NULL workspace smaller than the forward needs is refused before any device work
+    assert _fwd(lib, p, p, need - 256, **c4) == 1 and b"workspace too small" in lib.ops3d_fda_last_error()
 
 
 def test_backward_workspace_check(lib):
