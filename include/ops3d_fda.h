@@ -92,7 +92,7 @@ OPS3D_FDA_API int ops3d_fda_forward(const void *value, const int64_t *spatial_sh
  * Bytes of device workspace ops3d_fda_backward / ops3d_fda_backward_accumulate_f32 need (0 on
  * invalid sizes): per sample (N = B*Q*G*L*K) its home tile, tile-local corner word and a 16-byte
  * stash, up to 8 four-byte tile entries; per tile (<= B*G*S) a count, a start and a cursor; 8
- * work counters; for small volumes (B*G*ceil(S/128) < 2048) fp32 partial sums of 4096 split
+ * work counters; for small volumes (B*G*ceil(S/128) < 2048) fp32 partial sums of 2048 split
  * tiles; the bucketing matrix (B*G x 64 x (S/16 + 64) words); and head-major copies of value
  * (G > 1) and of grad_output (G > 1 and grad_output larger than 64 MiB; smaller ones are read in
  * place).  The pointer passed must be 256-byte aligned.

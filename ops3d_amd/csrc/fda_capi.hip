@@ -178,7 +178,7 @@ hipError_t launch(int dtype, int which, const Geometry &g, hipStream_t st) {
 //                    kernel's split tiles; else nothing
 //   head-major copies of value (G > 1; head slices of at most head_copy_rows_max(S) rows,
 //   large levels paired) and of grad_output (grad_out_copied)
-constexpr uint64_t kSplitTiles = 2048, kSplitSlots = 4096;
+constexpr uint64_t kSplitTiles = 2048, kSplitSlots = 2048;
 constexpr size_t kDirectGradOutBytes = (size_t)64 << 20;
 
 // Whether the head-major copy of value pays.  It keeps one head's rows together so that the XCD

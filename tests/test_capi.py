@@ -93,10 +93,10 @@ def test_workspace_bytes(lib):
     # c5: grad_output (306 MB) gets its head-major copy
     c5 = (1, 598016, 8, 32, 3, 598016, 4)
     assert lib.ops3d_fda_backward_workspace_bytes(2, *c5) == want(*c5, 0)
-    # c2: at least 8 * 4608/128 = 288 tiles (< 2048): 4096 scratch tiles for split tiles; value
+    # c2: at least 8 * 4608/128 = 288 tiles (< 2048): 2048 scratch tiles for split tiles; value
     # (2.4 MB) under 8 MiB: no head-major copy
     c2 = (1, 4608, 8, 32, 2, 4608, 4)
-    assert lib.ops3d_fda_backward_workspace_bytes(2, *c2) == want(*c2, 4096, value_copy=False)
+    assert lib.ops3d_fda_backward_workspace_bytes(2, *c2) == want(*c2, 2048, value_copy=False)
 
 
 def _fwd(lib, ptr=None, ws=None, ws_bytes=0, **kw):
