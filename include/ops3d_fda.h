@@ -157,6 +157,26 @@ OPS3D_FDA_API int ops3d_fda_backward_accumulate_f32(
     int im2col_step, void *stream);
 
 /*
+ * Allocation-free backward.  Same as ops3d_fda_backward, with no workspace argument: the
+ * workspace is a static device array of OPS3D_FDA_NOALLOC_SCRATCH_BYTES (64 MiB) inside the
+ * library, which every device it runs on holds until the process ends.  Problems whose
+ * ops3d_fda_backward_workspace_bytes() exceed that size are refused (OPS3D_FDA_EINVAL).  The call
+ * allocates nothing (no hipMalloc, hipFree or allocating library routine); its first call on a
+ * device resolves that device's array address.  Every call on a device shares that device's
+ * array: calls that overlap on one device (different streams or host threads) race and must be
+ * serialised by the caller.  No counterpart in the reference; for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).
+ */
+#define OPS3D_FDA_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+OPS3D_FDA_API int ops3d_fda_backward_noalloc(const void *value, const int64_t *spatial_shapes,
+                       const int64_t *level_start_index, const void *sampling_loc_attn,
+                       const void *grad_output, void *grad_value,
+                       void *grad_sampling_loc_attn, int dtype, int batch, int spatial_size,
+                       int num_heads, int channels, int num_levels, int num_query, int num_point,
+                       int im2col_step, void *stream);
+
+/*
  * Phase timing (no counterpart in the reference; for benchmarks and profilers).  After
  * ops3d_fda_profile_enable(1), every call records HIP events on its stream around its phases.
  * ops3d_fda_profile_read(which, ms, n) waits for the last call of that kind to finish and writes

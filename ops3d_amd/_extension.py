@@ -37,6 +37,7 @@ EXPORTED_SYMBOLS = (
     "ops3d_fda_backward",
     "ops3d_fda_backward_ex",
     "ops3d_fda_backward_accumulate_f32",
+    "ops3d_fda_backward_noalloc",
     "ops3d_fda_profile_enable",
     "ops3d_fda_profile_read",
 )
@@ -65,6 +66,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ops3d_fda_profile_read.argtypes = [_i, ctypes.POINTER(ctypes.c_float), _i]
     lib.ops3d_fda_backward_accumulate_f32.restype = _i
     lib.ops3d_fda_backward_accumulate_f32.argtypes = [_vp] * 8 + [_sz] + [_i] * 9 + [_vp]
+    lib.ops3d_fda_backward_noalloc.restype = _i
+    lib.ops3d_fda_backward_noalloc.argtypes = [_vp] * 7 + [_i] * 9 + [_vp]
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -238,6 +241,32 @@ class _NativeFDA:
         if rc != OPS3D_FDA_OK:
             self._raise(rc, "flash_deform_attn_backward_accumulate failed")
         return grad_sla
+
+    def flash_deform_attn_backward_noalloc(
+        self, value, spatial_shapes, level_start_index, sampling_loc_attn, grad_output, im2col_step, K,
+    ):
+        """Backward through the allocation-free entry point (the library's static device scratch,
+        at most 64 MiB of workspace; calls overlapping on one device race).  The output tensors
+        are allocated here by torch; a caller that cannot allocate calls
+        ops3d_fda_backward_noalloc with its own output buffers."""
+        B, S, G, D, L, Q = self._common(
+            value, spatial_shapes, level_start_index, sampling_loc_attn, K, {"grad_output": grad_output}
+        )
+        if grad_output.numel() != B * Q * G * D:
+            raise ValueError(f"grad_output must have B*Q*G*D = {B * Q * G * D} elements, got {grad_output.numel()}")
+        code = _DTYPE_CODE[value.dtype]
+        grad_value = torch.empty_like(value)
+        grad_sla = torch.empty_like(sampling_loc_attn)
+        stream = torch.cuda.current_stream(value.device).cuda_stream
+        with torch.cuda.device(value.device):
+            rc = self._lib.ops3d_fda_backward_noalloc(
+                _ptr(value), _ptr(spatial_shapes), _ptr(level_start_index), _ptr(sampling_loc_attn),
+                _ptr(grad_output), _ptr(grad_value), _ptr(grad_sla),
+                code, B, S, G, D, L, Q, int(K), int(im2col_step), stream,
+            )
+        if rc != OPS3D_FDA_OK:
+            self._raise(rc, "flash_deform_attn_backward_noalloc failed")
+        return [grad_value, grad_sla]
 
     def profile_enable(self, on: bool = True) -> None:
         """Record HIP events around the backward phases of every following call."""

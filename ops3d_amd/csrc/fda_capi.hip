@@ -18,6 +18,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <mutex>
 #include <string>
 
 #include "../../include/ops3d_fda.h"
@@ -347,6 +348,42 @@ hipError_t launch_head_major(const void *src, void *dst, int64_t B, int64_t N, i
 
 }  // namespace
 
+// Device scratch of ops3d_fda_backward_noalloc: the backward workspace for callers that cannot
+// allocate.  Each device holds its own copy for the life of the process; host code uses only the
+// per-device address hipGetSymbolAddress returns (the array's name is a host-side stand-in).
+static __device__ __align__(256) unsigned char scratch[OPS3D_FDA_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's scratch address (resolved once per device), or nullptr with the error set.
+void *scratch_address() {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    fail(OPS3D_FDA_ERUNTIME, "hipGetDevice failed: %s", hipGetErrorString(e));
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    fail(OPS3D_FDA_ERUNTIME, "device %d beyond the %d devices the scratch table holds", dev, kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      fail(OPS3D_FDA_ERUNTIME, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+}  // namespace
+
 extern "C" {
 
 int ops3d_fda_abi_version(void) { return 5; }
@@ -618,6 +655,31 @@ int ops3d_fda_backward_accumulate_f32(const void *value, const int64_t *spatial_
   return backward_impl(value, nullptr, spatial_shapes, level_start_index, sampling_loc_attn, grad_output,
                        grad_value_f32, true, grad_sampling_loc_attn, workspace, workspace_bytes, dtype, batch,
                        spatial_size, num_heads, channels, num_levels, num_query, num_point, im2col_step,
+                       static_cast<hipStream_t>(stream));
+}
+
+int ops3d_fda_backward_noalloc(const void *value, const int64_t *spatial_shapes,
+                               const int64_t *level_start_index, const void *sampling_loc_attn,
+                               const void *grad_output, void *grad_value, void *grad_sampling_loc_attn,
+                               int dtype, int batch, int spatial_size, int num_heads, int channels,
+                               int num_levels, int num_query, int num_point, int im2col_step, void *stream) {
+  g_last_error.clear();
+  Geometry geo;
+  int rc = common_checks(dtype, batch, spatial_size, num_heads, channels, num_levels, num_query, num_point,
+                         im2col_step, true, geo);
+  if (rc) return rc;
+  const size_t need = ops3d_fda_backward_workspace_bytes(dtype, batch, spatial_size, num_heads, channels,
+                                                         num_levels, num_query, num_point);
+  if (need > (size_t)OPS3D_FDA_NOALLOC_SCRATCH_BYTES)
+    return fail(OPS3D_FDA_EINVAL,
+                "problem too large for the allocation-free backward: needs %zu bytes of scratch, the "
+                "library holds %zu (use ops3d_fda_backward with a caller workspace)",
+                need, (size_t)OPS3D_FDA_NOALLOC_SCRATCH_BYTES);
+  void *ws = scratch_address();
+  if (!ws) return OPS3D_FDA_ERUNTIME;
+  return backward_impl(value, nullptr, spatial_shapes, level_start_index, sampling_loc_attn, grad_output,
+                       grad_value, false, grad_sampling_loc_attn, ws, (size_t)OPS3D_FDA_NOALLOC_SCRATCH_BYTES, dtype,
+                       batch, spatial_size, num_heads, channels, num_levels, num_query, num_point, im2col_step,
                        static_cast<hipStream_t>(stream));
 }
 

@@ -136,3 +136,13 @@ def test_backward_workspace_check(lib):
     # argument errors are still reported before anything else
     rc = lib.ops3d_fda_backward(p, p, p, p, p, p, p, None, 0, 2, 1, 576, 8, 32, 6, 576, 4, 64, None)
     assert rc == 1 and b"invalid number of scales" in lib.ops3d_fda_last_error()
+
+
+def test_noalloc_refuses_large_problems_before_device_work(lib):
+    p = ctypes.c_void_p(256)
+    # c4 needs 340 MiB of workspace; the static scratch holds 64 MiB
+    rc = lib.ops3d_fda_backward_noalloc(p, p, p, p, p, p, p, 2, 1, 73728, 8, 32, 2, 73728, 4, 64, None)
+    assert rc == 1 and b"too large for the allocation-free backward" in lib.ops3d_fda_last_error()
+    # argument errors first
+    rc = lib.ops3d_fda_backward_noalloc(p, p, p, p, p, p, p, 2, 1, 576, 8, 32, 6, 576, 4, 64, None)
+    assert rc == 1 and b"invalid number of scales" in lib.ops3d_fda_last_error()
