@@ -335,11 +335,15 @@ __device__ __forceinline__ void unit_softmax(float *logits, int n, int j) {
 
 // Pixel coordinate of a normalised location exactly as torch's grid_sample computes it for
 // align_corners=False on grid = 2*loc - 1:  ((grid + 1) * size - 1) / 2, each step rounded in
-// fp32 (no contraction), so the kernel samples at the same coordinate as the PyTorch path.
-// (Reference CUDA: loc * size - 0.5, flash_deform_im2col_cuda.cuh:268-270; equal up to 1 ulp.)
+// fp32, so the kernel samples at the same coordinate as the PyTorch path.  Contraction is off
+// here: hipcc's default would fuse the products and subtractions into FMAs (one rounding of
+// loc * size - 0.5), up to 1 ulp away from both torch and the reference CUDA's two roundings
+// (float loc * size, then - 0.5 in double rounded to float, flash_deform_im2col_cuda.cuh:268-270),
+// which costs the location gradients up to ~25 ulp of their terms near such a coordinate.
 __device__ __forceinline__ float pixel_coord(float loc, float size) {
-  const float grid = __fsub_rn(__fmul_rn(2.f, loc), 1.f);
-  return __fmul_rn(__fsub_rn(__fmul_rn(__fadd_rn(grid, 1.f), size), 1.f), 0.5f);
+#pragma clang fp contract(off)
+  const float grid = 2.f * loc - 1.f;
+  return ((grid + 1.f) * size - 1.f) * 0.5f;
 }
 
 // Per-sample trilinear set-up shared by forward and backward.

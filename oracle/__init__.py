@@ -108,30 +108,28 @@ def backward(value, shapes, loc_attn, grad_out, K, coord_mode=1, abs_mode=0):
 
 FP32_UNIT_ROUNDOFF = 2.0 ** -24
 
-
-def fp32_grad_value_allowance(value, shapes, loc_attn, grad_out, K):
-    """Per-element rounding allowance for fp32 grad_value: 4 * sqrt(n) * u * M, with M the sum
-    of |terms| of the element and n its number of terms (sample corners on that voxel) plus 3
-    (the rounded products attn * w * g).  Each element is a sum whose order the GPU's bucketing
-    leaves to run time (as the reference's atomic adds do), so no fixed relative bar holds for
-    elements whose terms cancel; this is the same random-walk bound as for the location
-    gradients (fp32_rounding_allowance)."""
-    m, _ = backward(value, shapes, loc_attn, grad_out, K, coord_mode=1, abs_mode=1)
-    n, _ = backward(value, shapes, loc_attn, grad_out, K, coord_mode=1, abs_mode=2)
-    return 4.0 * np.sqrt(n + 3.0) * FP32_UNIT_ROUNDOFF * m
+# Allowance factor of the fp32 location gradients, in units of sqrt(n) * u * M (below).  Sized
+# on the fp32 PyTorch path (torch_port: grid_sample + autograd) against this float64 oracle on
+# the benchmark inputs: it breaks the plain rtol 1e-5 / atol 1e-6 bar on up to 0.45 % of the
+# location gradients (by up to 81x), and needs at most 0.14 sqrt(n) u M beyond that bar; the
+# other outputs (forward, grad_value, logit gradients) stay inside the plain bar.
+FP32_LOC_ALLOWANCE_K = 0.15
 
 
-def fp32_rounding_allowance(value, shapes, loc_attn, grad_out, K):
-    """Per-element rounding allowance for fp32 gradients of sampling_loc_attn:
-    4 * sqrt(n) * u * M, with M the sum of |terms| of each element (backward(abs_mode=1)), u the
-    fp32 unit roundoff and n = 8*D + 2*L*K + 8 the number of rounded operations in one element
-    (8 corners x D channels, the softmax sums, the weight products).  The worst-case bound of an
-    n-term floating-point sum is n * u * M; rounding errors of independent operations add like
-    a random walk, so sqrt(n) * u * M is the typical size, and 4x that is the allowance (the
-    fp32 PyTorch path stays under 0.1 of it on the benchmark inputs)."""
+def fp32_loc_allowance(value, shapes, loc_attn, grad_out, K, k=FP32_LOC_ALLOWANCE_K):
+    """Per-element rounding allowance for fp32 gradients of sampling_loc_attn, shaped like it:
+    k * sqrt(n) * u * M on the 3*L*K location entries and 0 on the L*K logit entries.  M is the
+    sum of |terms| of the element (backward(abs_mode=1)), u the fp32 unit roundoff and
+    n = 8*D + 2*L*K + 8 the number of rounded operations in one element (8 corners x D channels,
+    the softmax sums, the weight products).  A location gradient sums the value differences of
+    corner pairs, which cancel: its magnitude can be far below M, so no fixed relative bar
+    holds for it in fp32 whatever the summation order; rounding errors of independent operations
+    add like a random walk, whose typical size is sqrt(n) * u * M."""
     value = np.asarray(value)
     D = value.shape[-1]
     L = len(shapes)
     _, m = backward(value, shapes, loc_attn, grad_out, K, coord_mode=1, abs_mode=1)
     n = 8 * D + 2 * L * K + 8
-    return 4.0 * np.sqrt(n) * FP32_UNIT_ROUNDOFF * m
+    allow = k * np.sqrt(n) * FP32_UNIT_ROUNDOFF * m
+    allow[..., 3 * L * K:] = 0.0
+    return allow
