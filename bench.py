@@ -9,8 +9,8 @@ grad N(0,1)), all resident in HBM before timing.
 A step is one forward + backward through FlashDeformAttnFunction (autograd), over one batch.
 W untimed warmup steps, then K timed steps bracketed by torch.cuda.synchronize(); HIP events
 on the launch stream give per-step times (median / p10 / p90) and, in separate loops, the
-average duration of each kernel launch (forward kernel; backward kernel via the
-accumulate-only entry point).
+average duration of each kernel launch (HIP events the library records between its launches,
+ops3d_fda_profile_*).
 
   value    = fwd+bwd algorithmic bytes / ms_per_step (GB/s).  Algorithmic bytes count each
              tensor once at its API dtype: fwd reads value + sampling_loc_attn and writes the
@@ -18,8 +18,11 @@ accumulate-only entry point).
              grad_sampling_loc_attn.
   roofline = the same figure for the dominant kernel alone, against 8 TB/s HBM3E peak.
   cpu_baseline = the PyTorch restatement of the reference's naive path (oracle/torch_port.py:
-             grid_sample + softmax + autograd) in fp32 on the host CPU, on a query slice,
-             scaled linearly to the full query count.
+             grid_sample + softmax + autograd) in fp32 on the host CPU, on all queries when
+             that fits the time target, else on a query slice scaled linearly to the full
+             query count (the sample field says which).
+  memory   = the library's forward / backward workspace sizes and torch's peak allocation of
+             a step above the resident inputs.
 
 --all prints a per-configuration table (c1..c5, plus fp16 and fp32 forward at c5) to stderr.
 """
@@ -49,6 +52,21 @@ def pct(xs, p):
     k = (len(xs) - 1) * p / 100.0
     lo, hi = int(k), min(int(k) + 1, len(xs) - 1)
     return xs[lo] + (xs[hi] - xs[lo]) * (k - lo)
+
+
+def _rocprof_avg_us(kernel: str, workload: str):
+    """Average dispatch duration (us) of `kernel` in the committed rocprofv3 --stats summary
+    profiles/kernel_stats_<workload>_bf16.md (a cross-check of the event timing)."""
+    path = os.path.join(ROOT, "profiles", f"kernel_stats_{workload}_bf16.md")
+    if not os.path.exists(path):
+        return None
+    stem = kernel.replace("fda_bwd_query_kernel", "fda_bwd_query_pair_kernel").replace(
+        "fda_forward_kernel", "fda_forward_pair_kernel")
+    for line in open(path):
+        m = re.match(r"\|\s*`" + re.escape(stem) + r"[<`][^|]*\|\s*\d+\s*\|\s*([0-9.]+)", line)
+        if m:
+            return float(m.group(1))
+    return None
 
 
 def _traffic_from_profiles(kernel: str, workload: str):
@@ -93,6 +111,22 @@ class Bench:
 
         with self.torch.no_grad():
             FlashDeformAttnFunction.apply(self.value, self.st, self.lsi, self.sla, 64, self.w.K, True)
+
+    def memory(self, base, peak):
+        """Device memory of a fwd+bwd step: the library's workspaces (from its size queries)
+        and torch's peak allocation above the resident inputs (outputs, gradients, saved
+        forward workspace, backward workspace)."""
+        from ops3d_amd import _C
+
+        w = self.w
+        code = {self.torch.float32: 0, self.torch.float16: 1, self.torch.bfloat16: 2}[self.value.dtype]
+        args = (code, w.B, w.S, w.G, w.D, w.L, w.nq, w.K)
+        return {
+            "inputs_bytes": int(base),
+            "fwd_workspace_bytes": int(_C._lib.ops3d_fda_forward_workspace_bytes(*args)),
+            "bwd_workspace_bytes": int(_C._lib.ops3d_fda_backward_workspace_bytes(*args)),
+            "step_peak_above_inputs_bytes": int(peak - base),
+        }
 
     def time_loop(self, fn, steps, warmup):
         torch = self.torch
@@ -150,7 +184,13 @@ def measure(w, dtype, steps, warmup, device, with_kernels=True, fwd_only=False):
     res["bytes"] = by
     res["fwd"] = b.time_loop(b.fwd, steps, warmup)
     if not fwd_only:
+        import torch
+
+        torch.cuda.synchronize()
+        base = torch.cuda.memory_allocated()
+        torch.cuda.reset_peak_memory_stats()
         res["step"] = b.time_loop(b.step, steps, warmup)
+        res["memory"] = b.memory(base, torch.cuda.max_memory_allocated())
     if with_kernels:
         fk, bk = b.kernel_times(steps, warmup)
         res["fwd_kernel"], res["bwd_kernel"] = fk, bk
@@ -191,6 +231,7 @@ def cpu_baseline(w, target_s=4.0, reps=3):
         ts.append(time.perf_counter() - t0)
     t = statistics.median(ts)
     t_full = t * w.nq / nq
+    scaled = nq < w.nq
     by = w.algorithmic_bytes(2 if w.dtype in ("bf16", "fp16") else 4)["total"]
     cpu = "unknown"
     try:
@@ -200,15 +241,19 @@ def cpu_baseline(w, target_s=4.0, reps=3):
                 break
     except OSError:
         pass
+    if scaled:
+        what = (f"on {nq} of {w.nq} queries of {w.name}, median of {reps}, {t:.2f} s per rep, scaled "
+                f"linearly to the full query count ({t_full * 1e3:.0f} ms)")
+    else:
+        what = f"on all {w.nq} queries of {w.name}, median of {reps}, {t:.2f} s per rep"
     return {
         "value": round(by / t_full / 1e9, 4),
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
-        "sample": (f"oracle/torch_port fp32 fwd+bwd (grid_sample+softmax+autograd) on {nq} of {w.nq} "
-                   f"queries of {w.name}, median of {reps}, {t:.2f} s per rep, scaled linearly to the full "
-                   f"query count ({t_full * 1e3:.0f} ms extrapolated); CPU: {cpu}"),
-        "ms_extrapolated": round(t_full * 1e3, 1),
+        "sample": f"oracle/torch_port fp32 fwd+bwd (grid_sample+softmax+autograd) {what}; CPU: {cpu}",
+        "ms_full_workload": round(t_full * 1e3, 1),
+        "queries_timed": nq,
     }
 
 
@@ -234,6 +279,10 @@ def summary_line(r):
                      f"q {ph['query_kernel']['mean'] * 1e3:.1f} count {ph['tile_count']['mean'] * 1e3:.1f} "
                      f"scatter {ph['tile_scatter']['mean'] * 1e3:.1f} tile {ph['tile_kernel']['mean'] * 1e3:.1f}]")
     parts.append(f"{samples / (s or f) / 1e6:.3g} Gsamples/s" if (s or f) else "")
+    if "memory" in r:
+        m = r["memory"]
+        parts.append(f"ws fwd {m['fwd_workspace_bytes'] / 2**20:.0f} MiB bwd {m['bwd_workspace_bytes'] / 2**20:.0f} MiB, "
+                     f"step peak +{m['step_peak_above_inputs_bytes'] / 2**20:.0f} MiB")
     return " | ".join(parts)
 
 
@@ -325,6 +374,7 @@ def main():
     achieved = kbytes / (kms * 1e-3) / 1e9
     kf, kb = r["fwd_kernel"]["total"]["mean"], ph["total"]["mean"]
     traffic = _traffic_from_profiles(dominant, w.name)
+    rp_us = _rocprof_avg_us(dominant, w.name)
     line = {
         "metric": METRIC,
         "value": round(by["total"] / (ms_step * 1e-3) / 1e9, 2),
@@ -364,7 +414,13 @@ def main():
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "algorithmic_bytes": kbytes,
+            "duration_us": round(kms * 1e3, 2),
+            "duration_source": "HIP events the library records around the kernel on its launch stream, mean over the timed calls",
+            "rocprof_avg_us": rp_us,
+            "traffic_source": (f"profiles/pmc_{dominant}_{w.name}.md: rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE per "
+                               f"dispatch, scaled by the copy-kernel calibration" if traffic is not None else None),
         },
+        "memory": r["memory"],
         "cpu_baseline": None,
     }
     if not args.no_cpu:

@@ -1,4 +1,5 @@
-"""Build libops3d_fda.so (the gfx950 HIP kernels + C ABI) in-tree with hipcc.
+"""Build libops3d_fda.so (the gfx950 HIP kernels + C ABI) in-tree with hipcc, and the PyTorch
+extension module over it (g++ against torch's headers).
 
 gfx950 only, no hipify, no CUDA headers.  Sources are compiled in parallel, then linked with
 hipcc.  Used by ``setup.py`` and ``__graft_entry__.build()``; also runnable as
@@ -16,6 +17,7 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_NAME = "libops3d_fda.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
+TORCH_EXT_NAME = "_fda_torch"
 SOURCES = ["fda_capi.hip", "fda_tiles.hip", "fda_f32.hip", "fda_f16.hip", "fda_bf16.hip"]
 ARCH = "gfx950"
 
@@ -58,8 +60,32 @@ def _run(cmd: list[str]) -> None:
         sys.stderr.write(err + "\n")
 
 
+def _torch_ext_cmds(build_dir: str) -> tuple[list[str], list[str], str]:
+    """g++ compile and link commands of the PyTorch extension module (csrc/torch_ext.cpp: host
+    code over the C ABI, linked against libops3d_fda.so next to it)."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    obj = os.path.join(build_dir, "torch_ext.o")
+    out = os.path.join(PKG_DIR, TORCH_EXT_NAME + sysconfig.get_config_var("EXT_SUFFIX"))
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    inc = [f"-I{p}" for p in cpp_extension.include_paths()] + [
+        f"-I{sysconfig.get_paths()['include']}", "-I/opt/rocm/include"]
+    cc = ["g++", "-std=c++17", "-O2", "-fPIC", "-fvisibility=hidden", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+          f"-DTORCH_EXTENSION_NAME={TORCH_EXT_NAME}", "-DTORCH_API_INCLUDE_EXTENSION_H", "-DUSE_ROCM",
+          "-D__HIP_PLATFORM_AMD__=1", *inc, "-c", os.path.join(CSRC, "torch_ext.cpp"), "-o", obj]
+    libdirs = cpp_extension.library_paths()
+    link = ["g++", "-shared", obj, "-o", out + ".tmp", *[f"-L{d}" for d in libdirs], f"-L{PKG_DIR}",
+            "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python", "-lops3d_fda",
+            "-Wl,-rpath,$ORIGIN", *[f"-Wl,-rpath,{d}" for d in libdirs]]
+    return cc, link, out
+
+
 def build(out_path: str = LIB_PATH, build_dir: str | None = None) -> str:
-    """Compile every source for gfx950 and link ``libops3d_fda.so``; return its path."""
+    """Compile every source for gfx950 and link ``libops3d_fda.so``, then the PyTorch
+    extension module over it; return the library's path."""
     hipcc = _hipcc()
     build_dir = build_dir or os.path.join(PKG_DIR, "_build")
     os.makedirs(build_dir, exist_ok=True)
@@ -69,11 +95,16 @@ def build(out_path: str = LIB_PATH, build_dir: str | None = None) -> str:
         obj = os.path.join(build_dir, src.replace(".hip", ".o"))
         objs.append(obj)
         cmds.append([hipcc, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+    ext_cc, ext_link, ext_out = _torch_ext_cmds(build_dir)
+    cmds.append(ext_cc)
     with ThreadPoolExecutor(max_workers=min(len(cmds), os.cpu_count() or 1)) as ex:
         list(ex.map(_run, cmds))
     tmp = out_path + ".tmp"
     _run([hipcc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp])
     os.replace(tmp, out_path)
+    if out_path == LIB_PATH:
+        _run(ext_link)
+        os.replace(ext_out + ".tmp", ext_out)
     return out_path
 
 

@@ -79,12 +79,20 @@ class _NativeFDA:
 
     ABI_VERSION = 5
 
-    def __init__(self, lib: ctypes.CDLL, path: str):
+    def __init__(self, lib: ctypes.CDLL, path: str, ext=None):
         self._lib = lib
         self.__file__ = path
         ver = lib.ops3d_fda_abi_version()
         if ver != self.ABI_VERSION:
             raise ImportError(f"{path}: ABI version {ver}, expected {self.ABI_VERSION}")
+        # The PyTorch extension module (csrc/torch_ext.cpp) does the same checks and calls of
+        # the four tensor entry points in C++, for a fraction of the host time: when it is
+        # built, those methods are its functions.
+        self._ext = ext
+        if ext is not None:
+            for name in ("flash_deform_attn_forward", "flash_deform_attn_backward",
+                         "forward_keep_head_major", "backward_with_head_major"):
+                setattr(self, name, getattr(ext, name))
 
     # -- helpers ---------------------------------------------------------------------------
     def _raise(self, rc: int, what: str) -> None:
@@ -299,9 +307,27 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     return lib
 
 
-def _load():
+def _torch_ext(fresh_library: bool):
+    """The PyTorch extension module, or None when it is not built (or, after a rebuild, when an
+    earlier build of it is already loaded in this process: an extension module cannot be
+    unloaded, and it would keep the old library)."""
+    import sys
+
+    name = __package__ + "._fda_torch"
+    if fresh_library and name in sys.modules:
+        return None
     try:
-        return _NativeFDA(load_library(LIB_PATH), LIB_PATH)
+        import importlib
+
+        return importlib.import_module(name)
+    except ImportError:
+        return None
+
+
+def _load(fresh_library: bool = False):
+    try:
+        lib = load_library(LIB_PATH)
+        return _NativeFDA(lib, LIB_PATH, _torch_ext(fresh_library))
     except (OSError, ImportError, AttributeError):
         return None
 
@@ -322,7 +348,7 @@ def reload() -> None:
             _ctypes.dlclose(_HANDLES.pop())
         except OSError:
             pass
-    _C = _load()
+    _C = _load(fresh_library=True)
     import sys
 
     from . import flash_deform_attn as _fda

@@ -1,0 +1,176 @@
+// PyTorch extension module over the C ABI of libops3d_fda.so: the tensor-level entry points of
+// the reference's `_C` (csrc/vision.cpp:23-24 -> csrc/flash_deform_attn.h:7-52), plus the two
+// calls FlashDeformAttnFunction makes (forward keeping the head-major copy of value, backward
+// reusing it).  Host code only: argument checks, output allocation through torch's caching
+// allocator, torch's current HIP stream, then one C ABI call.  It exists for host overhead --
+// the same checks and calls through ctypes cost several times as much per call.
+//
+// Errors: a failed check or an OPS3D_FDA_EINVAL from the library raises ValueError
+// (std::invalid_argument, as the reference's), OPS3D_FDA_ERUNTIME raises RuntimeError.
+#include <torch/extension.h>
+
+// torch's ROCm build reports HIP devices as device type cuda: the guard and stream accessors
+// are the "masquerading" ones
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+
+#include <stdexcept>
+#include <string>
+#include <tuple>
+
+#include "../../include/ops3d_fda.h"
+
+namespace {
+
+int dtype_code(const at::Tensor &t) {
+  switch (t.scalar_type()) {
+    case at::kFloat: return OPS3D_FDA_F32;
+    case at::kHalf: return OPS3D_FDA_F16;
+    case at::kBFloat16: return OPS3D_FDA_BF16;
+    default: throw std::invalid_argument(std::string("unsupported value dtype ") + c10::toString(t.scalar_type()));
+  }
+}
+
+void check_tensor(const at::Tensor &t, const char *name, const at::Tensor &value) {
+  // reference csrc/flash_deform_attn.h:24,51 (CPU tensors are not implemented)
+  if (!t.is_cuda()) throw std::runtime_error(std::string("Not implemented on the CPU (") + name + " is on the CPU)");
+  if (!t.is_contiguous()) throw std::runtime_error(std::string(name) + " tensor has to be contiguous");
+  if (t.device() != value.device()) throw std::runtime_error(std::string(name) + " is on another device than value");
+}
+
+struct Sizes {
+  int code, B, S, G, D, L, Q, K;
+};
+
+// Shared checks of every entry point; returns the problem sizes.
+Sizes common(const at::Tensor &value, const at::Tensor &shapes, const at::Tensor &lsi, const at::Tensor &sla,
+             int64_t K) {
+  check_tensor(value, "value", value);
+  check_tensor(shapes, "spatial_shapes", value);
+  check_tensor(lsi, "level_start_index", value);
+  check_tensor(sla, "sampling_loc_attn", value);
+  Sizes z{};
+  z.code = dtype_code(value);
+  if (sla.scalar_type() != value.scalar_type())
+    throw std::invalid_argument("sampling_loc_attn dtype differs from value dtype");
+  if (shapes.scalar_type() != at::kLong || lsi.scalar_type() != at::kLong)
+    throw std::invalid_argument("spatial_shapes and level_start_index must be int64");
+  if (value.dim() != 4) throw std::invalid_argument("value must be [B, S, G, D]");
+  if (shapes.dim() != 2 || shapes.size(1) != 3) throw std::invalid_argument("spatial_shapes must be [L, 3]");
+  const int64_t L = shapes.size(0);
+  if (lsi.dim() != 1 || lsi.size(0) != L) throw std::invalid_argument("level_start_index must be [L]");
+  if (sla.dim() != 4 || sla.size(0) != value.size(0) || sla.size(2) != value.size(2))
+    throw std::invalid_argument("sampling_loc_attn must be [B, Q, G, P]");
+  if (sla.size(3) != L * K * 4)
+    throw std::invalid_argument("sampling_loc_attn last dimension (" + std::to_string(sla.size(3)) +
+                                ") does not match L=" + std::to_string(L) + ", K=" + std::to_string(K) +
+                                " (expected " + std::to_string(L * K * 4) + ")");
+  z.B = (int)value.size(0);
+  z.S = (int)value.size(1);
+  z.G = (int)value.size(2);
+  z.D = (int)value.size(3);
+  z.L = (int)L;
+  z.Q = (int)sla.size(1);
+  z.K = (int)K;
+  return z;
+}
+
+void raise(int rc, const char *what) {
+  const char *msg = ops3d_fda_last_error();
+  const std::string m = (msg && *msg) ? msg : what;
+  if (rc == OPS3D_FDA_EINVAL) throw std::invalid_argument(m);
+  throw std::runtime_error(m);
+}
+
+hipStream_t stream_of(const at::Tensor &value) {
+  return c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(value.device().index()).stream();
+}
+
+void *ptr(const at::Tensor &t) { return t.defined() && t.numel() > 0 ? t.data_ptr() : nullptr; }
+
+void check_grad_output(const at::Tensor &grad_output, const at::Tensor &value, const Sizes &z) {
+  check_tensor(grad_output, "grad_output", value);
+  if (grad_output.scalar_type() != value.scalar_type())
+    throw std::invalid_argument("grad_output dtype differs from value dtype");
+  if (grad_output.numel() != (int64_t)z.B * z.Q * z.G * z.D)
+    throw std::invalid_argument("grad_output must have B*Q*G*D elements");
+}
+
+// Forward; returns the output and the forward workspace (the head-major copy of value), which
+// is undefined (None) when the library makes no copy.
+std::tuple<at::Tensor, c10::optional<at::Tensor>> forward_keep_head_major(
+    const at::Tensor &value, const at::Tensor &shapes, const at::Tensor &lsi, const at::Tensor &sla,
+    int64_t im2col_step, int64_t K) {
+  const Sizes z = common(value, shapes, lsi, sla, K);
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(value.device());
+  at::Tensor out = at::empty({z.B, z.Q, (int64_t)z.G * z.D}, value.options());
+  const size_t n = ops3d_fda_forward_workspace_bytes(z.code, z.B, z.S, z.G, z.D, z.L, z.Q, z.K);
+  c10::optional<at::Tensor> ws;
+  if (n) ws = at::empty({(int64_t)n}, value.options().dtype(at::kByte));
+  const int rc = ops3d_fda_forward(ptr(value), shapes.data_ptr<int64_t>(), lsi.data_ptr<int64_t>(), ptr(sla),
+                                   ptr(out), ws ? ws->data_ptr() : nullptr, n, z.code, z.B, z.S, z.G, z.D, z.L, z.Q,
+                                   z.K, (int)im2col_step, stream_of(value));
+  if (rc != OPS3D_FDA_OK) raise(rc, "flash_deform_attn_forward failed");
+  return {out, ws};
+}
+
+// Backward; value_head_major: the forward workspace for this value, or None.
+std::vector<at::Tensor> backward_with_head_major(const at::Tensor &value,
+                                                 const c10::optional<at::Tensor> &value_head_major,
+                                                 const at::Tensor &shapes, const at::Tensor &lsi,
+                                                 const at::Tensor &sla, const at::Tensor &grad_output,
+                                                 int64_t im2col_step, int64_t K) {
+  const Sizes z = common(value, shapes, lsi, sla, K);
+  check_grad_output(grad_output, value, z);
+  const void *vhm = nullptr;
+  if (value_head_major && value_head_major->defined()) {
+    const at::Tensor &h = *value_head_major;
+    const size_t need = ops3d_fda_forward_workspace_bytes(z.code, z.B, z.S, z.G, z.D, z.L, z.Q, z.K);
+    if (h.device() != value.device() || h.scalar_type() != at::kByte || (size_t)h.numel() != need)
+      throw std::invalid_argument("value_head_major is not a forward workspace of this value");
+    vhm = h.data_ptr();
+  }
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(value.device());
+  at::Tensor grad_value = at::empty_like(value);
+  at::Tensor grad_sla = at::empty_like(sla);
+  const size_t n = ops3d_fda_backward_workspace_bytes(z.code, z.B, z.S, z.G, z.D, z.L, z.Q, z.K);
+  at::Tensor ws;
+  if (n) ws = at::empty({(int64_t)n}, value.options().dtype(at::kByte));
+  const int rc = ops3d_fda_backward_ex(ptr(value), vhm, shapes.data_ptr<int64_t>(), lsi.data_ptr<int64_t>(),
+                                       ptr(sla), ptr(grad_output), ptr(grad_value), ptr(grad_sla), ptr(ws), n,
+                                       z.code, z.B, z.S, z.G, z.D, z.L, z.Q, z.K, (int)im2col_step,
+                                       stream_of(value));
+  if (rc != OPS3D_FDA_OK) raise(rc, "flash_deform_attn_backward failed");
+  return {grad_value, grad_sla};
+}
+
+// reference csrc/flash_deform_attn.h:7-25 (d_stride, block_thread and use_reg are launch hints
+// of the CUDA build; the gfx950 library chooses its own geometry)
+at::Tensor flash_deform_attn_forward(const at::Tensor &value, const at::Tensor &shapes, const at::Tensor &lsi,
+                                     const at::Tensor &sla, int64_t im2col_step, int64_t K, int64_t /*d_stride*/,
+                                     int64_t /*block_thread*/, bool /*use_reg*/) {
+  return std::get<0>(forward_keep_head_major(value, shapes, lsi, sla, im2col_step, K));
+}
+
+// reference csrc/flash_deform_attn.h:27-52
+std::vector<at::Tensor> flash_deform_attn_backward(const at::Tensor &value, const at::Tensor &shapes,
+                                                   const at::Tensor &lsi, const at::Tensor &sla,
+                                                   const at::Tensor &grad_output, int64_t im2col_step, int64_t K,
+                                                   int64_t /*d_stride*/, int64_t /*block_thread*/) {
+  return backward_with_head_major(value, c10::nullopt, shapes, lsi, sla, grad_output, im2col_step, K);
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("flash_deform_attn_forward", &flash_deform_attn_forward, "flash_deform_attn_forward",
+        py::arg("value"), py::arg("spatial_shapes"), py::arg("level_start_index"), py::arg("sampling_loc_attn"),
+        py::arg("im2col_step"), py::arg("K"), py::arg("d_stride") = 8, py::arg("block_thread") = 0,
+        py::arg("use_reg") = true);
+  m.def("flash_deform_attn_backward", &flash_deform_attn_backward, "flash_deform_attn_backward",
+        py::arg("value"), py::arg("spatial_shapes"), py::arg("level_start_index"), py::arg("sampling_loc_attn"),
+        py::arg("grad_output"), py::arg("im2col_step"), py::arg("K"), py::arg("d_stride") = 1,
+        py::arg("block_thread") = 0);
+  m.def("forward_keep_head_major", &forward_keep_head_major, "forward that also returns its workspace");
+  m.def("backward_with_head_major", &backward_with_head_major, "backward reusing the forward workspace");
+}

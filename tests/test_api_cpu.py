@@ -128,3 +128,24 @@ def test_workload_byte_counts():
     c5 = WORKLOADS["c5"].algorithmic_bytes(2)
     assert round(c5["fwd"] / 1e6, 1) == 1071.6 and round(c5["bwd"] / 1e6, 1) == 1837.1
     assert WORKLOADS["c4"].S == 73728 and WORKLOADS["c5"].S == 598016 and WORKLOADS["c3"].S == 37376
+
+
+def test_torch_extension_bound_and_checks():
+    """The PyTorch extension module (C++ over the C ABI) is built and serves _C's tensor entry
+    points, with the reference's error behaviour."""
+    import ops3d_amd
+    from ops3d_amd import _fda_torch
+
+    C = ops3d_amd._C
+    if C is None:
+        pytest.skip("libops3d_fda.so not built")
+    for name in ("flash_deform_attn_forward", "flash_deform_attn_backward", "forward_keep_head_major",
+                 "backward_with_head_major"):
+        assert getattr(C, name) is getattr(_fda_torch, name), name
+    v = torch.zeros(1, 8, 1, 8)
+    st = torch.tensor([[2, 2, 2]])
+    lsi = torch.zeros(1, dtype=torch.long)
+    with pytest.raises(RuntimeError, match="CPU"):
+        C.flash_deform_attn_forward(v, st, lsi, torch.zeros(1, 2, 1, 16), 64, 4)
+    with pytest.raises(TypeError):
+        C.flash_deform_attn_forward(v.numpy(), st, lsi, torch.zeros(1, 2, 1, 16), 64, 4)
