@@ -24,7 +24,9 @@ ops3d_fda_profile_*).
   memory   = the library's forward / backward workspace sizes and torch's peak allocation of
              a step above the resident inputs.
 
---all prints a per-configuration table (c1..c5, plus fp16 and fp32 forward at c5) to stderr.
+--all prints a per-configuration table (c1..c5, plus fp16 and fp32 forward at c5) to stderr,
+and at c4 and c5 the offset-mode op (FlashDeformAttnFromOffsets: caller-side fusion of the
+location producer) against the unfused caller.
 """
 from __future__ import annotations
 
@@ -177,6 +179,44 @@ class Bench:
         return fwd, bwd
 
 
+def measure_offsets(w, steps, warmup, device):
+    """Caller-side fusion at workload w: fwd+bwd of FlashDeformAttnFromOffsets (offsets from one
+    projection, locations formed in the kernels) against the caller the reference's tests
+    write -- locations ref + offset / size and torch.cat in torch, the packed op, autograd
+    splitting the gradient -- on the same inputs (bf16 offsets/logits, fp32 reference points)."""
+    import torch
+
+    from ops3d_amd import FlashDeformAttnFromOffsets, FlashDeformAttnFunction
+    from ops3d_amd.workloads import make_inputs
+
+    inp = make_inputs(w, seed=0, dtype=w.dtype, device=device)
+    B, Q, G, L, K = w.B, w.nq, w.G, w.L, w.K
+    n = 3 * L * K
+    gen = torch.Generator(device=device).manual_seed(1)
+    value = inp["value"].requires_grad_(True)
+    oa = inp["sampling_loc_attn"].clone()
+    oa[..., :n] = (torch.randn(B, Q, G, n, generator=gen, device=device) * 2.0).to(oa.dtype)
+    oa.requires_grad_(True)
+    ref = torch.rand(B, Q, 1, 3, generator=gen, device=device, requires_grad=True)
+    st, lsi, go = inp["spatial_shapes"], inp["level_start_index"], inp["grad_output"]
+    size = st.flip(-1).to(torch.float32).view(1, 1, 1, L, 1, 3)
+
+    def fused():
+        value.grad = oa.grad = ref.grad = None
+        FlashDeformAttnFromOffsets.apply(value, st, lsi, oa, ref, 64, K).backward(go)
+
+    def unfused():
+        value.grad = oa.grad = ref.grad = None
+        off = oa[..., :n].view(B, Q, G, L, K, 3)
+        loc = (ref.view(B, Q, 1, 1, 1, 3) + off.float() / size).to(oa.dtype)
+        sla = torch.cat([loc.reshape(B, Q, G, n), oa[..., n:]], -1)
+        FlashDeformAttnFunction.apply(value, st, lsi, sla, 64, K, True).backward(go)
+
+    b = Bench.__new__(Bench)
+    b.torch = torch
+    return {"fused": b.time_loop(fused, steps, warmup), "unfused": b.time_loop(unfused, steps, warmup)}
+
+
 def measure(w, dtype, steps, warmup, device, with_kernels=True, fwd_only=False):
     b = Bench(w, dtype, device)
     res = {"workload": w.name, "dtype": dtype}
@@ -297,6 +337,8 @@ def main():
     ap.add_argument("--json-out", default=None, help="write all results as JSON to this path")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the per-kernel loops of --config (for profilers); prints no JSON line")
+    ap.add_argument("--offsets", action="store_true",
+                    help="only the offset-mode op against the unfused caller at --config (stderr)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB, 5 times (HBM counter calibration)")
     args = ap.parse_args()
@@ -327,6 +369,11 @@ def main():
         torch.cuda.synchronize()
         log(f"copied {args.copy_calibration} MiB 5 times")
         return
+    if args.offsets:
+        o = measure_offsets(WORKLOADS[args.config], args.steps, args.warmup, dev)
+        log(f" {args.config} offsets | fwd+bwd fused (FlashDeformAttnFromOffsets) {o['fused']['median'] * 1e3:8.1f} us"
+            f" | unfused caller (ref + off/size, cat, packed op) {o['unfused']['median'] * 1e3:8.1f} us")
+        return
     if args.kernels_only:
         w = WORKLOADS[args.config]
         b = Bench(w, w.dtype, dev)
@@ -346,6 +393,13 @@ def main():
             r["samples"] = w.samples()
             results.append(r)
             log(summary_line(r))
+
+        for name in ("c4", "c5"):
+            o = measure_offsets(WORKLOADS[name], args.steps, args.warmup, dev)
+            log(f" {name} offsets | fwd+bwd fused (FlashDeformAttnFromOffsets) {o['fused']['median'] * 1e3:8.1f} us"
+                f" | unfused caller (ref + off/size, cat, packed op) {o['unfused']['median'] * 1e3:8.1f} us")
+            results.append({"workload": name, "offsets": o})
+            torch.cuda.empty_cache()
 
     w = WORKLOADS[args.config]
     log(f"[bench] headline {w.name} {w.dtype} steps={args.steps} warmup={args.warmup}")

@@ -157,6 +157,43 @@ OPS3D_FDA_API int ops3d_fda_backward_accumulate_f32(
     int im2col_step, void *stream);
 
 /*
+ * Offset mode: caller-side fusion of the sampling_loc_attn producer and of the
+ * grad_sampling_loc_attn consumer (no counterpart in the reference, whose callers build the packed
+ * tensor with torch.cat from separately computed locations and logits,
+ * tests/test_flash_deform_attn.py:30-37).  offset_attn has the packed planar layout of
+ * sampling_loc_attn ([B,Q,G,P]: L*K (x,y,z) triples, then L*K logits), but its triples are
+ * offsets in voxels of their level -- the output of one linear projection of the query, used as
+ * is.  The kernels form each location as
+ *     loc = reference_points[b,q,r] + offset / (W, H, D) of the level     (fp32, step by step),
+ * r = the level when ref_levels == L, 0 when ref_levels == 1; reference_points is
+ * [B,Q,ref_levels,3] fp32 whatever the value dtype (a 16-bit reference point would be off by
+ * about a voxel on a 256-wide level), (x, y, z) in [0, 1].  For fp32 values the result equals
+ * ops3d_fda_forward on the locations a caller computes that way in fp32; for 16-bit values it is
+ * more accurate (the location is never rounded to 16 bits).  The backward writes
+ * grad_offset_attn in the same layout: offset gradients (d pixel / d offset = 1, so they are the
+ * location gradients divided by the level size) and logit gradients; and, when
+ * grad_reference_points is not NULL, ADDS the gradient of reference_points into it ([B,Q,
+ * ref_levels,3] fp32, pass it zeroed): the sum over heads and points of offset gradient * level
+ * size, by fp32 atomics (the order of the heads' additions, and so the rounding, can differ
+ * between runs).  Same workspaces, errors and head-major reuse as
+ * ops3d_fda_forward / ops3d_fda_backward_ex; ref_levels must be 1 or num_levels.
+ */
+OPS3D_FDA_API int ops3d_fda_forward_offsets(const void *value, const int64_t *spatial_shapes,
+                       const int64_t *level_start_index, const void *offset_attn,
+                       const float *reference_points, int ref_levels, void *output, void *workspace,
+                       size_t workspace_bytes, int dtype, int batch, int spatial_size, int num_heads,
+                       int channels, int num_levels, int num_query, int num_point, int im2col_step,
+                       void *stream);
+OPS3D_FDA_API int ops3d_fda_backward_offsets(const void *value, const void *value_head_major,
+                       const int64_t *spatial_shapes, const int64_t *level_start_index,
+                       const void *offset_attn, const float *reference_points, int ref_levels,
+                       const void *grad_output, void *grad_value, void *grad_offset_attn,
+                       float *grad_reference_points, void *workspace, size_t workspace_bytes,
+                       int dtype, int batch,
+                       int spatial_size, int num_heads, int channels, int num_levels,
+                       int num_query, int num_point, int im2col_step, void *stream);
+
+/*
  * Allocation-free backward.  Same as ops3d_fda_backward, with no workspace argument: the
  * workspace is a static device array of OPS3D_FDA_NOALLOC_SCRATCH_BYTES (64 MiB) inside the
  * library, which every device it runs on holds until the process ends.  Problems whose

@@ -38,6 +38,8 @@ EXPORTED_SYMBOLS = (
     "ops3d_fda_backward_ex",
     "ops3d_fda_backward_accumulate_f32",
     "ops3d_fda_backward_noalloc",
+    "ops3d_fda_forward_offsets",
+    "ops3d_fda_backward_offsets",
     "ops3d_fda_profile_enable",
     "ops3d_fda_profile_read",
 )
@@ -68,6 +70,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ops3d_fda_backward_accumulate_f32.argtypes = [_vp] * 8 + [_sz] + [_i] * 9 + [_vp]
     lib.ops3d_fda_backward_noalloc.restype = _i
     lib.ops3d_fda_backward_noalloc.argtypes = [_vp] * 7 + [_i] * 9 + [_vp]
+    lib.ops3d_fda_forward_offsets.restype = _i
+    lib.ops3d_fda_forward_offsets.argtypes = [_vp] * 5 + [_i] + [_vp] * 2 + [_sz] + [_i] * 9 + [_vp]
+    lib.ops3d_fda_backward_offsets.restype = _i
+    lib.ops3d_fda_backward_offsets.argtypes = [_vp] * 6 + [_i] + [_vp] * 5 + [_sz] + [_i] * 9 + [_vp]
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -86,12 +92,13 @@ class _NativeFDA:
         if ver != self.ABI_VERSION:
             raise ImportError(f"{path}: ABI version {ver}, expected {self.ABI_VERSION}")
         # The PyTorch extension module (csrc/torch_ext.cpp) does the same checks and calls of
-        # the four tensor entry points in C++, for a fraction of the host time: when it is
-        # built, those methods are its functions.
+        # the tensor entry points in C++, for a fraction of the host time: when it is built,
+        # those methods are its functions.
         self._ext = ext
         if ext is not None:
             for name in ("flash_deform_attn_forward", "flash_deform_attn_backward",
-                         "forward_keep_head_major", "backward_with_head_major"):
+                         "forward_keep_head_major", "backward_with_head_major",
+                         "forward_offsets", "backward_offsets"):
                 setattr(self, name, getattr(ext, name))
 
     # -- helpers ---------------------------------------------------------------------------
@@ -249,6 +256,69 @@ class _NativeFDA:
         if rc != OPS3D_FDA_OK:
             self._raise(rc, "flash_deform_attn_backward_accumulate failed")
         return grad_sla
+
+    def _ref_levels(self, reference_points, value, B, Q, L):
+        self._check_inputs({"reference_points": reference_points}, value)
+        if reference_points.dtype != torch.float32:
+            raise ValueError(f"reference_points must be float32, got {reference_points.dtype}")
+        if reference_points.dim() != 4 or tuple(reference_points.shape[:2]) != (B, Q) \
+                or reference_points.shape[3] != 3 or reference_points.shape[2] not in (1, L):
+            raise ValueError(f"reference_points must be [B={B}, Q={Q}, 1 or L={L}, 3], "
+                             f"got {tuple(reference_points.shape)}")
+        return int(reference_points.shape[2])
+
+    def forward_offsets(self, value, spatial_shapes, level_start_index, offset_attn, reference_points,
+                        im2col_step, K):
+        """Offset-mode forward (ops3d_fda_forward_offsets): offset_attn holds offsets in voxels of
+        their level instead of locations.  Returns the output and the forward workspace."""
+        B, S, G, D, L, Q = self._common(value, spatial_shapes, level_start_index, offset_attn, K, {})
+        R = self._ref_levels(reference_points, value, B, Q, L)
+        out = torch.empty((B, Q, G * D), dtype=value.dtype, device=value.device)
+        code = _DTYPE_CODE[value.dtype]
+        n = self._lib.ops3d_fda_forward_workspace_bytes(code, B, S, G, D, L, Q, int(K))
+        ws = torch.empty(n, dtype=torch.uint8, device=value.device) if n else None
+        stream = torch.cuda.current_stream(value.device).cuda_stream
+        with torch.cuda.device(value.device):
+            rc = self._lib.ops3d_fda_forward_offsets(
+                _ptr(value), _ptr(spatial_shapes), _ptr(level_start_index), _ptr(offset_attn),
+                _ptr(reference_points), R, _ptr(out), _ptr(ws), n, code, B, S, G, D, L, Q, int(K),
+                int(im2col_step), stream,
+            )
+        if rc != OPS3D_FDA_OK:
+            self._raise(rc, "flash_deform_attn_forward_offsets failed")
+        return out, ws
+
+    def backward_offsets(self, value, value_head_major, spatial_shapes, level_start_index, offset_attn,
+                         reference_points, grad_output, im2col_step, K, want_ref_grad):
+        """Offset-mode backward (ops3d_fda_backward_offsets): returns [grad_value,
+        grad_offset_attn (offset and logit gradients, in offset_attn's layout),
+        grad_reference_points (fp32, None unless want_ref_grad)]."""
+        B, S, G, D, L, Q = self._common(
+            value, spatial_shapes, level_start_index, offset_attn, K, {"grad_output": grad_output}
+        )
+        R = self._ref_levels(reference_points, value, B, Q, L)
+        if grad_output.numel() != B * Q * G * D:
+            raise ValueError(f"grad_output must have B*Q*G*D = {B * Q * G * D} elements, got {grad_output.numel()}")
+        code = _DTYPE_CODE[value.dtype]
+        if value_head_major is not None:
+            need = self._lib.ops3d_fda_forward_workspace_bytes(code, B, S, G, D, L, Q, int(K))
+            if (value_head_major.device != value.device or value_head_major.dtype != torch.uint8
+                    or value_head_major.numel() != need):
+                raise ValueError("value_head_major is not a forward workspace of this value")
+        grad_value = torch.empty_like(value)
+        grad_oa = torch.empty_like(offset_attn)
+        grad_ref = torch.zeros_like(reference_points) if want_ref_grad else None
+        ws, ws_bytes = self._workspace(code, B, S, G, D, L, Q, K, value.device)
+        stream = torch.cuda.current_stream(value.device).cuda_stream
+        with torch.cuda.device(value.device):
+            rc = self._lib.ops3d_fda_backward_offsets(
+                _ptr(value), _ptr(value_head_major), _ptr(spatial_shapes), _ptr(level_start_index),
+                _ptr(offset_attn), _ptr(reference_points), R, _ptr(grad_output), _ptr(grad_value), _ptr(grad_oa),
+                _ptr(grad_ref), _ptr(ws), ws_bytes, code, B, S, G, D, L, Q, int(K), int(im2col_step), stream,
+            )
+        if rc != OPS3D_FDA_OK:
+            self._raise(rc, "flash_deform_attn_backward_offsets failed")
+        return [grad_value, grad_oa, grad_ref]
 
     def flash_deform_attn_backward_noalloc(
         self, value, spatial_shapes, level_start_index, sampling_loc_attn, grad_output, im2col_step, K,

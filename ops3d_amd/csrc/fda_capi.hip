@@ -405,12 +405,11 @@ size_t ops3d_fda_forward_workspace_bytes(int dtype, int batch, int spatial_size,
   return align256((size_t)batch * num_heads * (size_t)head_copy_rows_max(spatial_size, channels * e) * channels * e);
 }
 
-int ops3d_fda_forward(const void *value, const int64_t *spatial_shapes,
-                      const int64_t *level_start_index, const void *sampling_loc_attn,
-                      void *output, void *workspace, size_t workspace_bytes, int dtype, int batch,
-                      int spatial_size, int num_heads, int channels, int num_levels,
-                      int num_query, int num_point, int im2col_step, void *stream) {
-  g_last_error.clear();
+static int forward_impl(const void *value, const int64_t *spatial_shapes, const int64_t *level_start_index,
+                        const void *sampling_loc_attn, const float *ref, int ref_levels, void *output,
+                        void *workspace, size_t workspace_bytes, int dtype, int batch, int spatial_size,
+                        int num_heads, int channels, int num_levels, int num_query, int num_point,
+                        int im2col_step, void *stream) {
   Geometry geo;
   int rc = common_checks(dtype, batch, spatial_size, num_heads, channels, num_levels, num_query,
                          num_point, im2col_step, false, geo);
@@ -439,6 +438,8 @@ int ops3d_fda_forward(const void *value, const int64_t *spatial_shapes,
   geo.a.shapes = spatial_shapes;
   geo.a.lsi = level_start_index;
   geo.a.loc_attn = sampling_loc_attn;
+  geo.a.ref = ref;
+  geo.a.ref_levels = ref_levels;
   geo.a.out = output;
   prof_mark(7, st);
   hipError_t e = launch(dtype, 0, geo, st);
@@ -448,6 +449,17 @@ int ops3d_fda_forward(const void *value, const int64_t *spatial_shapes,
   prof_mark(8, st);
   if (g_prof_on) g_prof_recorded[1] = true;
   return OPS3D_FDA_OK;
+}
+
+int ops3d_fda_forward(const void *value, const int64_t *spatial_shapes,
+                      const int64_t *level_start_index, const void *sampling_loc_attn,
+                      void *output, void *workspace, size_t workspace_bytes, int dtype, int batch,
+                      int spatial_size, int num_heads, int channels, int num_levels,
+                      int num_query, int num_point, int im2col_step, void *stream) {
+  g_last_error.clear();
+  return forward_impl(value, spatial_shapes, level_start_index, sampling_loc_attn, nullptr, 0, output, workspace,
+                      workspace_bytes, dtype, batch, spatial_size, num_heads, channels, num_levels, num_query,
+                      num_point, im2col_step, stream);
 }
 
 size_t ops3d_fda_backward_workspace_bytes(int dtype, int batch, int spatial_size, int num_heads,
@@ -470,7 +482,8 @@ static int backward_impl(const void *value, const void *value_head_major, const 
                          void *grad_sampling_loc_attn, void *workspace, size_t workspace_bytes,
                          int dtype, int batch, int spatial_size, int num_heads, int channels,
                          int num_levels, int num_query, int num_point, int im2col_step,
-                         hipStream_t st) {
+                         hipStream_t st, const float *ref = nullptr, int ref_levels = 0,
+                         float *grad_ref = nullptr) {
   Geometry geo;
   int rc = common_checks(dtype, batch, spatial_size, num_heads, channels, num_levels, num_query,
                          num_point, im2col_step, true, geo);
@@ -510,6 +523,9 @@ static int backward_impl(const void *value, const void *value_head_major, const 
   a.shapes = spatial_shapes;
   a.lsi = level_start_index;
   a.loc_attn = sampling_loc_attn;
+  a.ref = ref;
+  a.ref_levels = ref_levels;
+  a.grad_ref = grad_ref;
   a.grad_out = grad_output;
   a.grad_loc_attn = grad_sampling_loc_attn;
   a.keys = keys;
@@ -681,6 +697,50 @@ int ops3d_fda_backward_noalloc(const void *value, const int64_t *spatial_shapes,
                        grad_value, false, grad_sampling_loc_attn, ws, (size_t)OPS3D_FDA_NOALLOC_SCRATCH_BYTES, dtype,
                        batch, spatial_size, num_heads, channels, num_levels, num_query, num_point, im2col_step,
                        static_cast<hipStream_t>(stream));
+}
+
+// Offset mode: checks of the reference points shared by both entry points.
+static int offsets_checks(const float *reference_points, int ref_levels, int num_levels) {
+  if (!reference_points) return fail(OPS3D_FDA_EINVAL, "reference_points is NULL");
+  if (ref_levels != 1 && ref_levels != num_levels)
+    return fail(OPS3D_FDA_EINVAL, "ref_levels must be 1 or num_levels (%d), got %d", num_levels, ref_levels);
+  if (misaligned(reference_points)) return fail(OPS3D_FDA_EINVAL, "reference_points must be 4-byte aligned");
+  return OPS3D_FDA_OK;
+}
+
+int ops3d_fda_forward_offsets(const void *value, const int64_t *spatial_shapes, const int64_t *level_start_index,
+                              const void *offset_attn, const float *reference_points, int ref_levels, void *output,
+                              void *workspace, size_t workspace_bytes, int dtype, int batch, int spatial_size,
+                              int num_heads, int channels, int num_levels, int num_query, int num_point,
+                              int im2col_step, void *stream) {
+  g_last_error.clear();
+  if ((int64_t)batch * num_query > 0) {
+    const int rc = offsets_checks(reference_points, ref_levels, num_levels);
+    if (rc) return rc;
+  }
+  return forward_impl(value, spatial_shapes, level_start_index, offset_attn, reference_points, ref_levels, output,
+                      workspace, workspace_bytes, dtype, batch, spatial_size, num_heads, channels, num_levels,
+                      num_query, num_point, im2col_step, stream);
+}
+
+int ops3d_fda_backward_offsets(const void *value, const void *value_head_major, const int64_t *spatial_shapes,
+                               const int64_t *level_start_index, const void *offset_attn,
+                               const float *reference_points, int ref_levels, const void *grad_output,
+                               void *grad_value, void *grad_offset_attn, float *grad_reference_points,
+                               void *workspace, size_t workspace_bytes,
+                               int dtype, int batch, int spatial_size, int num_heads, int channels, int num_levels,
+                               int num_query, int num_point, int im2col_step, void *stream) {
+  g_last_error.clear();
+  if ((int64_t)batch * num_query > 0) {
+    const int rc = offsets_checks(reference_points, ref_levels, num_levels);
+    if (rc) return rc;
+  }
+  if (value_head_major && misaligned(value_head_major))
+    return fail(OPS3D_FDA_EINVAL, "value_head_major must be 4-byte aligned");
+  return backward_impl(value, value_head_major, spatial_shapes, level_start_index, offset_attn, grad_output,
+                       grad_value, false, grad_offset_attn, workspace, workspace_bytes, dtype, batch, spatial_size,
+                       num_heads, channels, num_levels, num_query, num_point, im2col_step,
+                       static_cast<hipStream_t>(stream), reference_points, ref_levels, grad_reference_points);
 }
 
 }  // extern "C"

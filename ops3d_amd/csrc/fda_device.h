@@ -38,6 +38,11 @@ struct Args {
   const int64_t *shapes;      // [L,3] (D,H,W)
   const int64_t *lsi;         // [L]
   const void *loc_attn;       // [B,Q,G,P] T
+  const float *ref;           // offset mode: reference points [B,Q,ref_levels,3] fp32 (x,y,z in
+                              // [0,1]); the location entries of loc_attn are then offsets in
+                              // voxels of their level (NULL: normalised locations)
+  int ref_levels;             // 1 (one point per query) or L (one per level)
+  float *grad_ref;            // offset mode, backward: [B,Q,ref_levels,3] fp32, added into (NULL: none)
   const void *grad_out;       // [B,Q,G*D] T          (backward)
   void *out;                  // [B,Q,G*D] T          (forward)
   float *grad_value;          // [B,S,G,D] fp32 acc   (backward)
@@ -299,6 +304,46 @@ __device__ __forceinline__ void stage_record(const T *rec_g, int P, int j, bool 
     Elem<T>::unpack(word, f);
 #pragma unroll
     for (int e = 0; e < EPW; ++e) rec[w * EPW + e] = f[e];
+  }
+}
+
+// Offset mode (Args::ref): the staged location entries are offsets in voxels of their level;
+// turn them into normalised locations loc = ref + offset / size, rounded in fp32 step by step
+// (division, then addition; no contraction) -- the location a caller computing it in fp32 and
+// packing it would pass.  Lane j of the unit handles samples j, j+LPU, ...; bq = b*Q + q.
+template <typename T, int LPU>
+__device__ __forceinline__ void offsets_to_locations(const Args &a, int64_t bq, int j, bool live, float *rec) {
+#pragma clang fp contract(off)
+  const int LK = a.L * a.K;
+  const float *ref = a.ref + bq * a.ref_levels * 3;
+  for (int s = j; s < LK; s += LPU) {
+    const int l = s / a.K;
+    const int r = a.ref_levels > 1 ? 3 * l : 0;
+    const float rx = live ? ref[r] : 0.f, ry = live ? ref[r + 1] : 0.f, rz = live ? ref[r + 2] : 0.f;
+    rec[3 * s] = rx + rec[3 * s] / (float)a.shapes[3 * l + 2];
+    rec[3 * s + 1] = ry + rec[3 * s + 1] / (float)a.shapes[3 * l + 1];
+    rec[3 * s + 2] = rz + rec[3 * s + 2] / (float)a.shapes[3 * l];
+  }
+}
+
+// Offset mode, backward: add this unit's part of the reference-point gradient,
+//     grad_ref[b,q,r,c] += sum over the unit's samples of reference r of grad_offset_c * size_c
+// (d loc / d ref = 1, d loc / d offset = 1 / size), from the offset gradients in rec.  Lane j
+// of the unit handles (r, c) pairs j, j+LPU, ...; fp32 atomics, as the G heads of a query add
+// to the same elements (their order, and so the rounding, varies between runs).
+template <int LPU>
+__device__ __forceinline__ void add_ref_grad(const Args &a, int64_t bq, int j, const float *rec) {
+  const int R = a.ref_levels, K = a.K, L = a.L;
+  for (int t = j; t < 3 * R; t += LPU) {
+    const int r = t / 3, c = t - 3 * r;
+    const int l0 = R > 1 ? r : 0, l1 = R > 1 ? r + 1 : L;
+    float acc = 0.f;
+    for (int l = l0; l < l1; ++l) {
+      float sl = 0.f;
+      for (int k = 0; k < K; ++k) sl += rec[3 * (l * K + k) + c];
+      acc = fmaf(sl, (float)a.shapes[3 * l + 2 - c], acc);   // size of axis c: W, H, D
+    }
+    atomicAdd(a.grad_ref + bq * 3 * R + t, acc);
   }
 }
 

@@ -97,6 +97,10 @@ __global__ __launch_bounds__(kBlock) void fda_forward_kernel(const Args a) {
 
   stage_record<T, LPU>(static_cast<const T *>(a.loc_attn) + unit * P, P, j, live, rec);
   wave_lds_sync();
+  if (a.ref) {
+    offsets_to_locations<T, LPU>(a, unit / a.G, j, live, rec);
+    wave_lds_sync();
+  }
   unit_softmax<LPU>(rec + 3 * LK, LK, j);
   wave_lds_sync();
 
@@ -193,6 +197,10 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kFwdWave
 
   stage_record<T, UL>(static_cast<const T *>(a.loc_attn) + unit * P, P, ju, live, rec);
   wave_lds_sync();
+  if (a.ref) {
+    offsets_to_locations<T, UL>(a, unit / a.G, ju, live, rec);
+    wave_lds_sync();
+  }
   unit_softmax<UL>(rec + 3 * LK, LK, ju);
   wave_lds_sync();
 
@@ -310,6 +318,10 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kQueryWa
 
   stage_record<T, UL>(static_cast<const T *>(a.loc_attn) + unit * P, P, ju, live, rec);
   wave_lds_sync();
+  if (a.ref) {
+    offsets_to_locations<T, UL>(a, unit / a.G, ju, live, rec);
+    wave_lds_sync();
+  }
   unit_softmax<UL>(rec + 3 * LK, LK, ju);
   wave_lds_sync();
 
@@ -399,10 +411,11 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kQueryWa
           if (ju == 0) {
             const int su = l * K + k0 + u;
             const float at = rec[3 * LK + su];
-            // d(pixel)/d(loc) = size (grid_sample: size/2 per unit of grid, grid = 2*loc - 1)
-            rec[3 * su] = gx * at * (float)Wl;
-            rec[3 * su + 1] = gy * at * (float)Hl;
-            rec[3 * su + 2] = gz * at * (float)Dl;
+            // d(pixel)/d(loc) = size (grid_sample: size/2 per unit of grid, grid = 2*loc - 1);
+            // offset mode: d(pixel)/d(offset) = 1
+            rec[3 * su] = gx * at * (a.ref ? 1.f : (float)Wl);
+            rec[3 * su + 1] = gy * at * (a.ref ? 1.f : (float)Hl);
+            rec[3 * su + 2] = gz * at * (a.ref ? 1.f : (float)Dl);
             gat_s[su] = ga;
           }
         }
@@ -448,6 +461,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kQueryWa
     rec[3 * LK + t] = at * (gat_s[t] - dot);
   }
   wave_lds_sync();
+  if (live && a.grad_ref) add_ref_grad<UL>(a, unit / a.G, ju, rec);
   if (live) write_record<T, UL>(static_cast<T *>(a.grad_loc_attn) + unit * P, P, ju, rec);
   clear_tile_counts(a);
 }
@@ -488,6 +502,10 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
 
   stage_record<T, LPU>(static_cast<const T *>(a.loc_attn) + unit * P, P, j, live, rec);
   wave_lds_sync();
+  if (a.ref) {
+    offsets_to_locations<T, LPU>(a, unit / a.G, j, live, rec);
+    wave_lds_sync();
+  }
   unit_softmax<LPU>(rec + 3 * LK, LK, j);
   wave_lds_sync();
 
@@ -570,10 +588,11 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
         ga = unit_sum<LPU>(ga);
         if (j == 0 && u < nk) {
           const int su = s + u;
-          // d(pixel)/d(loc) = size (grid_sample: size/2 per unit of grid, grid = 2*loc - 1)
-          rec[3 * su] = gx * at[u] * (float)Wl;
-          rec[3 * su + 1] = gy * at[u] * (float)Hl;
-          rec[3 * su + 2] = gz * at[u] * (float)Dl;
+          // d(pixel)/d(loc) = size (grid_sample: size/2 per unit of grid, grid = 2*loc - 1);
+          // offset mode: d(pixel)/d(offset) = 1
+          rec[3 * su] = gx * at[u] * (a.ref ? 1.f : (float)Wl);
+          rec[3 * su + 1] = gy * at[u] * (a.ref ? 1.f : (float)Hl);
+          rec[3 * su + 2] = gz * at[u] * (a.ref ? 1.f : (float)Dl);
           gat_s[su] = ga;
           cx_s[su] = in[u] ? (uint32_t)(m.x0 + 1) : kKeyInvalid;
           cy_s[su] = (uint32_t)(m.y0 + 1);
@@ -626,6 +645,7 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
     rec[3 * LK + t] = at * (gat_s[t] - dot);
   }
   wave_lds_sync();
+  if (live && a.grad_ref) add_ref_grad<LPU>(a, unit / a.G, j, rec);
   if (live) write_record<T, LPU>(static_cast<T *>(a.grad_loc_attn) + unit * P, P, j, rec);
   clear_tile_counts(a);
 }

@@ -1,7 +1,7 @@
 // PyTorch extension module over the C ABI of libops3d_fda.so: the tensor-level entry points of
 // the reference's `_C` (csrc/vision.cpp:23-24 -> csrc/flash_deform_attn.h:7-52), plus the two
 // calls FlashDeformAttnFunction makes (forward keeping the head-major copy of value, backward
-// reusing it).  Host code only: argument checks, output allocation through torch's caching
+// reusing it) and the offset-mode pair.  Host code only: argument checks, output allocation through torch's caching
 // allocator, torch's current HIP stream, then one C ABI call.  It exists for host overhead --
 // the same checks and calls through ctypes cost several times as much per call.
 //
@@ -144,6 +144,70 @@ std::vector<at::Tensor> backward_with_head_major(const at::Tensor &value,
   return {grad_value, grad_sla};
 }
 
+// Offset mode: reference_points [B,Q,1 or L,3] fp32; returns ref_levels.
+int ref_levels_of(const at::Tensor &ref, const at::Tensor &value, const Sizes &z) {
+  check_tensor(ref, "reference_points", value);
+  if (ref.scalar_type() != at::kFloat) throw std::invalid_argument("reference_points must be float32");
+  if (ref.dim() != 4 || ref.size(0) != z.B || ref.size(1) != z.Q || ref.size(3) != 3 ||
+      (ref.size(2) != 1 && ref.size(2) != z.L))
+    throw std::invalid_argument("reference_points must be [B, Q, 1 or L, 3]");
+  return (int)ref.size(2);
+}
+
+// Forward with offsets in voxels of their level in place of locations (ops3d_fda_forward_offsets).
+std::tuple<at::Tensor, c10::optional<at::Tensor>> forward_offsets(
+    const at::Tensor &value, const at::Tensor &shapes, const at::Tensor &lsi, const at::Tensor &offset_attn,
+    const at::Tensor &reference_points, int64_t im2col_step, int64_t K) {
+  const Sizes z = common(value, shapes, lsi, offset_attn, K);
+  const int R = ref_levels_of(reference_points, value, z);
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(value.device());
+  at::Tensor out = at::empty({z.B, z.Q, (int64_t)z.G * z.D}, value.options());
+  const size_t n = ops3d_fda_forward_workspace_bytes(z.code, z.B, z.S, z.G, z.D, z.L, z.Q, z.K);
+  c10::optional<at::Tensor> ws;
+  if (n) ws = at::empty({(int64_t)n}, value.options().dtype(at::kByte));
+  const int rc = ops3d_fda_forward_offsets(ptr(value), shapes.data_ptr<int64_t>(), lsi.data_ptr<int64_t>(),
+                                           ptr(offset_attn), reference_points.data_ptr<float>(), R, ptr(out),
+                                           ws ? ws->data_ptr() : nullptr, n, z.code, z.B, z.S, z.G, z.D, z.L, z.Q,
+                                           z.K, (int)im2col_step, stream_of(value));
+  if (rc != OPS3D_FDA_OK) raise(rc, "flash_deform_attn_forward_offsets failed");
+  return {out, ws};
+}
+
+// Backward of forward_offsets (ops3d_fda_backward_offsets): [grad_value, grad_offset_attn,
+// grad_reference_points] (the last undefined -- None -- unless want_ref_grad).
+std::vector<at::Tensor> backward_offsets(const at::Tensor &value, const c10::optional<at::Tensor> &value_head_major,
+                                         const at::Tensor &shapes, const at::Tensor &lsi,
+                                         const at::Tensor &offset_attn, const at::Tensor &reference_points,
+                                         const at::Tensor &grad_output, int64_t im2col_step, int64_t K,
+                                         bool want_ref_grad) {
+  const Sizes z = common(value, shapes, lsi, offset_attn, K);
+  check_grad_output(grad_output, value, z);
+  const int R = ref_levels_of(reference_points, value, z);
+  const void *vhm = nullptr;
+  if (value_head_major && value_head_major->defined()) {
+    const at::Tensor &h = *value_head_major;
+    const size_t need = ops3d_fda_forward_workspace_bytes(z.code, z.B, z.S, z.G, z.D, z.L, z.Q, z.K);
+    if (h.device() != value.device() || h.scalar_type() != at::kByte || (size_t)h.numel() != need)
+      throw std::invalid_argument("value_head_major is not a forward workspace of this value");
+    vhm = h.data_ptr();
+  }
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(value.device());
+  at::Tensor grad_value = at::empty_like(value);
+  at::Tensor grad_oa = at::empty_like(offset_attn);
+  at::Tensor grad_ref;
+  if (want_ref_grad) grad_ref = at::zeros_like(reference_points);
+  const size_t n = ops3d_fda_backward_workspace_bytes(z.code, z.B, z.S, z.G, z.D, z.L, z.Q, z.K);
+  at::Tensor ws;
+  if (n) ws = at::empty({(int64_t)n}, value.options().dtype(at::kByte));
+  const int rc = ops3d_fda_backward_offsets(ptr(value), vhm, shapes.data_ptr<int64_t>(), lsi.data_ptr<int64_t>(),
+                                            ptr(offset_attn), reference_points.data_ptr<float>(), R, ptr(grad_output),
+                                            ptr(grad_value), ptr(grad_oa),
+                                            want_ref_grad ? grad_ref.data_ptr<float>() : nullptr, ptr(ws), n, z.code, z.B, z.S, z.G, z.D,
+                                            z.L, z.Q, z.K, (int)im2col_step, stream_of(value));
+  if (rc != OPS3D_FDA_OK) raise(rc, "flash_deform_attn_backward_offsets failed");
+  return {grad_value, grad_oa, grad_ref};
+}
+
 // reference csrc/flash_deform_attn.h:7-25 (d_stride, block_thread and use_reg are launch hints
 // of the CUDA build; the gfx950 library chooses its own geometry)
 at::Tensor flash_deform_attn_forward(const at::Tensor &value, const at::Tensor &shapes, const at::Tensor &lsi,
@@ -173,4 +237,6 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("block_thread") = 0);
   m.def("forward_keep_head_major", &forward_keep_head_major, "forward that also returns its workspace");
   m.def("backward_with_head_major", &backward_with_head_major, "backward reusing the forward workspace");
+  m.def("forward_offsets", &forward_offsets, "forward from offsets and reference points");
+  m.def("backward_offsets", &backward_offsets, "backward of forward_offsets");
 }

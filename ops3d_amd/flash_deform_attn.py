@@ -120,6 +120,45 @@ class FlashDeformAttnFunction(Function):
         return grad_value, None, None, grad_sampling_loc_attn, None, None, None
 
 
+class FlashDeformAttnFromOffsets(Function):
+    """Caller-side fusion of the op's producer and consumer (offset mode, no counterpart in the
+    reference).  ``offset_attn`` [B,Q,G,4*L*K] has the packed planar layout of
+    sampling_loc_attn, but its L*K (x,y,z) triples are offsets in voxels of their level: it is
+    the output of one linear projection of the query, used as is.  The kernels form
+    ``loc = reference_points + offset / (W, H, D)_level`` in fp32 (``reference_points``
+    [B,Q,1 or L,3] float32, (x,y,z) in [0,1]), so the caller's add, divide and torch.cat passes
+    (reference tests/test_flash_deform_attn.py:30-37) and their backward split disappear.
+    Gradients: value, offset_attn (offsets and logits in its layout) and, when it requires
+    grad, reference_points (the sum over heads and points of offset gradient * level size,
+    added up in the kernels)."""
+
+    @staticmethod
+    def forward(ctx, value, value_spatial_shapes, value_level_start_index, offset_attn, reference_points,
+                im2col_step, K=8):
+        if _C is None:
+            raise RuntimeError(
+                "ops3d_amd native library (libops3d_fda.so) not built; FlashDeformAttnFromOffsets requires it."
+            )
+        ctx.K = K
+        ctx.im2col_step = im2col_step
+        output, value_hm = _C.forward_offsets(
+            value, value_spatial_shapes, value_level_start_index, offset_attn, reference_points, im2col_step, K
+        )
+        ctx.save_for_backward(value, value_spatial_shapes, value_level_start_index, offset_attn, reference_points,
+                              value_hm)
+        return output
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, grad_output):
+        value, shapes, lsi, offset_attn, ref, value_hm = ctx.saved_tensors
+        grad_value, grad_oa, grad_ref = _C.backward_offsets(
+            value, value_hm, shapes, lsi, offset_attn, ref, grad_output.contiguous(), ctx.im2col_step, ctx.K,
+            bool(ctx.needs_input_grad[4]),
+        )
+        return grad_value, None, None, grad_oa, grad_ref, None, None
+
+
 def ms_deform_attn_core_pytorch_3d(value, value_spatial_shapes, sampling_locations, attention_weights):
     """PyTorch path of 3-D deformable attention (reference ops3d/flash_deform_attn.py:139-165).
 

@@ -146,3 +146,17 @@ def test_noalloc_refuses_large_problems_before_device_work(lib):
     # argument errors first
     rc = lib.ops3d_fda_backward_noalloc(p, p, p, p, p, p, p, 2, 1, 576, 8, 32, 6, 576, 4, 64, None)
     assert rc == 1 and b"invalid number of scales" in lib.ops3d_fda_last_error()
+
+
+def test_offsets_argument_errors_before_device_work(lib):
+    p = ctypes.c_void_p(256)
+    args = (2, 1, 576, 8, 32, 2, 576, 4, 64, None)   # dtype, B, S, G, D, L, Q, K, step, stream
+    rc = lib.ops3d_fda_forward_offsets(p, p, p, p, None, 1, p, None, 0, *args)
+    assert rc == 1 and b"reference_points is NULL" in lib.ops3d_fda_last_error()
+    rc = lib.ops3d_fda_forward_offsets(p, p, p, p, p, 3, p, None, 0, *args)
+    assert rc == 1 and b"ref_levels must be 1 or num_levels" in lib.ops3d_fda_last_error()
+    rc = lib.ops3d_fda_backward_offsets(p, None, p, p, p, p, 3, p, p, p, None, None, 0, *args)
+    assert rc == 1 and b"ref_levels must be 1 or num_levels" in lib.ops3d_fda_last_error()
+    # nothing to do (Q = 0): no check of the reference points, success
+    rc = lib.ops3d_fda_forward_offsets(p, p, p, p, None, 1, p, None, 0, 2, 1, 576, 8, 32, 2, 0, 4, 64, None)
+    assert rc == 0
