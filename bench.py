@@ -217,6 +217,40 @@ def measure_offsets(w, steps, warmup, device):
     return {"fused": b.time_loop(fused, steps, warmup), "unfused": b.time_loop(unfused, steps, warmup)}
 
 
+def measure_nms(n, steps, warmup, device, threshold=0.3, cpu=True):
+    """3-D NMS over n clustered boxes (a few hundred clusters, extents 2-12, scores with ties):
+    the whole _C.nms_3d call (sort, IoU mask, greedy pass, the kept count read back), and the
+    float32 CPU oracle on the same boxes."""
+    import numpy as np
+    import torch
+
+    from ops3d_amd import _C
+
+    r = np.random.default_rng(0)
+    centres = r.uniform(0, 100, size=(max(1, n // 20), 3))
+    c = centres[r.integers(0, len(centres), n)] + r.normal(0, 3.0, size=(n, 3))
+    e = r.uniform(2.0, 12.0, size=(n, 3))
+    boxes = np.concatenate([c - e / 2, c + e / 2], 1).astype(np.float32)
+    scores = np.round(r.uniform(0, 1, n), 2).astype(np.float32)
+    b = torch.from_numpy(boxes).to(device)
+    s = torch.from_numpy(scores).to(device)
+    kept = []
+
+    def call():
+        kept.append(_C.nms_3d(b, s, threshold).numel())
+
+    bb = Bench.__new__(Bench)
+    bb.torch = torch
+    res = {"n": n, "gpu": bb.time_loop(call, steps, warmup), "kept": kept[-1]}
+    if cpu:
+        from oracle import nms3d as O
+
+        t0 = time.perf_counter()
+        O.nms3d(boxes, scores, threshold)
+        res["cpu_ms"] = (time.perf_counter() - t0) * 1e3
+    return res
+
+
 def measure(w, dtype, steps, warmup, device, with_kernels=True, fwd_only=False):
     b = Bench(w, dtype, device)
     res = {"workload": w.name, "dtype": dtype}
@@ -337,6 +371,7 @@ def main():
     ap.add_argument("--json-out", default=None, help="write all results as JSON to this path")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the per-kernel loops of --config (for profilers); prints no JSON line")
+    ap.add_argument("--nms", action="store_true", help="only 3-D NMS at 4k, 16k and 64k boxes (stderr)")
     ap.add_argument("--offsets", action="store_true",
                     help="only the offset-mode op against the unfused caller at --config (stderr)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -369,6 +404,14 @@ def main():
         torch.cuda.synchronize()
         log(f"copied {args.copy_calibration} MiB 5 times")
         return
+    if args.nms or args.all:
+        for n in (4096, 16384, 65536):
+            o = measure_nms(n, args.steps, args.warmup, dev, cpu=n <= 16384)
+            cpu = f" | CPU oracle (numpy fp32, 1 core) {o['cpu_ms']:9.1f} ms" if "cpu_ms" in o else ""
+            log(f" nms3d n={n:6d} | GPU {o['gpu']['median'] * 1e3:9.1f} us per call (sort + mask + greedy + count), "
+                f"kept {o['kept']}{cpu}")
+        if args.nms:
+            return
     if args.offsets:
         o = measure_offsets(WORKLOADS[args.config], args.steps, args.warmup, dev)
         log(f" {args.config} offsets | fwd+bwd fused (FlashDeformAttnFromOffsets) {o['fused']['median'] * 1e3:8.1f} us"

@@ -40,6 +40,8 @@ EXPORTED_SYMBOLS = (
     "ops3d_fda_backward_noalloc",
     "ops3d_fda_forward_offsets",
     "ops3d_fda_backward_offsets",
+    "ops3d_nms3d_workspace_bytes",
+    "ops3d_nms3d",
     "ops3d_fda_profile_enable",
     "ops3d_fda_profile_read",
 )
@@ -73,6 +75,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ops3d_fda_forward_offsets.restype = _i
     lib.ops3d_fda_forward_offsets.argtypes = [_vp] * 5 + [_i] + [_vp] * 2 + [_sz] + [_i] * 9 + [_vp]
     lib.ops3d_fda_backward_offsets.restype = _i
+    lib.ops3d_nms3d_workspace_bytes.restype = _sz
+    lib.ops3d_nms3d_workspace_bytes.argtypes = [_i]
+    lib.ops3d_nms3d.restype = _i
+    lib.ops3d_nms3d.argtypes = [_vp, _vp, _i, ctypes.c_float, _vp, _sz, _vp, _vp, _vp]
     lib.ops3d_fda_backward_offsets.argtypes = [_vp] * 6 + [_i] + [_vp] * 5 + [_sz] + [_i] * 9 + [_vp]
 
 
@@ -98,7 +104,7 @@ class _NativeFDA:
         if ext is not None:
             for name in ("flash_deform_attn_forward", "flash_deform_attn_backward",
                          "forward_keep_head_major", "backward_with_head_major",
-                         "forward_offsets", "backward_offsets"):
+                         "forward_offsets", "backward_offsets", "nms_3d"):
                 setattr(self, name, getattr(ext, name))
 
     # -- helpers ---------------------------------------------------------------------------
@@ -345,6 +351,34 @@ class _NativeFDA:
         if rc != OPS3D_FDA_OK:
             self._raise(rc, "flash_deform_attn_backward_noalloc failed")
         return [grad_value, grad_sla]
+
+    def nms_3d(self, dets, scores, threshold):
+        """3-D NMS (reference csrc/nms_3d.h:27-44): dets [N,6] (x1,y1,z1,x2,y2,z2), scores [N]
+        -> int64 indices of the kept boxes, in decreasing score order (ties in index order)."""
+        if not dets.is_cuda:
+            raise RuntimeError("Not compiled with CPU support")
+        if dets.numel() == 0:
+            return torch.empty(0, dtype=torch.long, device=dets.device)
+        if dets.dim() != 2 or dets.shape[1] != 6:
+            raise ValueError("dets must be [N, 6] (x1,y1,z1,x2,y2,z2)")
+        if scores.dim() != 1 or scores.shape[0] != dets.shape[0] or scores.device != dets.device:
+            raise ValueError("scores must be [N] on the boxes' device")
+        order = torch.sort(scores, stable=True, descending=True)[1]
+        boxes = dets.index_select(0, order).to(torch.float32).contiguous()
+        n = boxes.shape[0]
+        wsb = self._lib.ops3d_nms3d_workspace_bytes(n)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dets.device)
+        keep = torch.empty(n, dtype=torch.long, device=dets.device)
+        num = torch.empty(1, dtype=torch.int32, device=dets.device)
+        stream = torch.cuda.current_stream(dets.device).cuda_stream
+        with torch.cuda.device(dets.device):
+            rc = self._lib.ops3d_nms3d(_ptr(boxes), _ptr(order), n, float(threshold), _ptr(ws), wsb, _ptr(keep),
+                                       _ptr(num), stream)
+        if rc == OPS3D_FDA_EINVAL:
+            raise ValueError("nms_3d: too many boxes (at most 2^19)")
+        if rc != OPS3D_FDA_OK:
+            raise RuntimeError("nms_3d: kernel launch failed")
+        return keep[: int(num.item())]
 
     def profile_enable(self, on: bool = True) -> None:
         """Record HIP events around the backward phases of every following call."""

@@ -19,6 +19,7 @@
 #include <tuple>
 
 #include "../../include/ops3d_fda.h"
+#include "../../include/ops3d_nms3d.h"
 
 namespace {
 
@@ -224,6 +225,31 @@ std::vector<at::Tensor> flash_deform_attn_backward(const at::Tensor &value, cons
   return backward_with_head_major(value, c10::nullopt, shapes, lsi, sla, grad_output, im2col_step, K);
 }
 
+// reference csrc/nms_3d.h:27-44 -> nms_3d_cuda (csrc/cuda/nms_3d_cuda.cu:105-162): boxes [N,6]
+// (x1,y1,z1,x2,y2,z2) and scores [N] on the GPU -> int64 indices of the kept boxes in
+// decreasing score order.  Ties in score keep index order (a stable sort).  The kept count is
+// read back to size the result (the reference synchronises too).
+at::Tensor nms_3d(const at::Tensor &dets, const at::Tensor &scores, double threshold) {
+  if (!dets.is_cuda()) throw std::runtime_error("Not compiled with CPU support");
+  if (dets.numel() == 0) return at::empty({0}, dets.options().dtype(at::kLong));
+  if (dets.dim() != 2 || dets.size(1) != 6) throw std::invalid_argument("dets must be [N, 6] (x1,y1,z1,x2,y2,z2)");
+  if (scores.dim() != 1 || scores.size(0) != dets.size(0) || scores.device() != dets.device())
+    throw std::invalid_argument("scores must be [N] on the boxes' device");
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(dets.device());
+  const at::Tensor order = std::get<1>(scores.sort(/*stable=*/true, /*dim=*/0, /*descending=*/true));
+  const at::Tensor boxes = dets.index_select(0, order).to(at::kFloat).contiguous();
+  const int n = (int)boxes.size(0);
+  const size_t wsb = ops3d_nms3d_workspace_bytes(n);
+  at::Tensor ws = at::empty({(int64_t)wsb}, dets.options().dtype(at::kByte));
+  at::Tensor keep = at::empty({n}, dets.options().dtype(at::kLong));
+  at::Tensor num = at::empty({1}, dets.options().dtype(at::kInt));
+  const int rc = ops3d_nms3d(boxes.data_ptr<float>(), order.data_ptr<int64_t>(), n, (float)threshold, ws.data_ptr(),
+                             wsb, keep.data_ptr<int64_t>(), num.data_ptr<int32_t>(), stream_of(dets));
+  if (rc == OPS3D_FDA_EINVAL) throw std::invalid_argument("nms_3d: too many boxes (at most 2^19)");
+  if (rc != OPS3D_FDA_OK) throw std::runtime_error("nms_3d: kernel launch failed");
+  return keep.narrow(0, 0, num.item<int32_t>());
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -239,4 +265,5 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("backward_with_head_major", &backward_with_head_major, "backward reusing the forward workspace");
   m.def("forward_offsets", &forward_offsets, "forward from offsets and reference points");
   m.def("backward_offsets", &backward_offsets, "backward of forward_offsets");
+  m.def("nms_3d", &nms_3d, "non-maximum suppression for 3d");
 }

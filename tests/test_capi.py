@@ -9,12 +9,12 @@ import re
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "ops3d_fda.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in sorted(os.listdir(os.path.join(ROOT, "include")))]
 
 
 def _declared():
-    text = open(HEADER).read()
-    return sorted(set(re.findall(r"OPS3D_FDA_API\s+[\w\s\*]*?\b(ops3d_fda_\w+)\s*\(", text)))
+    text = "".join(open(h).read() for h in HEADERS)
+    return sorted(set(re.findall(r"OPS3D_FDA_API\s+[\w\s\*]*?\b(ops3d_\w+)\s*\(", text)))
 
 
 @pytest.fixture(scope="module")
