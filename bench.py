@@ -251,6 +251,41 @@ def measure_nms(n, steps, warmup, device, threshold=0.3, cpu=True):
     return res
 
 
+def measure_roi_align(steps, warmup, device, dtype="bf16"):
+    """3-D RoI Align fwd and bwd: features [2, 256, 32, 64, 64], 512 rois of 4-32 voxels per
+    axis, 7x7x7 bins, sampling_ratio 2 (8 trilinear samples per bin), linear order."""
+    import numpy as np
+    import torch
+
+    from ops3d_amd.roi_align import roi_align_3d
+
+    dt = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[dtype]
+    N, C, D, H, W, R = 2, 256, 32, 64, 64, 512
+    g = torch.Generator(device=device).manual_seed(0)
+    x = torch.randn(N, C, D, H, W, generator=g, device=device).to(dt).requires_grad_(True)
+    r = np.random.default_rng(0)
+    ext = r.uniform(4, 32, size=(R, 3))
+    lo = r.uniform(0, 1, size=(R, 3)) * (np.array([W, H, D]) - ext)
+    rois = torch.from_numpy(np.concatenate([r.integers(0, N, (R, 1)), lo, lo + ext], 1).astype(np.float32))
+    rois = rois.to(device).to(dt)
+    pooled = (7, 7, 7)
+    gout = torch.randn(R, C, *pooled, generator=g, device=device).to(dt)
+
+    def fwd():
+        with torch.no_grad():
+            roi_align_3d(x, rois, pooled, 1.0, 2, 1)
+
+    def step():
+        x.grad = None
+        roi_align_3d(x, rois, pooled, 1.0, 2, 1).backward(gout)
+
+    b = Bench.__new__(Bench)
+    b.torch = torch
+    out_bytes = R * C * 343 * x.element_size()
+    return {"fwd": b.time_loop(fwd, steps, warmup), "step": b.time_loop(step, steps, warmup),
+            "samples": R * C * 343 * 8, "out_bytes": out_bytes}
+
+
 def measure(w, dtype, steps, warmup, device, with_kernels=True, fwd_only=False):
     b = Bench(w, dtype, device)
     res = {"workload": w.name, "dtype": dtype}
@@ -372,6 +407,7 @@ def main():
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the per-kernel loops of --config (for profilers); prints no JSON line")
     ap.add_argument("--nms", action="store_true", help="only 3-D NMS at 4k, 16k and 64k boxes (stderr)")
+    ap.add_argument("--roi", action="store_true", help="only 3-D RoI Align fwd and fwd+bwd (stderr)")
     ap.add_argument("--offsets", action="store_true",
                     help="only the offset-mode op against the unfused caller at --config (stderr)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -404,6 +440,13 @@ def main():
         torch.cuda.synchronize()
         log(f"copied {args.copy_calibration} MiB 5 times")
         return
+    if args.roi or args.all:
+        o = measure_roi_align(args.steps, args.warmup, dev)
+        f, st = o["fwd"]["median"], o["step"]["median"]
+        log(f" roi_align3d bf16 [2,256,32,64,64] x 512 rois, 7^3 bins, 8 samples | fwd {f * 1e3:8.1f} us "
+            f"({o['samples'] / f / 1e6:.3g} G samples/s) | fwd+bwd {st * 1e3:8.1f} us")
+        if args.roi:
+            return
     if args.nms or args.all:
         for n in (4096, 16384, 65536):
             o = measure_nms(n, args.steps, args.warmup, dev, cpu=n <= 16384)

@@ -1,0 +1,50 @@
+/*
+ * C ABI of 3-D RoI Align in libops3d_fda.so (gfx950).  Replaces roi_align_3d_forward /
+ * roi_align_3d_backward (reference csrc/roi_align_3d.h:97-136 -> csrc/cuda/roi_align_3d_cuda.cu:
+ * 22-74 -> csrc/cuda/roi_align_3d_cuda_kernel.cuh:27-220), bound as _C.roi_align_3d_forward /
+ * _C.roi_align_3d_backward (csrc/vision.cpp:17-18).  Device pointers, sizes, a hipStream_t as
+ * void*; asynchronous; return codes as in ops3d_fda.h; dtype OPS3D_FDA_F32 / F16 / BF16.
+ */
+#ifndef OPS3D_ROI_ALIGN3D_H
+#define OPS3D_ROI_ALIGN3D_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "ops3d_fda.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/*
+ * Forward.  features [N,C,D,H,W], rois [R,7] (batch index, x1, y1, z1, x2, y2, z2) in the same
+ * dtype, output [R,C,PD,PH,PW] (every element written).  Per bin: the roi scaled by
+ * spatial_scale, extents clamped to >= 1, sampling_ratio samples per axis (<= 0: ceil(extent /
+ * pooled)), each sample interpolated (order 1: trilinear with the reference's edge handling;
+ * order 0: nearest corner) and the samples averaged, in fp32.
+ */
+OPS3D_FDA_API int ops3d_roi_align3d_forward(const void *features, const void *rois, void *output, int dtype, int N,
+                                            int C, int D, int H, int W, int R, int PD, int PH, int PW,
+                                            float spatial_scale, int sampling_ratio, int order, void *stream);
+
+/* Bytes of fp32 workspace ops3d_roi_align3d_backward needs: 0 for fp32 (it accumulates in
+ * grad_input itself), N*C*D*H*W*4 for 16-bit types. */
+OPS3D_FDA_API size_t ops3d_roi_align3d_backward_workspace_bytes(int dtype, int N, int C, int D, int H, int W);
+
+/*
+ * Backward: grad_input [N,C,D,H,W] = the adjoint of the forward applied to grad_output
+ * [R,C,PD,PH,PW]; every element of grad_input is written (cleared, then the samples' corner
+ * contributions added by fp32 atomics, whose order -- and so the last bit -- can differ
+ * between runs, as with the reference's atomics).
+ */
+OPS3D_FDA_API int ops3d_roi_align3d_backward(const void *grad_output, const void *rois, void *grad_input,
+                                             void *workspace, size_t workspace_bytes, int dtype, int N, int C, int D,
+                                             int H, int W, int R, int PD, int PH, int PW, float spatial_scale,
+                                             int sampling_ratio, int order, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OPS3D_ROI_ALIGN3D_H */

@@ -18,7 +18,7 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_NAME = "libops3d_fda.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 TORCH_EXT_NAME = "_fda_torch"
-SOURCES = ["fda_capi.hip", "fda_tiles.hip", "fda_f32.hip", "fda_f16.hip", "fda_bf16.hip", "nms3d.hip"]
+SOURCES = ["fda_capi.hip", "fda_tiles.hip", "fda_f32.hip", "fda_f16.hip", "fda_bf16.hip", "nms3d.hip", "roi_align3d.hip"]
 ARCH = "gfx950"
 
 # -packed-fp32-ops off: hipcc must not form v_pk_{add,mul,fma}_f32 on its own.

@@ -42,6 +42,9 @@ EXPORTED_SYMBOLS = (
     "ops3d_fda_backward_offsets",
     "ops3d_nms3d_workspace_bytes",
     "ops3d_nms3d",
+    "ops3d_roi_align3d_forward",
+    "ops3d_roi_align3d_backward_workspace_bytes",
+    "ops3d_roi_align3d_backward",
     "ops3d_fda_profile_enable",
     "ops3d_fda_profile_read",
 )
@@ -79,6 +82,12 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ops3d_nms3d_workspace_bytes.argtypes = [_i]
     lib.ops3d_nms3d.restype = _i
     lib.ops3d_nms3d.argtypes = [_vp, _vp, _i, ctypes.c_float, _vp, _sz, _vp, _vp, _vp]
+    lib.ops3d_roi_align3d_forward.restype = _i
+    lib.ops3d_roi_align3d_forward.argtypes = [_vp] * 3 + [_i] * 10 + [ctypes.c_float, _i, _i, _vp]
+    lib.ops3d_roi_align3d_backward_workspace_bytes.restype = _sz
+    lib.ops3d_roi_align3d_backward_workspace_bytes.argtypes = [_i] * 6
+    lib.ops3d_roi_align3d_backward.restype = _i
+    lib.ops3d_roi_align3d_backward.argtypes = [_vp] * 4 + [_sz] + [_i] * 10 + [ctypes.c_float, _i, _i, _vp]
     lib.ops3d_fda_backward_offsets.argtypes = [_vp] * 6 + [_i] + [_vp] * 5 + [_sz] + [_i] * 9 + [_vp]
 
 
@@ -104,7 +113,8 @@ class _NativeFDA:
         if ext is not None:
             for name in ("flash_deform_attn_forward", "flash_deform_attn_backward",
                          "forward_keep_head_major", "backward_with_head_major",
-                         "forward_offsets", "backward_offsets", "nms_3d"):
+                         "forward_offsets", "backward_offsets", "nms_3d", "roi_align_3d_forward",
+                         "roi_align_3d_backward"):
                 setattr(self, name, getattr(ext, name))
 
     # -- helpers ---------------------------------------------------------------------------
@@ -379,6 +389,59 @@ class _NativeFDA:
         if rc != OPS3D_FDA_OK:
             raise RuntimeError("nms_3d: kernel launch failed")
         return keep[: int(num.item())]
+
+    @staticmethod
+    def _roi_checks(data, rois, other):
+        if not data.is_cuda:
+            raise RuntimeError("RoIAlign is not implemented on CPU")
+        if rois.dim() != 2 or rois.shape[1] != 7:
+            raise RuntimeError("wrong roi size! size_rois should be 7")
+        for t in (rois, other):
+            if t.device != data.device:
+                raise RuntimeError("RoIAlign tensors must be on one device")
+            if t.dtype != data.dtype:
+                raise ValueError("RoIAlign tensors must share a dtype")
+        if not other.is_contiguous():
+            raise RuntimeError("RoIAlign output tensor has to be contiguous")
+        if data.dtype not in _DTYPE_CODE:
+            raise ValueError(f"unsupported dtype {data.dtype}")
+        return _DTYPE_CODE[data.dtype]
+
+    def roi_align_3d_forward(self, features, rois, output, out_d, out_h, out_w, spatial_scale, sampling_ratio, order):
+        """RoI Align 3-D forward into `output` [R, C, out_d, out_h, out_w] (reference
+        csrc/roi_align_3d.h:97-115)."""
+        code = self._roi_checks(features, rois, output)
+        f, r = features.contiguous(), rois.contiguous()
+        N, C, D, H, W = f.shape
+        if tuple(output.shape) != (r.shape[0], C, out_d, out_h, out_w):
+            raise ValueError("output must be [R, C, out_d, out_h, out_w]")
+        with torch.cuda.device(f.device):
+            rc = self._lib.ops3d_roi_align3d_forward(
+                _ptr(f), _ptr(r), _ptr(output), code, N, C, D, H, W, r.shape[0], out_d, out_h, out_w,
+                float(spatial_scale), int(sampling_ratio), int(order), torch.cuda.current_stream(f.device).cuda_stream)
+        if rc == OPS3D_FDA_EINVAL:
+            raise ValueError("roi_align_3d_forward: invalid sizes or order")
+        if rc != OPS3D_FDA_OK:
+            raise RuntimeError("roi_align_3d_forward: kernel launch failed")
+
+    def roi_align_3d_backward(self, top_grad, rois, bottom_grad, out_d, out_h, out_w, spatial_scale, sampling_ratio,
+                              order):
+        """RoI Align 3-D backward into `bottom_grad` [N, C, D, H, W], every element written
+        (reference csrc/roi_align_3d.h:117-136)."""
+        code = self._roi_checks(top_grad, rois, bottom_grad)
+        g, r = top_grad.contiguous(), rois.contiguous()
+        N, C, D, H, W = bottom_grad.shape
+        wsb = self._lib.ops3d_roi_align3d_backward_workspace_bytes(code, N, C, D, H, W)
+        ws = torch.empty(wsb // 4, dtype=torch.float32, device=g.device) if wsb else None
+        with torch.cuda.device(g.device):
+            rc = self._lib.ops3d_roi_align3d_backward(
+                _ptr(g), _ptr(r), _ptr(bottom_grad), _ptr(ws), wsb, code, N, C, D, H, W, r.shape[0], out_d, out_h,
+                out_w, float(spatial_scale), int(sampling_ratio), int(order),
+                torch.cuda.current_stream(g.device).cuda_stream)
+        if rc == OPS3D_FDA_EINVAL:
+            raise ValueError("roi_align_3d_backward: invalid sizes or order")
+        if rc != OPS3D_FDA_OK:
+            raise RuntimeError("roi_align_3d_backward: kernel launch failed")
 
     def profile_enable(self, on: bool = True) -> None:
         """Record HIP events around the backward phases of every following call."""

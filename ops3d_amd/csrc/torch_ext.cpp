@@ -20,6 +20,7 @@
 
 #include "../../include/ops3d_fda.h"
 #include "../../include/ops3d_nms3d.h"
+#include "../../include/ops3d_roi_align3d.h"
 
 namespace {
 
@@ -250,6 +251,56 @@ at::Tensor nms_3d(const at::Tensor &dets, const at::Tensor &scores, double thres
   return keep.narrow(0, 0, num.item<int32_t>());
 }
 
+// RoI Align 3-D (reference csrc/roi_align_3d.h:35-136): shared checks; returns the dtype code.
+int roi_checks(const at::Tensor &data, const at::Tensor &rois, const at::Tensor &other) {
+  if (!data.is_cuda()) throw std::runtime_error("RoIAlign is not implemented on CPU");
+  if (rois.dim() != 2 || rois.size(1) != 7) throw std::runtime_error("wrong roi size! size_rois should be 7");
+  for (const at::Tensor *t : {&rois, &other}) {
+    if (t->device() != data.device()) throw std::runtime_error("RoIAlign tensors must be on one device");
+    if (t->scalar_type() != data.scalar_type()) throw std::invalid_argument("RoIAlign tensors must share a dtype");
+  }
+  if (!other.is_contiguous()) throw std::runtime_error("RoIAlign output tensor has to be contiguous");
+  return dtype_code(data);
+}
+
+void roi_align_3d_forward(const at::Tensor &input, const at::Tensor &rois, at::Tensor output, int64_t pd, int64_t ph,
+                          int64_t pw, double spatial_scale, int64_t sampling_ratio, int64_t order) {
+  const int code = roi_checks(input, rois, output);
+  if (input.dim() != 5) throw std::invalid_argument("features must be [N, C, D, H, W]");
+  const at::Tensor f = input.contiguous(), r = rois.contiguous();
+  if (output.dim() != 5 || output.size(0) != r.size(0) || output.size(1) != f.size(1) || output.size(2) != pd ||
+      output.size(3) != ph || output.size(4) != pw)
+    throw std::invalid_argument("output must be [R, C, out_d, out_h, out_w]");
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(input.device());
+  const int rc = ops3d_roi_align3d_forward(ptr(f), ptr(r), ptr(output), code, (int)f.size(0), (int)f.size(1),
+                                           (int)f.size(2), (int)f.size(3), (int)f.size(4), (int)r.size(0), (int)pd,
+                                           (int)ph, (int)pw, (float)spatial_scale, (int)sampling_ratio, (int)order,
+                                           stream_of(input));
+  if (rc == OPS3D_FDA_EINVAL) throw std::invalid_argument("roi_align_3d_forward: invalid sizes or order");
+  if (rc != OPS3D_FDA_OK) throw std::runtime_error("roi_align_3d_forward: kernel launch failed");
+}
+
+void roi_align_3d_backward(const at::Tensor &top_grad, const at::Tensor &rois, at::Tensor bottom_grad, int64_t pd,
+                           int64_t ph, int64_t pw, double spatial_scale, int64_t sampling_ratio, int64_t order) {
+  const int code = roi_checks(top_grad, rois, bottom_grad);
+  if (bottom_grad.dim() != 5) throw std::invalid_argument("bottom_grad must be [N, C, D, H, W]");
+  const at::Tensor g = top_grad.contiguous(), r = rois.contiguous();
+  const int N = (int)bottom_grad.size(0), C = (int)bottom_grad.size(1), D = (int)bottom_grad.size(2),
+            H = (int)bottom_grad.size(3), W = (int)bottom_grad.size(4);
+  if (g.dim() != 5 || g.size(0) != r.size(0) || g.size(1) != C || g.size(2) != pd || g.size(3) != ph ||
+      g.size(4) != pw)
+    throw std::invalid_argument("top_grad must be [R, C, out_d, out_h, out_w]");
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(top_grad.device());
+  const size_t wsb = ops3d_roi_align3d_backward_workspace_bytes(code, N, C, D, H, W);
+  at::Tensor ws;
+  if (wsb) ws = at::empty({(int64_t)(wsb / 4)}, top_grad.options().dtype(at::kFloat));
+  const int rc = ops3d_roi_align3d_backward(ptr(g), ptr(r), ptr(bottom_grad), ptr(ws), wsb, code, N, C, D, H, W,
+                                            (int)r.size(0), (int)pd, (int)ph, (int)pw, (float)spatial_scale,
+                                            (int)sampling_ratio, (int)order, stream_of(top_grad));
+  if (rc == OPS3D_FDA_EINVAL) throw std::invalid_argument("roi_align_3d_backward: invalid sizes or order");
+  if (rc != OPS3D_FDA_OK) throw std::runtime_error("roi_align_3d_backward: kernel launch failed");
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -266,4 +317,6 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("forward_offsets", &forward_offsets, "forward from offsets and reference points");
   m.def("backward_offsets", &backward_offsets, "backward of forward_offsets");
   m.def("nms_3d", &nms_3d, "non-maximum suppression for 3d");
+  m.def("roi_align_3d_forward", &roi_align_3d_forward, "roi_align_3d_forward");
+  m.def("roi_align_3d_backward", &roi_align_3d_backward, "roi_align_3d_backward");
 }

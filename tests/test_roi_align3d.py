@@ -1,0 +1,141 @@
+"""3-D RoI Align: the CPU oracle pinned (closed forms, nearest rounding, the adjoint identity,
+batch-index guard) and the GPU kernels against it (marked gpu).
+
+The reference ships no RoI Align tests; its semantics are those of
+csrc/cuda/roi_align_3d_cuda_kernel.cuh:27-220 and csrc/cuda/interpolation_helpers_3d.h:25-260."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import roi_align3d as O
+
+
+def _rois(R, N, size, seed, lo=-2.0, hi=None):
+    r = np.random.default_rng(seed)
+    D, H, W = size
+    hi = hi if hi is not None else max(D, H, W) + 2.0
+    p = r.uniform(lo, hi, size=(R, 2, 3))
+    a, b = np.minimum(p[:, 0], p[:, 1]), np.maximum(p[:, 0], p[:, 1])
+    bi = r.integers(0, N, size=(R, 1)).astype(np.float64)
+    return np.concatenate([bi, a, b], 1).astype(np.float32)   # (b, x1, y1, z1, x2, y2, z2)
+
+
+# --- oracle pinning (CPU) --------------------------------------------------------------------
+def test_constant_and_linear_fields():
+    N, C, D, H, W = 1, 2, 8, 9, 10
+    z, y, x = np.meshgrid(np.arange(D), np.arange(H), np.arange(W), indexing="ij")
+    lin = 0.5 * x + 0.25 * y - 0.75 * z + 3.0
+    feat = np.stack([np.full((D, H, W), 2.5), lin])[None]
+    # rois well inside [0, size-1] on every axis (x 1..8, y 1..7, z 1..6): every sample interpolates
+    rois = np.array([[0, 1.0, 1.0, 1.0, 8.0, 7.0, 6.0], [0, 2.2, 1.5, 1.25, 5.0, 6.5, 4.75]], np.float32)
+    for sr in (1, 2, 3):
+        out = O.forward(feat, rois, (3, 2, 4), 1.0, sr)
+        assert np.allclose(out[:, 0], 2.5)
+        for r in range(2):
+            x1, y1, z1, x2, y2, z2 = rois[r, 1:]
+            for pd in range(3):
+                for ph in range(2):
+                    for pw in range(4):
+                        cx = x1 + (pw + 0.5) * (x2 - x1) / 4
+                        cy = y1 + (ph + 0.5) * (y2 - y1) / 2
+                        cz = z1 + (pd + 0.5) * (z2 - z1) / 3
+                        want = 0.5 * cx + 0.25 * cy - 0.75 * cz + 3.0   # linear: mean = value at the centre
+                        assert abs(out[r, 1, pd, ph, pw] - want) < 1e-5
+
+
+def test_nearest_rounds_half_down_and_clamps():
+    D = H = W = 4
+    feat = np.arange(D * H * W, dtype=np.float64).reshape(1, 1, D, H, W)
+    # one sample per bin at the roi centre: roi [c - 0.5, c + 0.5] -> sample at c
+    def at(x, y, z):
+        roi = np.array([[0, x - 0.5, y - 0.5, z - 0.5, x + 0.5, y + 0.5, z + 0.5]], np.float32)
+        return O.forward(feat, roi, (1, 1, 1), 1.0, 1, order=0)[0, 0, 0, 0, 0]
+    assert at(1.3, 2.0, 0.0) == (0 * H + 2) * W + 1      # x frac .3 -> x0
+    assert at(1.5, 2.0, 0.0) == (0 * H + 2) * W + 1      # .5 -> x0 (hx >= .5 is tested first)
+    assert at(1.7, 2.0, 0.0) == (0 * H + 2) * W + 2      # .7 -> x1
+    assert at(3.4, 3.9, 2.6) == (3 * H + 3) * W + 3      # beyond size-1: clamped to the last voxel
+    assert at(-0.6, 0.0, 0.0) == 0                       # below 0 (but >= -1): clamped to 0
+
+
+def test_out_of_range_samples_and_batch_guard():
+    feat = np.ones((1, 1, 4, 4, 4))
+    # a roi entirely beyond the volume (samples > size) reads nothing
+    far = np.array([[0, 10, 10, 10, 12, 12, 12]], np.float32)
+    assert np.all(O.forward(feat, far, (2, 2, 2), 1.0, 2) == 0)
+    bad = np.array([[3, 0, 0, 0, 2, 2, 2]], np.float32)      # batch index 3 of 1
+    assert np.all(O.forward(feat, bad, (2, 2, 2), 1.0, 2) == 0)
+
+
+@pytest.mark.parametrize("order,sr", [(1, 0), (1, 2), (0, 1)])
+def test_adjoint_identity(order, sr):
+    """The backward is the adjoint of the (linear) forward: <F(x), g> == <x, B(g)>."""
+    r = np.random.default_rng(order * 10 + sr)
+    shape = (2, 3, 5, 6, 7)
+    x = r.normal(size=shape)
+    rois = _rois(6, 2, shape[2:], seed=5)
+    pooled = (2, 3, 2)
+    g = r.normal(size=(6, 3) + pooled)
+    lhs = float(np.sum(O.forward(x, rois, pooled, 0.9, sr, order) * g))
+    rhs = float(np.sum(x * O.backward(g, rois, shape, 0.9, sr, order)))
+    assert abs(lhs - rhs) < 1e-9 * max(1.0, abs(lhs))
+
+
+# --- GPU ---------------------------------------------------------------------------------------
+CASES = [
+    # N, C, (D, H, W), R, pooled, scale, sampling_ratio, order, dtype
+    (2, 8, (8, 12, 16), 20, (3, 3, 3), 1.0, 2, 1, torch.float32),
+    (2, 8, (8, 12, 16), 20, (2, 3, 4), 0.5, 0, 1, torch.float32),       # adaptive grid
+    (1, 3, (5, 6, 7), 15, (2, 2, 2), 1.0, 1, 0, torch.float32),         # nearest, C % 4 != 0
+    (2, 16, (10, 10, 10), 30, (4, 4, 4), 1.0, 2, 1, torch.bfloat16),
+    (1, 4, (6, 8, 8), 12, (3, 2, 2), 2.0, 0, 1, torch.float16),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", range(len(CASES)))
+def test_gpu_matches_oracle(gpu_device, case):
+    from fda_helpers import TOL, assert_close, log
+
+    from ops3d_amd.roi_align import roi_align_3d
+
+    N, C, size, R, pooled, scale, sr, order, dt = CASES[case]
+    log(f"[case] roi_align3d #{case}: N={N} C={C} size={size} R={R} pooled={pooled} sr={sr} order={order} {dt}")
+    r = np.random.default_rng(case)
+    x = torch.from_numpy(r.normal(size=(N, C) + size).astype(np.float32)).to(dt)
+    rois_np = _rois(R, N, tuple(int(v / scale) for v in size), seed=100 + case)
+    rois = torch.from_numpy(rois_np).to(dt)
+    xg = x.to(gpu_device).requires_grad_(True)
+    out = roi_align_3d(xg, rois.to(gpu_device), pooled, scale, sr, order)
+    g = torch.from_numpy(r.normal(size=tuple(out.shape)).astype(np.float32)).to(dt)
+    out.backward(g.to(gpu_device))
+    torch.cuda.synchronize()
+    want = O.forward(x.double().numpy(), rois.double().numpy(), pooled, scale, sr, order)
+    gwant = O.backward(g.double().numpy(), rois.double().numpy(), x.shape, scale, sr, order)
+    rtol, atol = TOL[dt]
+    assert out.dtype == dt and tuple(out.shape) == (R, C) + pooled
+    assert_close("roi_align output", out.detach(), want, rtol, atol)
+    # gradients: fp32 sums of up to count * 8 terms per voxel, added by atomics in any order
+    assert_close("roi_align grad", xg.grad, gwant, rtol, atol * (10 if dt == torch.float32 else 1))
+
+
+@pytest.mark.gpu
+def test_gpu_module_edges(gpu_device):
+    from ops3d_amd import _C
+    from ops3d_amd.roi_align import RoIAlign
+
+    m = RoIAlign((2, 2, 2), 1.0, 2)
+    x = torch.randn(1, 4, 4, 4, 4, device=gpu_device)
+    rois = torch.tensor([[0, 0, 0, 0, 3, 3, 3], [5, 0, 0, 0, 3, 3, 3]], dtype=torch.float32, device=gpu_device)
+    out = m(x, rois)
+    torch.cuda.synchronize()
+    assert torch.all(out[1] == 0)                                    # batch index 5 of 1: nothing
+    want = O.forward(x.cpu().double().numpy(), rois.cpu().numpy(), (2, 2, 2), 1.0, 2)
+    assert np.allclose(out.cpu().numpy(), want, rtol=1e-5, atol=1e-6)
+    empty = m(x, torch.zeros(0, 7, device=gpu_device))
+    assert tuple(empty.shape) == (0, 4, 2, 2, 2)
+    with pytest.raises(RuntimeError, match="CPU"):
+        _C.roi_align_3d_forward(x.cpu(), rois.cpu(), torch.empty(2, 4, 2, 2, 2), 2, 2, 2, 1.0, 2, 1)
+    with pytest.raises(RuntimeError, match="size_rois should be 7"):
+        _C.roi_align_3d_forward(x, rois[:, :6], torch.empty(2, 4, 2, 2, 2, device=gpu_device), 2, 2, 2, 1.0, 2, 1)
