@@ -286,6 +286,37 @@ def measure_roi_align(steps, warmup, device, dtype="bf16"):
             "samples": R * C * 343 * 8, "out_bytes": out_bytes}
 
 
+def measure_dcnv4(steps, warmup, device, dtype="bf16"):
+    """DCNv4-3D fwd and fwd+bwd: value [2, 32, 64, 64, 256] (G 8 x D 32), 3x3x3 kernel, stride 1,
+    pad 1, softmax over the 27 masks, offsets ~N(0, 1) voxels."""
+    import torch
+
+    from ops3d_amd.dcnv4 import dcnv4_3d
+
+    dt = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[dtype]
+    B, D_, H_, W_, G, D = 2, 32, 64, 64, 8, 32
+    K = 27
+    padded = (G * 4 * K + 7) // 8 * 8
+    g = torch.Generator(device=device).manual_seed(0)
+    value = torch.randn(B, D_, H_, W_, G * D, generator=g, device=device).to(dt).requires_grad_(True)
+    off = torch.randn(B, D_, H_, W_, padded, generator=g, device=device).to(dt).requires_grad_(True)
+    gout = torch.randn(B, D_, H_, W_, G * D, generator=g, device=device).to(dt)
+    args = ((3, 3, 3), (1, 1, 1), (1, 1, 1), (1, 1, 1), G, D, 1.0, 64, 0, True)
+
+    def fwd():
+        with torch.no_grad():
+            dcnv4_3d(value, off, *args)
+
+    def step():
+        value.grad = off.grad = None
+        dcnv4_3d(value, off, *args).backward(gout)
+
+    b = Bench.__new__(Bench)
+    b.torch = torch
+    return {"fwd": b.time_loop(fwd, steps, warmup), "step": b.time_loop(step, steps, warmup),
+            "samples": B * D_ * H_ * W_ * G * K}
+
+
 def measure(w, dtype, steps, warmup, device, with_kernels=True, fwd_only=False):
     b = Bench(w, dtype, device)
     res = {"workload": w.name, "dtype": dtype}
@@ -408,6 +439,7 @@ def main():
                     help="only the per-kernel loops of --config (for profilers); prints no JSON line")
     ap.add_argument("--nms", action="store_true", help="only 3-D NMS at 4k, 16k and 64k boxes (stderr)")
     ap.add_argument("--roi", action="store_true", help="only 3-D RoI Align fwd and fwd+bwd (stderr)")
+    ap.add_argument("--dcn", action="store_true", help="only DCNv4-3D fwd and fwd+bwd (stderr)")
     ap.add_argument("--offsets", action="store_true",
                     help="only the offset-mode op against the unfused caller at --config (stderr)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -440,6 +472,13 @@ def main():
         torch.cuda.synchronize()
         log(f"copied {args.copy_calibration} MiB 5 times")
         return
+    if args.dcn or args.all:
+        o = measure_dcnv4(args.steps, args.warmup, dev)
+        f, st = o["fwd"]["median"], o["step"]["median"]
+        log(f" dcnv4_3d bf16 [2,32,64,64,8x32] 3^3 taps, softmax | fwd {f * 1e3:8.1f} us "
+            f"({o['samples'] / f / 1e6:.3g} G samples/s) | fwd+bwd {st * 1e3:8.1f} us")
+        if args.dcn:
+            return
     if args.roi or args.all:
         o = measure_roi_align(args.steps, args.warmup, dev)
         f, st = o["fwd"]["median"], o["step"]["median"]

@@ -40,6 +40,9 @@ EXPORTED_SYMBOLS = (
     "ops3d_fda_backward_noalloc",
     "ops3d_fda_forward_offsets",
     "ops3d_fda_backward_offsets",
+    "ops3d_dcnv4_workspace_bytes",
+    "ops3d_dcnv4_forward",
+    "ops3d_dcnv4_backward",
     "ops3d_nms3d_workspace_bytes",
     "ops3d_nms3d",
     "ops3d_roi_align3d_forward",
@@ -78,6 +81,12 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ops3d_fda_forward_offsets.restype = _i
     lib.ops3d_fda_forward_offsets.argtypes = [_vp] * 5 + [_i] + [_vp] * 2 + [_sz] + [_i] * 9 + [_vp]
     lib.ops3d_fda_backward_offsets.restype = _i
+    lib.ops3d_dcnv4_workspace_bytes.restype = _sz
+    lib.ops3d_dcnv4_workspace_bytes.argtypes = [_i] * 21
+    lib.ops3d_dcnv4_forward.restype = _i
+    lib.ops3d_dcnv4_forward.argtypes = [_vp] * 4 + [_sz] + [_i] * 19 + [ctypes.c_float] + [_i] * 4 + [_vp]
+    lib.ops3d_dcnv4_backward.restype = _i
+    lib.ops3d_dcnv4_backward.argtypes = [_vp] * 6 + [_sz] + [_i] * 19 + [ctypes.c_float] + [_i] * 4 + [_vp]
     lib.ops3d_nms3d_workspace_bytes.restype = _sz
     lib.ops3d_nms3d_workspace_bytes.argtypes = [_i]
     lib.ops3d_nms3d.restype = _i
@@ -114,7 +123,7 @@ class _NativeFDA:
             for name in ("flash_deform_attn_forward", "flash_deform_attn_backward",
                          "forward_keep_head_major", "backward_with_head_major",
                          "forward_offsets", "backward_offsets", "nms_3d", "roi_align_3d_forward",
-                         "roi_align_3d_backward"):
+                         "roi_align_3d_backward", "dcnv4_forward", "dcnv4_backward"):
                 setattr(self, name, getattr(ext, name))
 
     # -- helpers ---------------------------------------------------------------------------
@@ -442,6 +451,66 @@ class _NativeFDA:
             raise ValueError("roi_align_3d_backward: invalid sizes or order")
         if rc != OPS3D_FDA_OK:
             raise RuntimeError("roi_align_3d_backward: kernel launch failed")
+
+    def _dcn(self, value, p_offset, group, group_channels):
+        if not value.is_cuda:
+            raise RuntimeError("Not implemented on the CPU")
+        if not p_offset.is_cuda:
+            raise RuntimeError("offset must be a CUDA tensor")
+        if not value.is_contiguous() or not p_offset.is_contiguous():
+            raise RuntimeError("input tensor has to be contiguous")
+        if value.dim() != 5 or p_offset.dim() != 5:
+            raise ValueError("value and p_offset must be 5-D")
+        if p_offset.dtype != value.dtype or value.dtype not in _DTYPE_CODE:
+            raise ValueError("p_offset dtype differs from value (or unsupported dtype)")
+        if value.shape[4] != group * group_channels:
+            raise RuntimeError("Input channels and group times group channels dont match")
+        return _DTYPE_CODE[value.dtype]
+
+    def dcnv4_forward(self, value, p_offset, kd, kh, kw, sd, sh, sw, pd, ph, pw, dd, dh, dw, group, group_channels,
+                      offset_scale, im2col_step, remove_center, d_stride=8, block_thread=0, softmax=False):
+        """DCNv4-3D forward (reference csrc/dcnv4.h:7-32): value [B,Din,Hin,Win,G*D], p_offset
+        [B,Dout,Hout,Wout,padded] -> output [B,Dout,Hout,Wout,G*D]."""
+        code = self._dcn(value, p_offset, group, group_channels)
+        B, Din, Hin, Win, _ = value.shape
+        geo = [int(v) for v in (kd, kh, kw, sd, sh, sw, pd, ph, pw, dd, dh, dw)]
+        outs = [(n + 2 * p - (d * (k - 1) + 1)) // s + 1 for n, k, s, p, d in
+                zip((Din, Hin, Win), geo[0:3], geo[3:6], geo[6:9], geo[9:12])]
+        out = torch.empty((B, *outs, group * group_channels), dtype=value.dtype, device=value.device)
+        wsb = self._lib.ops3d_dcnv4_workspace_bytes(code, B, Din, Hin, Win, group, group_channels, *geo,
+                                                   int(remove_center), 0)
+        ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=value.device)
+        with torch.cuda.device(value.device):
+            rc = self._lib.ops3d_dcnv4_forward(
+                _ptr(value), _ptr(p_offset), _ptr(out), _ptr(ws), wsb, code, B, Din, Hin, Win, group,
+                group_channels, *geo, float(offset_scale), int(remove_center), 1 if softmax else 0,
+                p_offset.shape[4], int(im2col_step), torch.cuda.current_stream(value.device).cuda_stream)
+        if rc != OPS3D_FDA_OK:
+            self._raise(rc, "dcnv4_forward failed")
+        return out
+
+    def dcnv4_backward(self, value, p_offset, kd, kh, kw, sd, sh, sw, pd, ph, pw, dd, dh, dw, group,
+                       group_channels, offset_scale, im2col_step, grad_output, remove_center, d_stride=8,
+                       block_thread=0, softmax=False):
+        """DCNv4-3D backward (reference csrc/dcnv4.h:34-60) -> [grad_value, grad_offset]."""
+        code = self._dcn(value, p_offset, group, group_channels)
+        B, Din, Hin, Win, _ = value.shape
+        geo = [int(v) for v in (kd, kh, kw, sd, sh, sw, pd, ph, pw, dd, dh, dw)]
+        grad_value = torch.empty_like(value)
+        grad_offset = torch.zeros_like(p_offset)
+        wsb = self._lib.ops3d_dcnv4_workspace_bytes(code, B, Din, Hin, Win, group, group_channels, *geo,
+                                                   int(remove_center), 1)
+        ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=value.device)
+        go = grad_output.contiguous()
+        with torch.cuda.device(value.device):
+            rc = self._lib.ops3d_dcnv4_backward(
+                _ptr(value), _ptr(p_offset), _ptr(go), _ptr(grad_value), _ptr(grad_offset), _ptr(ws), wsb, code, B,
+                Din, Hin, Win, group, group_channels, *geo, float(offset_scale), int(remove_center),
+                1 if softmax else 0, p_offset.shape[4], int(im2col_step),
+                torch.cuda.current_stream(value.device).cuda_stream)
+        if rc != OPS3D_FDA_OK:
+            self._raise(rc, "dcnv4_backward failed")
+        return [grad_value, grad_offset]
 
     def profile_enable(self, on: bool = True) -> None:
         """Record HIP events around the backward phases of every following call."""

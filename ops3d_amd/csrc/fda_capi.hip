@@ -21,6 +21,7 @@
 #include <mutex>
 #include <string>
 
+#include "../../include/ops3d_dcnv4.h"
 #include "../../include/ops3d_fda.h"
 #include "fda_device.h"
 
@@ -105,13 +106,45 @@ struct Geometry {
   int cpl, lpu;
 };
 
+// DCNv4-3D convolution geometry (reference dcnv4_cuda.cu:20-91): output size per axis
+// (in + 2 pad - (dil (k - 1) + 1)) / stride + 1, K = kd kh kw taps (minus the centre).
+constexpr int kDcnMaxTaps = 128;
+struct DcnConv {
+  int kd, kh, kw, sd, sh, sw, pd, ph, pw, dd, dh, dw;
+  float scale;
+  int remove_center, softmax, rec_stride;
+  int Din, Hin, Win, Dout, Hout, Wout, K;
+  bool init(int D_, int H_, int W_) {
+    Din = D_; Hin = H_; Win = W_;
+    if (kd < 1 || kh < 1 || kw < 1 || sd < 1 || sh < 1 || sw < 1 || dd < 1 || dh < 1 || dw < 1 || pd < 0 ||
+        ph < 0 || pw < 0)
+      return false;
+    Dout = (Din + 2 * pd - (dd * (kd - 1) + 1)) / sd + 1;
+    Hout = (Hin + 2 * ph - (dh * (kh - 1) + 1)) / sh + 1;
+    Wout = (Win + 2 * pw - (dw * (kw - 1) + 1)) / sw + 1;
+    K = kd * kh * kw - (remove_center ? 1 : 0);
+    return Dout > 0 && Hout > 0 && Wout > 0 && K >= 1 && K <= kDcnMaxTaps;
+  }
+  void apply(Args &a) const {
+    a.dcn = 1;
+    a.dcn_softmax = softmax ? 1 : 0;
+    a.dcn_remove_center = remove_center ? 1 : 0;
+    a.rec_stride = rec_stride;
+    a.kd = kd; a.kh = kh; a.kw = kw; a.sd = sd; a.sh = sh; a.sw = sw; a.pd = pd; a.ph = ph; a.pw = pw;
+    a.dld = dd; a.dlh = dh; a.dlw = dw;
+    a.Dout = Dout; a.Hout = Hout; a.Wout = Wout;
+    a.offset_scale = scale;
+  }
+};
+
 int common_checks(int dtype, int B, int S, int G, int D, int L, int Q, int K, int step,
-                  bool backward, Geometry &geo) {
+                  bool backward, Geometry &geo, int max_k = 16) {
   if (elem_size(dtype) == 0) return fail(OPS3D_FDA_EINVAL, "unsupported dtype code %d", dtype);
   if (B < 0 || S < 0 || G <= 0 || D <= 0 || Q < 0)
     return fail(OPS3D_FDA_EINVAL, "invalid sizes B=%d S=%d G=%d D=%d Q=%d", B, S, G, D, Q);
   if (L < 1 || L > 5) return fail(OPS3D_FDA_EINVAL, "invalid number of scales L=%d (supported 1..5)", L);
-  if (K < 1 || K > 16) return fail(OPS3D_FDA_EINVAL, "invalid number of points K=%d (supported 1..16)", K);
+  if (K < 1 || K > max_k)
+    return fail(OPS3D_FDA_EINVAL, "invalid number of points K=%d (supported 1..%d)", K, max_k);
   if (step <= 0) return fail(OPS3D_FDA_EINVAL, "im2col_step must be positive, got %d", step);
   const int step_ = B < step ? B : step;
   if (B > 0 && B % step_ != 0)
@@ -483,10 +516,10 @@ static int backward_impl(const void *value, const void *value_head_major, const 
                          int dtype, int batch, int spatial_size, int num_heads, int channels,
                          int num_levels, int num_query, int num_point, int im2col_step,
                          hipStream_t st, const float *ref = nullptr, int ref_levels = 0,
-                         float *grad_ref = nullptr) {
+                         float *grad_ref = nullptr, const DcnConv *dcn = nullptr) {
   Geometry geo;
   int rc = common_checks(dtype, batch, spatial_size, num_heads, channels, num_levels, num_query,
-                         num_point, im2col_step, true, geo);
+                         num_point, im2col_step, true, geo, dcn ? kDcnMaxTaps : 16);
   if (rc) return rc;
   BwdLayout ly;
   rc = bwd_layout(batch, spatial_size, num_heads, channels, elem_size(dtype),
@@ -526,6 +559,7 @@ static int backward_impl(const void *value, const void *value_head_major, const 
   a.ref = ref;
   a.ref_levels = ref_levels;
   a.grad_ref = grad_ref;
+  if (dcn) dcn->apply(a);
   a.grad_out = grad_output;
   a.grad_loc_attn = grad_sampling_loc_attn;
   a.keys = keys;
@@ -741,6 +775,117 @@ int ops3d_fda_backward_offsets(const void *value, const void *value_head_major, 
                        grad_value, false, grad_offset_attn, workspace, workspace_bytes, dtype, batch, spatial_size,
                        num_heads, channels, num_levels, num_query, num_point, im2col_step,
                        static_cast<hipStream_t>(stream), reference_points, ref_levels, grad_reference_points);
+}
+
+// ----------------------------------------------------------------------------------------------
+// DCNv4-3D (reference csrc/dcnv4.h:7-60 -> csrc/cuda/dcnv4_cuda.cu:20-189): the same kernels in
+// DCN mode (one level = the input volume, records of K offset triples and K mask values per
+// group in rows of padded_offset_dim, pixel coordinates formed in the kernels).  The level's
+// spatial_shapes / level_start_index, which the kernels read from device memory, are written
+// into the first 256 bytes of the workspace by a one-thread kernel (no host copy).
+
+__global__ void dcn_meta_kernel(int64_t *meta, int D, int H, int W) {
+  meta[0] = D;
+  meta[1] = H;
+  meta[2] = W;
+  meta[3] = 0;
+}
+
+static int dcn_setup(DcnConv &c, int dtype, int batch, int din, int hin, int win, int group, int group_channels,
+                     int kd, int kh, int kw, int sd, int sh, int sw, int pd, int ph, int pw, int dd, int dh, int dw,
+                     float offset_scale, int remove_center, int softmax, int padded_offset_dim) {
+  c.kd = kd; c.kh = kh; c.kw = kw; c.sd = sd; c.sh = sh; c.sw = sw; c.pd = pd; c.ph = ph; c.pw = pw;
+  c.dd = dd; c.dh = dh; c.dw = dw;
+  c.scale = offset_scale;
+  c.remove_center = remove_center;
+  c.softmax = softmax;
+  c.rec_stride = padded_offset_dim;
+  if (elem_size(dtype) == 0) return fail(OPS3D_FDA_EINVAL, "unsupported dtype code %d", dtype);
+  if (batch < 0 || din < 1 || hin < 1 || win < 1 || group < 1 || group_channels < 1)
+    return fail(OPS3D_FDA_EINVAL, "invalid sizes");
+  if (!c.init(din, hin, win))
+    return fail(OPS3D_FDA_EINVAL, "invalid kernel / stride / pad / dilation (or more than %d taps)", kDcnMaxTaps);
+  if (padded_offset_dim < group * 4 * c.K)
+    return fail(OPS3D_FDA_EINVAL, "padded_offset_dim %d smaller than group * 4 * K = %d", padded_offset_dim,
+                group * 4 * c.K);
+  return OPS3D_FDA_OK;
+}
+
+size_t ops3d_dcnv4_workspace_bytes(int dtype, int batch, int din, int hin, int win, int group, int group_channels,
+                                   int kd, int kh, int kw, int sd, int sh, int sw, int pd, int ph, int pw, int dd,
+                                   int dh, int dw, int remove_center, int backward) {
+  DcnConv c;
+  const std::string saved = g_last_error;
+  const int rc = dcn_setup(c, dtype, batch, din, hin, win, group, group_channels, kd, kh, kw, sd, sh, sw, pd, ph, pw,
+                           dd, dh, dw, 1.f, remove_center, 0, 1 << 30);
+  g_last_error = saved;
+  if (rc) return 0;
+  if (!backward) return 256;
+  int cpl = 0, lpu = 0;
+  if (!pick_config(dtype, group_channels, cpl, lpu)) return 0;
+  BwdLayout ly;
+  if (bwd_layout(batch, din * hin * win, group, group_channels, elem_size(dtype),
+                 tile_lanes(lpu, cpl * elem_size(dtype)), 1, c.Dout * c.Hout * c.Wout, c.K, ly)) {
+    g_last_error = saved;
+    return 0;
+  }
+  return 256 + ly.total;
+}
+
+int ops3d_dcnv4_forward(const void *value, const void *offset, void *output, void *workspace, size_t workspace_bytes,
+                        int dtype, int batch, int din, int hin, int win, int group, int group_channels, int kd, int kh,
+                        int kw, int sd, int sh, int sw, int pd, int ph, int pw, int dd, int dh, int dw,
+                        float offset_scale, int remove_center, int softmax, int padded_offset_dim, int im2col_step,
+                        void *stream) {
+  g_last_error.clear();
+  DcnConv c;
+  int rc = dcn_setup(c, dtype, batch, din, hin, win, group, group_channels, kd, kh, kw, sd, sh, sw, pd, ph, pw, dd, dh,
+                     dw, offset_scale, remove_center, softmax, padded_offset_dim);
+  if (rc) return rc;
+  const int Q = c.Dout * c.Hout * c.Wout;
+  Geometry geo;
+  rc = common_checks(dtype, batch, din * hin * win, group, group_channels, 1, Q, c.K, im2col_step, false, geo,
+                     kDcnMaxTaps);
+  if (rc) return rc;
+  if (batch == 0) return OPS3D_FDA_OK;
+  if (!value || !offset || !output || !workspace) return fail(OPS3D_FDA_EINVAL, "NULL pointer argument");
+  if (workspace_bytes < 256 || (reinterpret_cast<uintptr_t>(workspace) & 255u))
+    return fail(OPS3D_FDA_EINVAL, "workspace must be at least 256 bytes, 256-byte aligned");
+  if (misaligned(value) || misaligned(offset) || misaligned(output))
+    return fail(OPS3D_FDA_EINVAL, "tensor data pointers must be 4-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int64_t *meta = static_cast<int64_t *>(workspace);
+  hipLaunchKernelGGL(dcn_meta_kernel, dim3(1), dim3(1), 0, st, meta, din, hin, win);
+  geo.a.value = value;
+  geo.a.shapes = meta;
+  geo.a.lsi = meta + 3;
+  geo.a.loc_attn = offset;
+  geo.a.out = output;
+  c.apply(geo.a);
+  hipError_t e = launch(dtype, 0, geo, st);
+  if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "dcnv4 forward launch failed: %s", hipGetErrorString(e));
+  return OPS3D_FDA_OK;
+}
+
+int ops3d_dcnv4_backward(const void *value, const void *offset, const void *grad_output, void *grad_value,
+                         void *grad_offset, void *workspace, size_t workspace_bytes, int dtype, int batch, int din,
+                         int hin, int win, int group, int group_channels, int kd, int kh, int kw, int sd, int sh,
+                         int sw, int pd, int ph, int pw, int dd, int dh, int dw, float offset_scale,
+                         int remove_center, int softmax, int padded_offset_dim, int im2col_step, void *stream) {
+  g_last_error.clear();
+  DcnConv c;
+  int rc = dcn_setup(c, dtype, batch, din, hin, win, group, group_channels, kd, kh, kw, sd, sh, sw, pd, ph, pw, dd, dh,
+                     dw, offset_scale, remove_center, softmax, padded_offset_dim);
+  if (rc) return rc;
+  if (!workspace || workspace_bytes < 256 || (reinterpret_cast<uintptr_t>(workspace) & 255u))
+    return fail(OPS3D_FDA_EINVAL, "workspace must be at least 256 bytes, 256-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int64_t *meta = static_cast<int64_t *>(workspace);
+  hipLaunchKernelGGL(dcn_meta_kernel, dim3(1), dim3(1), 0, st, meta, din, hin, win);
+  return backward_impl(value, nullptr, meta, meta + 3, offset, grad_output, grad_value, false, grad_offset,
+                       static_cast<unsigned char *>(workspace) + 256, workspace_bytes - 256, dtype, batch,
+                       din * hin * win, group, group_channels, 1, c.Dout * c.Hout * c.Wout, c.K, im2col_step, st,
+                       nullptr, 0, nullptr, &c);
 }
 
 }  // extern "C"

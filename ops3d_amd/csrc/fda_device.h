@@ -43,6 +43,13 @@ struct Args {
                               // voxels of their level (NULL: normalised locations)
   int ref_levels;             // 1 (one point per query) or L (one per level)
   float *grad_ref;            // offset mode, backward: [B,Q,ref_levels,3] fp32, added into (NULL: none)
+  // DCNv4-3D mode (dcn != 0): one level (the input volume), Q = Dout*Hout*Wout output voxels;
+  // unit (b, q, g)'s record sits at loc_attn + (b*Q + q) * rec_stride + g * P (rows padded to
+  // rec_stride); its L*K triples are offsets, turned into pixel coordinates in the kernels
+  // (dcn_to_pixels); the softmax over the K mask values is optional (dcn_softmax)
+  int dcn, dcn_softmax, dcn_remove_center, rec_stride;
+  int kd, kh, kw, sd, sh, sw, pd, ph, pw, dld, dlh, dlw, Dout, Hout, Wout;
+  float offset_scale;
   const void *grad_out;       // [B,Q,G*D] T          (backward)
   void *out;                  // [B,Q,G*D] T          (forward)
   float *grad_value;          // [B,S,G,D] fp32 acc   (backward)
@@ -347,6 +354,38 @@ __device__ __forceinline__ void add_ref_grad(const Args &a, int64_t bq, int j, c
   }
 }
 
+// Element offset of unit (b*Q + q)*G + g's record in loc_attn / grad_loc_attn: P per unit, or
+// (DCNv4-3D) rows of rec_stride per (b, q).
+__device__ __forceinline__ int64_t record_offset(const Args &a, int64_t unit) {
+  return a.rec_stride ? (unit / a.G) * a.rec_stride + (unit % a.G) * a.P : unit * a.P;
+}
+
+// DCNv4-3D mode: turn the staged offsets of unit (b, q) into pixel coordinates of the input
+// volume (reference dcnv4_im2col_cuda.cuh:144-196):  with (z, y, x) the output voxel of q,
+//     p0 = ((dil * (k - 1)) >> 1) - pad + pos * stride,  p0' = p0 - ((dil * (k - 1)) >> 1) * scale,
+//     pixel = p0' + (tap * dil + offset) * scale   per axis,
+// in fp32 step by step (no contraction).  Sample s is the s-th kernel tap in the order x (w)
+// outermost, y, z innermost, skipping the centre tap when remove_center is set.
+template <int LPU>
+__device__ __forceinline__ void dcn_to_pixels(const Args &a, int q, int j, float *rec) {
+#pragma clang fp contract(off)
+  const int K = a.K;
+  const int xo = q % a.Wout, yo = (q / a.Wout) % a.Hout, zo = q / (a.Wout * a.Hout);
+  const int hw = (a.dlw * (a.kw - 1)) >> 1, hh = (a.dlh * (a.kh - 1)) >> 1, hd = (a.dld * (a.kd - 1)) >> 1;
+  const float s = a.offset_scale;
+  const float p0w = (float)(hw - a.pw + xo * a.sw) - (float)hw * s;
+  const float p0h = (float)(hh - a.ph + yo * a.sh) - (float)hh * s;
+  const float p0d = (float)(hd - a.pd + zo * a.sd) - (float)hd * s;
+  const int centre = ((a.kw / 2) * a.kh + a.kh / 2) * a.kd + a.kd / 2;
+  for (int t = j; t < K; t += LPU) {
+    const int tap = (a.dcn_remove_center && t >= centre) ? t + 1 : t;
+    const int i = tap / (a.kh * a.kd), jj = (tap / a.kd) % a.kh, k = tap % a.kd;
+    rec[3 * t] = p0w + ((float)(i * a.dlw) + rec[3 * t]) * s;
+    rec[3 * t + 1] = p0h + ((float)(jj * a.dlh) + rec[3 * t + 1]) * s;
+    rec[3 * t + 2] = p0d + ((float)(k * a.dld) + rec[3 * t + 2]) * s;
+  }
+}
+
 // Write one unit's record (P fp32 values in LDS) to global memory as T.
 template <typename T, int LPU>
 __device__ __forceinline__ void write_record(T *rec_g, int P, int j, const float *rec) {
@@ -528,12 +567,15 @@ struct SampleBase {
 // such a sample gets base corner (-2, -2, -2), so all its loads are out of range and read zero,
 // and zero weights, so it contributes nothing -- as with zero padding.  Returns whether the
 // sample is inside.
+// pix: the coordinates are pixel coordinates already (DCNv4-3D), and the range is the
+// reference DCN's open (-1, size) (at exactly -1 a sample reads 0 either way).
 __device__ __forceinline__ bool sample_base(float lx, float ly, float lz, int Wl, int Hl, int Dl,
-                                            SampleBase &sb) {
-  const float x = pixel_coord(lx, (float)Wl);
-  const float y = pixel_coord(ly, (float)Hl);
-  const float z = pixel_coord(lz, (float)Dl);
-  const bool in = x >= -1.f && y >= -1.f && z >= -1.f && x < (float)Wl && y < (float)Hl && z < (float)Dl;
+                                            SampleBase &sb, bool pix = false) {
+  const float x = pix ? lx : pixel_coord(lx, (float)Wl);
+  const float y = pix ? ly : pixel_coord(ly, (float)Hl);
+  const float z = pix ? lz : pixel_coord(lz, (float)Dl);
+  const bool in = (pix ? (x > -1.f && y > -1.f && z > -1.f) : (x >= -1.f && y >= -1.f && z >= -1.f)) &&
+                  x < (float)Wl && y < (float)Hl && z < (float)Dl;
   const float x0f = floorf(x), y0f = floorf(y), z0f = floorf(z);
   sb.x0 = in ? (int)x0f : -2; sb.y0 = in ? (int)y0f : -2; sb.z0 = in ? (int)z0f : -2;
   sb.wx1 = in ? x - x0f : 0.f; sb.wx0 = in ? (x0f + 1.f) - x : 0.f;
@@ -567,9 +609,9 @@ __device__ __forceinline__ void sample_expand(const SampleBase &sb, int Wl, int 
 
 // Both steps in one lane.  Always fills sm; returns whether the sample is inside the volume.
 __device__ __forceinline__ bool sample_setup(float lx, float ly, float lz, int Wl, int Hl, int Dl,
-                                             int GD, Sample &sm) {
+                                             int GD, Sample &sm, bool pix = false) {
   SampleBase sb;
-  const bool in = sample_base(lx, ly, lz, Wl, Hl, Dl, sb);
+  const bool in = sample_base(lx, ly, lz, Wl, Hl, Dl, sb, pix);
   sample_expand(sb, Wl, Hl, Dl, GD, sm);
   return in;
 }

@@ -95,13 +95,17 @@ __global__ __launch_bounds__(kBlock) void fda_forward_kernel(const Args a) {
   float *rec = lds + ub * (P + 1);
   const int64_t unit = ((int64_t)b * a.Q + (live ? q : 0)) * a.G + g;
 
-  stage_record<T, LPU>(static_cast<const T *>(a.loc_attn) + unit * P, P, j, live, rec);
+  stage_record<T, LPU>(static_cast<const T *>(a.loc_attn) + record_offset(a, unit), P, j, live, rec);
   wave_lds_sync();
   if (a.ref) {
     offsets_to_locations<T, LPU>(a, unit / a.G, j, live, rec);
     wave_lds_sync();
   }
-  unit_softmax<LPU>(rec + 3 * LK, LK, j);
+  if (a.dcn) {
+    dcn_to_pixels<LPU>(a, live ? q : 0, j, rec);
+    wave_lds_sync();
+  }
+  if (!a.dcn || a.dcn_softmax) unit_softmax<LPU>(rec + 3 * LK, LK, j);
   wave_lds_sync();
 
   float acc[CPL];
@@ -125,7 +129,7 @@ __global__ __launch_bounds__(kBlock) void fda_forward_kernel(const Args a) {
       const int kj = k0 + (j < NG ? j : 0);
       const int sj = l * K + (kj < K ? kj : K - 1);
       Sample ms;
-      sample_setup(rec[3 * sj], rec[3 * sj + 1], rec[3 * sj + 2], Wl, Hl, Dl, RST, ms);
+      sample_setup(rec[3 * sj], rec[3 * sj + 1], rec[3 * sj + 2], Wl, Hl, Dl, RST, ms, a.dcn != 0);
       if (!live) {   // a dead unit loads zeros
 #pragma unroll
         for (int c = 0; c < 8; ++c) ms.off[c] = OOB_ELEM;
@@ -195,13 +199,17 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kFwdWave
   float *rec = lds + ub * (P + 1);
   const int64_t unit = ((int64_t)b * a.Q + (live ? q : 0)) * a.G + g;
 
-  stage_record<T, UL>(static_cast<const T *>(a.loc_attn) + unit * P, P, ju, live, rec);
+  stage_record<T, UL>(static_cast<const T *>(a.loc_attn) + record_offset(a, unit), P, ju, live, rec);
   wave_lds_sync();
   if (a.ref) {
     offsets_to_locations<T, UL>(a, unit / a.G, ju, live, rec);
     wave_lds_sync();
   }
-  unit_softmax<UL>(rec + 3 * LK, LK, ju);
+  if (a.dcn) {
+    dcn_to_pixels<UL>(a, live ? q : 0, ju, rec);
+    wave_lds_sync();
+  }
+  if (!a.dcn || a.dcn_softmax) unit_softmax<UL>(rec + 3 * LK, LK, ju);
   wave_lds_sync();
 
   float acc[CPL];
@@ -227,7 +235,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kFwdWave
       const int kj = k0 + (ju & 3);
       const int sj = l * K + (kj < K ? kj : K - 1);
       Sample ms;
-      sample_setup(rec[3 * sj], rec[3 * sj + 1], rec[3 * sj + 2], Wl, Hl, Dl, RST, ms);
+      sample_setup(rec[3 * sj], rec[3 * sj + 1], rec[3 * sj + 2], Wl, Hl, Dl, RST, ms, a.dcn != 0);
       uint32_t off4[4];
       float w4[4];
       // corner weights times the sample's attention weight (made once per set-up, not per channel)
@@ -316,13 +324,17 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kQueryWa
   }
   __syncthreads();
 
-  stage_record<T, UL>(static_cast<const T *>(a.loc_attn) + unit * P, P, ju, live, rec);
+  stage_record<T, UL>(static_cast<const T *>(a.loc_attn) + record_offset(a, unit), P, ju, live, rec);
   wave_lds_sync();
   if (a.ref) {
     offsets_to_locations<T, UL>(a, unit / a.G, ju, live, rec);
     wave_lds_sync();
   }
-  unit_softmax<UL>(rec + 3 * LK, LK, ju);
+  if (a.dcn) {
+    dcn_to_pixels<UL>(a, live ? q : 0, ju, rec);
+    wave_lds_sync();
+  }
+  if (!a.dcn || a.dcn_softmax) unit_softmax<UL>(rec + 3 * LK, LK, ju);
   wave_lds_sync();
 
   constexpr int NW = CPL * (int)sizeof(T) / 4;
@@ -358,7 +370,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kQueryWa
       const bool have = kq < K;
       const int sj = l * K + (have ? kq : K - 1);
       Sample ms;
-      const bool in_s = sample_setup(rec[3 * sj], rec[3 * sj + 1], rec[3 * sj + 2], Wl, Hl, Dl, RST, ms) && live;
+      const bool in_s = sample_setup(rec[3 * sj], rec[3 * sj + 1], rec[3 * sj + 2], Wl, Hl, Dl, RST, ms, a.dcn != 0) && live;
       if (dxl == 0 && have) {
         cx_s[sj] = in_s ? (uint32_t)(ms.x0 + 1) : kKeyInvalid;
         cy_s[sj] = (uint32_t)(ms.y0 + 1);
@@ -412,10 +424,10 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kQueryWa
             const int su = l * K + k0 + u;
             const float at = rec[3 * LK + su];
             // d(pixel)/d(loc) = size (grid_sample: size/2 per unit of grid, grid = 2*loc - 1);
-            // offset mode: d(pixel)/d(offset) = 1
-            rec[3 * su] = gx * at * (a.ref ? 1.f : (float)Wl);
-            rec[3 * su + 1] = gy * at * (a.ref ? 1.f : (float)Hl);
-            rec[3 * su + 2] = gz * at * (a.ref ? 1.f : (float)Dl);
+            // offset mode: d(pixel)/d(offset) = 1; DCNv4-3D: d(pixel)/d(offset) = offset_scale
+            rec[3 * su] = gx * at * (a.dcn ? a.offset_scale : (a.ref ? 1.f : (float)Wl));
+            rec[3 * su + 1] = gy * at * (a.dcn ? a.offset_scale : (a.ref ? 1.f : (float)Hl));
+            rec[3 * su + 2] = gz * at * (a.dcn ? a.offset_scale : (a.ref ? 1.f : (float)Dl));
             gat_s[su] = ga;
           }
         }
@@ -456,13 +468,14 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kQueryWa
   float dot = 0.f;
   for (int t = ju; t < LK; t += UL) dot = fmaf(rec[3 * LK + t], gat_s[t], dot);
   dot = unit_sum<UL>(dot);
+  const bool raw_mask = a.dcn && !a.dcn_softmax;   // DCNv4-3D without softmax: d(mask) = d(attn)
   for (int t = ju; t < LK; t += UL) {
     const float at = rec[3 * LK + t];
-    rec[3 * LK + t] = at * (gat_s[t] - dot);
+    rec[3 * LK + t] = raw_mask ? gat_s[t] : at * (gat_s[t] - dot);
   }
   wave_lds_sync();
   if (live && a.grad_ref) add_ref_grad<UL>(a, unit / a.G, ju, rec);
-  if (live) write_record<T, UL>(static_cast<T *>(a.grad_loc_attn) + unit * P, P, ju, rec);
+  if (live) write_record<T, UL>(static_cast<T *>(a.grad_loc_attn) + record_offset(a, unit), P, ju, rec);
   clear_tile_counts(a);
 }
 
@@ -500,13 +513,17 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
   }
   __syncthreads();
 
-  stage_record<T, LPU>(static_cast<const T *>(a.loc_attn) + unit * P, P, j, live, rec);
+  stage_record<T, LPU>(static_cast<const T *>(a.loc_attn) + record_offset(a, unit), P, j, live, rec);
   wave_lds_sync();
   if (a.ref) {
     offsets_to_locations<T, LPU>(a, unit / a.G, j, live, rec);
     wave_lds_sync();
   }
-  unit_softmax<LPU>(rec + 3 * LK, LK, j);
+  if (a.dcn) {
+    dcn_to_pixels<LPU>(a, live ? q : 0, j, rec);
+    wave_lds_sync();
+  }
+  if (!a.dcn || a.dcn_softmax) unit_softmax<LPU>(rec + 3 * LK, LK, j);
   wave_lds_sync();
 
   // the unit's grad_output channels as raw words (dot products run on the packed elements)
@@ -549,7 +566,7 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
         const float lx = rec[3 * su], ly = rec[3 * su + 1], lz = rec[3 * su + 2];
         at[u] = rec[3 * LK + su];
         // branch-free: a sample outside the volume (or of a dead unit) loads zeros, weighs zero
-        in[u] = sample_setup(lx, ly, lz, Wl, Hl, Dl, RST, sm[u]) && live && u < nk;
+        in[u] = sample_setup(lx, ly, lz, Wl, Hl, Dl, RST, sm[u], a.dcn != 0) && live && u < nk;
         if (!live || u >= nk) {
 #pragma unroll
           for (int c = 0; c < 8; ++c) sm[u].off[c] = OOB_ELEM;
@@ -589,10 +606,10 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
         if (j == 0 && u < nk) {
           const int su = s + u;
           // d(pixel)/d(loc) = size (grid_sample: size/2 per unit of grid, grid = 2*loc - 1);
-          // offset mode: d(pixel)/d(offset) = 1
-          rec[3 * su] = gx * at[u] * (a.ref ? 1.f : (float)Wl);
-          rec[3 * su + 1] = gy * at[u] * (a.ref ? 1.f : (float)Hl);
-          rec[3 * su + 2] = gz * at[u] * (a.ref ? 1.f : (float)Dl);
+          // offset mode: d(pixel)/d(offset) = 1; DCNv4-3D: d(pixel)/d(offset) = offset_scale
+          rec[3 * su] = gx * at[u] * (a.dcn ? a.offset_scale : (a.ref ? 1.f : (float)Wl));
+          rec[3 * su + 1] = gy * at[u] * (a.dcn ? a.offset_scale : (a.ref ? 1.f : (float)Hl));
+          rec[3 * su + 2] = gz * at[u] * (a.dcn ? a.offset_scale : (a.ref ? 1.f : (float)Dl));
           gat_s[su] = ga;
           cx_s[su] = in[u] ? (uint32_t)(m.x0 + 1) : kKeyInvalid;
           cy_s[su] = (uint32_t)(m.y0 + 1);
@@ -640,13 +657,14 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
   float dot = 0.f;
   for (int t = j; t < LK; t += LPU) dot = fmaf(rec[3 * LK + t], gat_s[t], dot);
   dot = unit_sum<LPU>(dot);
+  const bool raw_mask = a.dcn && !a.dcn_softmax;   // DCNv4-3D without softmax: d(mask) = d(attn)
   for (int t = j; t < LK; t += LPU) {
     const float at = rec[3 * LK + t];
-    rec[3 * LK + t] = at * (gat_s[t] - dot);
+    rec[3 * LK + t] = raw_mask ? gat_s[t] : at * (gat_s[t] - dot);
   }
   wave_lds_sync();
   if (live && a.grad_ref) add_ref_grad<LPU>(a, unit / a.G, j, rec);
-  if (live) write_record<T, LPU>(static_cast<T *>(a.grad_loc_attn) + unit * P, P, j, rec);
+  if (live) write_record<T, LPU>(static_cast<T *>(a.grad_loc_attn) + record_offset(a, unit), P, j, rec);
   clear_tile_counts(a);
 }
 

@@ -19,6 +19,7 @@
 #include <tuple>
 
 #include "../../include/ops3d_fda.h"
+#include "../../include/ops3d_dcnv4.h"
 #include "../../include/ops3d_nms3d.h"
 #include "../../include/ops3d_roi_align3d.h"
 
@@ -301,6 +302,77 @@ void roi_align_3d_backward(const at::Tensor &top_grad, const at::Tensor &rois, a
   if (rc != OPS3D_FDA_OK) throw std::runtime_error("roi_align_3d_backward: kernel launch failed");
 }
 
+// DCNv4-3D (reference csrc/dcnv4.h:7-60): value [B,Din,Hin,Win,G*D], p_offset
+// [B,Dout,Hout,Wout,padded]; d_stride and block_thread are launch hints of the CUDA build
+// (accepted, not used).
+struct DcnArgs {
+  int B, Din, Hin, Win, code;
+};
+
+DcnArgs dcn_check(const at::Tensor &value, const at::Tensor &p_offset, int64_t group, int64_t group_channels) {
+  if (!value.is_cuda()) throw std::runtime_error("Not implemented on the CPU");
+  if (!p_offset.is_cuda()) throw std::runtime_error("offset must be a CUDA tensor");
+  if (!value.is_contiguous()) throw std::runtime_error("input tensor has to be contiguous");
+  if (!p_offset.is_contiguous()) throw std::runtime_error("offset tensor has to be contiguous");
+  if (value.dim() != 5 || p_offset.dim() != 5) throw std::invalid_argument("value and p_offset must be 5-D");
+  if (p_offset.scalar_type() != value.scalar_type()) throw std::invalid_argument("p_offset dtype differs from value");
+  if (value.size(4) != group * group_channels)
+    throw std::runtime_error("Input channels and group times group channels dont match");
+  return {(int)value.size(0), (int)value.size(1), (int)value.size(2), (int)value.size(3), dtype_code(value)};
+}
+
+at::Tensor dcnv4_forward(const at::Tensor &value, const at::Tensor &p_offset, int64_t kd, int64_t kh, int64_t kw,
+                         int64_t sd, int64_t sh, int64_t sw, int64_t pd, int64_t ph, int64_t pw, int64_t dd,
+                         int64_t dh, int64_t dw, int64_t group, int64_t group_channels, double offset_scale,
+                         int64_t im2col_step, int64_t remove_center, int64_t /*d_stride*/, int64_t /*block_thread*/,
+                         bool softmax) {
+  const DcnArgs z = dcn_check(value, p_offset, group, group_channels);
+  const int Dout = (z.Din + 2 * (int)pd - ((int)dd * ((int)kd - 1) + 1)) / (int)sd + 1;
+  const int Hout = (z.Hin + 2 * (int)ph - ((int)dh * ((int)kh - 1) + 1)) / (int)sh + 1;
+  const int Wout = (z.Win + 2 * (int)pw - ((int)dw * ((int)kw - 1) + 1)) / (int)sw + 1;
+  if (p_offset.size(0) != z.B || p_offset.size(1) != Dout || p_offset.size(2) != Hout || p_offset.size(3) != Wout)
+    throw std::invalid_argument("p_offset must be [B, Dout, Hout, Wout, padded_offset_dim]");
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(value.device());
+  at::Tensor out = at::empty({z.B, Dout, Hout, Wout, group * group_channels}, value.options());
+  const size_t wsb = ops3d_dcnv4_workspace_bytes(z.code, z.B, z.Din, z.Hin, z.Win, (int)group, (int)group_channels,
+                                                 (int)kd, (int)kh, (int)kw, (int)sd, (int)sh, (int)sw, (int)pd,
+                                                 (int)ph, (int)pw, (int)dd, (int)dh, (int)dw, (int)remove_center, 0);
+  at::Tensor ws = at::empty({(int64_t)(wsb ? wsb : 256)}, value.options().dtype(at::kByte));
+  const int rc = ops3d_dcnv4_forward(ptr(value), ptr(p_offset), ptr(out), ws.data_ptr(), wsb, z.code, z.B, z.Din,
+                                     z.Hin, z.Win, (int)group, (int)group_channels, (int)kd, (int)kh, (int)kw,
+                                     (int)sd, (int)sh, (int)sw, (int)pd, (int)ph, (int)pw, (int)dd, (int)dh, (int)dw,
+                                     (float)offset_scale, (int)remove_center, softmax ? 1 : 0,
+                                     (int)p_offset.size(4), (int)im2col_step, stream_of(value));
+  if (rc != OPS3D_FDA_OK) raise(rc, "dcnv4_forward failed");
+  return out;
+}
+
+std::vector<at::Tensor> dcnv4_backward(const at::Tensor &value, const at::Tensor &p_offset, int64_t kd, int64_t kh,
+                                       int64_t kw, int64_t sd, int64_t sh, int64_t sw, int64_t pd, int64_t ph,
+                                       int64_t pw, int64_t dd, int64_t dh, int64_t dw, int64_t group,
+                                       int64_t group_channels, double offset_scale, int64_t im2col_step,
+                                       const at::Tensor &grad_output, int64_t remove_center,
+                                       int64_t /*d_stride*/, int64_t /*block_thread*/, bool softmax) {
+  const DcnArgs z = dcn_check(value, p_offset, group, group_channels);
+  if (!grad_output.is_cuda() || !grad_output.is_contiguous() || grad_output.scalar_type() != value.scalar_type())
+    throw std::runtime_error("grad_output tensor has to be a contiguous CUDA tensor of the value dtype");
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(value.device());
+  at::Tensor grad_value = at::empty_like(value);
+  at::Tensor grad_offset = at::zeros_like(p_offset);   // the row padding stays zero
+  const size_t wsb = ops3d_dcnv4_workspace_bytes(z.code, z.B, z.Din, z.Hin, z.Win, (int)group, (int)group_channels,
+                                                 (int)kd, (int)kh, (int)kw, (int)sd, (int)sh, (int)sw, (int)pd,
+                                                 (int)ph, (int)pw, (int)dd, (int)dh, (int)dw, (int)remove_center, 1);
+  at::Tensor ws = at::empty({(int64_t)(wsb ? wsb : 256)}, value.options().dtype(at::kByte));
+  const int rc = ops3d_dcnv4_backward(ptr(value), ptr(p_offset), ptr(grad_output), ptr(grad_value), ptr(grad_offset),
+                                      ws.data_ptr(), wsb, z.code, z.B, z.Din, z.Hin, z.Win, (int)group,
+                                      (int)group_channels, (int)kd, (int)kh, (int)kw, (int)sd, (int)sh, (int)sw,
+                                      (int)pd, (int)ph, (int)pw, (int)dd, (int)dh, (int)dw, (float)offset_scale,
+                                      (int)remove_center, softmax ? 1 : 0, (int)p_offset.size(4), (int)im2col_step,
+                                      stream_of(value));
+  if (rc != OPS3D_FDA_OK) raise(rc, "dcnv4_backward failed");
+  return {grad_value, grad_offset};
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -317,6 +389,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("forward_offsets", &forward_offsets, "forward from offsets and reference points");
   m.def("backward_offsets", &backward_offsets, "backward of forward_offsets");
   m.def("nms_3d", &nms_3d, "non-maximum suppression for 3d");
+  m.def("dcnv4_forward", &dcnv4_forward, "dcnv4_forward");
+  m.def("dcnv4_backward", &dcnv4_backward, "dcnv4_backward");
   m.def("roi_align_3d_forward", &roi_align_3d_forward, "roi_align_3d_forward");
   m.def("roi_align_3d_backward", &roi_align_3d_backward, "roi_align_3d_backward");
 }
