@@ -13,17 +13,17 @@
 // the reference computes in the element type), rounded step by step (no contraction).
 //
 // Forward: a gather, one thread per (roi, group of CPT channels, bin), so each sample's
-// set-up (8 offsets and weights) serves CPT channels.  Backward: the adjoint scatter of
-// top_grad * w / count into the 8 corners with fp32 hardware atomics, into the fp32 gradient
-// itself or, for 16-bit types, into an fp32 workspace cast afterwards; the call clears it first
-// (a fill kernel) and writes every element of grad_input.  A roi whose batch index is outside
-// [0, N) reads and writes nothing (its output is 0; the reference indexes out of bounds).
+// set-up (8 offsets and weights) serves CPT channels.  Backward: the adjoint, as a gather when
+// the output has at most 64 bins per axis and 384 in all (each voxel sums, in registers, the
+// rois that reach it, in roi order: no atomics, no workspace, the same bits on every run),
+// otherwise by fp32 atomics into a channels-last workspace (64 lanes = 64 contiguous channels
+// per atomic instruction) transposed into grad_input afterwards.  A roi whose batch index is
+// outside [0, N) reads and writes nothing (its output is 0; the reference indexes out of
+// bounds).
 #include <hip/hip_runtime.h>
 #include <hip/hip_bf16.h>
 #include <hip/hip_fp16.h>
 #include <stdint.h>
-
-#include <type_traits>
 
 #include "../../include/ops3d_roi_align3d.h"
 
@@ -155,44 +155,443 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float *p, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = 0.f;
 }
 
+// Channels-last fp32 [N, V, C] -> [N, C, V] in T, through a 64 x 64 LDS tile (padded rows: the
+// column reads are conflict-free).  grid (ceil(V/64), ceil(C/64), N), 256 threads.
 template <typename T>
-__global__ __launch_bounds__(256) void cast_kernel(const float *src, T *dst, int64_t n) {
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = from_f<T>(src[i]);
+__global__ __launch_bounds__(256) void channels_last_to_ncdhw_kernel(const float *src, T *dst, int C, int64_t V) {
+  __shared__ float t[64][65];
+  const int tid = threadIdx.x, lane = tid & 63, row = tid >> 6;
+  const int64_t v0 = (int64_t)blockIdx.x * 64;
+  const int c0 = blockIdx.y * 64;
+  const int64_t n = blockIdx.z;
+  const float *s = src + n * V * C;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int vv = i * 4 + row;
+    if (v0 + vv < V && c0 + lane < C) t[vv][lane] = s[(v0 + vv) * C + c0 + lane];
+  }
+  __syncthreads();
+  T *d = dst + n * C * V;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int cc = i * 4 + row;
+    if (c0 + cc < C && v0 + lane < V) d[(int64_t)(c0 + cc) * V + v0 + lane] = from_f<T>(t[lane][cc]);
+  }
 }
 
-// One thread per (roi, channel, bin): the 8 corners of each sample get top * w / count.
-template <typename T>
-__global__ __launch_bounds__(256) void roi_align3d_backward_kernel(const T *top, const T *rois, float *grad, int N, int C,
-                                                                   int D, int H, int W, int R, int PD, int PH, int PW,
-                                                                   float scale, int sr, int order) {
+// One axis of a sample's interpolation, with the edge rules of corners(): valid unless beyond
+// [-1, size]; below 0 clamps to 0; a base at size - 1 collapses both taps onto it (weights 1, 0).
+// Order 0 keeps the nearest tap (the low one when its weight is >= 0.5), weight 1.  corners()'s
+// eight weights are the products of the three axes' (its nearest-corner rule picks, axis by
+// axis, the low tap whenever allowed, so it is this per-axis choice too).
+struct AxisTap {
+  bool ok;
+  int i0, i1;
+  float w0, w1;
+};
+__device__ __forceinline__ AxisTap axis_tap(float c, int size, int order) {
 #pragma clang fp contract(off)
-  const int64_t total = (int64_t)R * C * PD * PH * PW;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= total) return;
-  const int pw = (int)(idx % PW), ph = (int)((idx / PW) % PH), pd = (int)((idx / ((int64_t)PW * PH)) % PD);
-  const int c = (int)((idx / ((int64_t)PW * PH * PD)) % C);
-  const int r = (int)(idx / ((int64_t)PW * PH * PD * C));
-  const float g = to_f(top[idx]);
-  if (g == 0.f) return;   // adds zeros only
+  AxisTap t;
+  t.ok = !(c < -1.f || c > (float)size);
+  if (c <= 0.f) c = 0.f;
+  t.i0 = (int)c;
+  if (t.i0 >= size - 1) {
+    t.i1 = t.i0 = size - 1;
+    c = (float)t.i0;
+  } else {
+    t.i1 = t.i0 + 1;
+  }
+  const float l = c - (float)t.i0, h = 1.f - l;
+  if (order == 0) {
+    t.w0 = h >= 0.5f ? 1.f : 0.f;
+    t.w1 = h >= 0.5f ? 0.f : 1.f;
+  } else {
+    t.w0 = h;
+    t.w1 = l;
+  }
+  return t;
+}
+
+// Sum of the valid samples' weights on tap position `pos` of one axis (sample i at
+// sample_coord(start, p, bin, i, grid)).
+__device__ __forceinline__ float axis_weight_at(int pos, float start, int p, float bin, int grid, int size, int order) {
+  float s = 0.f;
+  for (int i = 0; i < grid; ++i) {
+    const AxisTap t = axis_tap(sample_coord(start, p, bin, i, grid), size, order);
+    if (!t.ok) continue;
+    if (t.i0 == pos) s += t.w0;
+    if (t.i1 == pos && t.i1 != t.i0) s += t.w1;
+  }
+  return s;
+}
+
+// Backward: one wave per (roi, 64 channels, output row (pd, ph)); lane = channel.  The weights
+// are separable, so the row's contribution to voxel (z, y, x) is WZ[z] * WY[y] * X[x], with WZ
+// and WY the row's summed z and y tap weights and X[x] = sum over the row's x samples of
+// top[bin] * wx / count.  The wave walks the x samples in increasing x (they are sorted), keeps
+// the running X of the two newest tap positions per lane and, once the walk has passed a
+// position, adds WZ * WY * X to every (z, y) tap of it with one atomic instruction each: 64
+// contiguous channels of the channels-last workspace.  Every voxel a row touches thus gets one
+// atomic per (row, 64 channels) instead of one per sample corner.  WZ / WY sit in lanes
+// (lane t: tap position min + t); rows with more than 64 tap positions on an axis (adaptive
+// grids of huge bins) take the per-sample path.
+constexpr int kBwdWaves = 4;
+template <typename T>
+__global__ __launch_bounds__(64 * kBwdWaves) void roi_align3d_backward_kernel(const T *top, const T *rois, float *acc,
+                                                                            int N, int C, int D, int H, int W, int R,
+                                                                            int PD, int PH, int PW, float scale, int sr,
+                                                                            int order) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int CG = (C + 63) / 64;
+  const int64_t wid = (int64_t)blockIdx.x * kBwdWaves + (threadIdx.x >> 6);
+  if (wid >= (int64_t)R * CG * PD * PH) return;   // whole waves
+  const int ph = (int)(wid % PH), pd = (int)((wid / PH) % PD);
+  const int cg = (int)((wid / ((int64_t)PH * PD)) % CG);
+  const int r = (int)(wid / ((int64_t)PH * PD * CG));
+  const int c = cg * 64 + lane;
+  const bool active = c < C;
   const Roi q = roi_setup(rois, r, scale, sr, PD, PH, PW);
   if (q.b < 0 || q.b >= N) return;   // a roi of a batch item that does not exist
   const int64_t vol = (int64_t)D * H * W;
-  float *base = grad + ((int64_t)q.b * C + c) * vol;
-  for (int iz = 0; iz < q.gd; ++iz) {
-    const float z = sample_coord(q.sd, pd, q.bd, iz, q.gd);
-    for (int iy = 0; iy < q.gh; ++iy) {
-      const float y = sample_coord(q.sh, ph, q.bh, iy, q.gh);
+  float *base = acc + (int64_t)q.b * vol * C + c;
+  const T *tg = top + (((int64_t)r * C + (active ? c : 0)) * PD + pd) * PH * PW + (int64_t)ph * PW;
+  // tap ranges of the row's z and y samples (coordinates increase with the sample index)
+  int z_lo = 1 << 30, z_hi = -1, y_lo = 1 << 30, y_hi = -1;
+  for (int i = 0; i < q.gd; ++i) {
+    const AxisTap t = axis_tap(sample_coord(q.sd, pd, q.bd, i, q.gd), D, order);
+    if (t.ok) { z_lo = min(z_lo, t.i0); z_hi = max(z_hi, t.i1); }
+  }
+  for (int i = 0; i < q.gh; ++i) {
+    const AxisTap t = axis_tap(sample_coord(q.sh, ph, q.bh, i, q.gh), H, order);
+    if (t.ok) { y_lo = min(y_lo, t.i0); y_hi = max(y_hi, t.i1); }
+  }
+  if (z_hi < 0 || y_hi < 0) return;   // no valid sample in z or y: the row adds nothing
+  const int nz = z_hi - z_lo + 1, ny = y_hi - y_lo + 1;
+  if (nz <= 64 && ny <= 64) {
+    const float wz_l = lane < nz ? axis_weight_at(z_lo + lane, q.sd, pd, q.bd, q.gd, D, order) : 0.f;
+    const float wy_l = lane < ny ? axis_weight_at(y_lo + lane, q.sh, ph, q.bh, q.gh, H, order) : 0.f;
+    // X of the tap position px (a0) and px + 1 (a1); `open`: px holds a position
+    int px = 0;
+    bool open = false, used1 = false;
+    float a0 = 0.f, a1 = 0.f;
+    const auto flush = [&](int x, float v) {
+      const float vc = v / q.count;
+      for (int tz = 0; tz < nz; ++tz) {
+        const float wz = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wz_l), tz));
+        if (wz == 0.f) continue;
+        for (int ty = 0; ty < ny; ++ty) {
+          const float wy = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wy_l), ty));
+          if (wy == 0.f) continue;
+          if (active) atomicAdd(base + (((int64_t)(z_lo + tz) * H + (y_lo + ty)) * W + x) * C, (wz * wy) * vc);
+        }
+      }
+    };
+    for (int pw = 0; pw < PW; ++pw) {
+      const float g = active ? to_f(tg[pw]) : 0.f;
       for (int ix = 0; ix < q.gw; ++ix) {
-        const float x = sample_coord(q.sw, pw, q.bw, ix, q.gw);
-        int64_t off[8];
-        float w[8];
-        if (!corners(z, y, x, D, H, W, order, off, w)) continue;
-#pragma unroll
-        for (int k = 0; k < 8; ++k)
-          if (w[k] != 0.f) atomicAdd(base + off[k], g * w[k] / q.count);
+        const AxisTap t = axis_tap(sample_coord(q.sw, pw, q.bw, ix, q.gw), W, order);
+        if (!t.ok) continue;
+        if (!open) {
+          px = t.i0;
+          open = true;
+        } else if (t.i0 == px + 1) {
+          flush(px, a0);
+          px = t.i0;
+          a0 = a1;
+          a1 = 0.f;
+          used1 = false;
+        } else if (t.i0 > px + 1) {
+          flush(px, a0);
+          if (used1) flush(px + 1, a1);
+          px = t.i0;
+          a0 = a1 = 0.f;
+          used1 = false;
+        }
+        a0 += g * t.w0;
+        if (t.i1 != t.i0) {
+          a1 += g * t.w1;
+          used1 = true;
+        }
       }
     }
+    if (open) {
+      flush(px, a0);
+      if (used1) flush(px + 1, a1);
+    }
+    return;
+  }
+  // per-sample path: the 8 corners of each sample, top * w / count each
+  for (int pw = 0; pw < PW; ++pw) {
+    const float g = active ? to_f(tg[pw]) : 0.f;
+    for (int iz = 0; iz < q.gd; ++iz) {
+      const float z = sample_coord(q.sd, pd, q.bd, iz, q.gd);
+      for (int iy = 0; iy < q.gh; ++iy) {
+        const float y = sample_coord(q.sh, ph, q.bh, iy, q.gh);
+        for (int ix = 0; ix < q.gw; ++ix) {
+          const float x = sample_coord(q.sw, pw, q.bw, ix, q.gw);
+          int64_t off[8];
+          float w[8];
+          if (!corners(z, y, x, D, H, W, order, off, w)) continue;
+#pragma unroll
+          for (int k = 0; k < 8; ++k)
+            if (w[k] != 0.f && active) atomicAdd(base + off[k] * C, g * w[k] / q.count);
+        }
+      }
+    }
+  }
+}
+
+// Backward as a gather (no atomics): a block owns a tile of 4 x 8 x 8 voxels of one batch item
+// (a thread per voxel) and 16 channels, and sums into registers the contributions of every roi
+// whose footprint reaches the tile, rois in index order, so the result is the same on every run.
+// The weights are separable: voxel (z, y, x) gets, from roi r, the sum over bins (pd, ph, pw) of
+// WZ[z][pd] * WY[y][ph] * WX[x][pw] * top[r, c, pd, ph, pw] / count, where WZ[z][pd] is the sum of
+// bin pd's z-sample tap weights on z (and so on) -- the sum over the bin's samples of their
+// corner weights.  The block takes its rois in groups, so that one round trip to memory serves
+// several rois: for up to 8 rois it finds the bins that reach the tile on each axis (a thread
+// per (roi, tile position, bin)), keeps the longest prefix whose bin boxes and weight tables fit
+// the LDS arenas, writes their tables and stages top for their boxes and its 16 channels as
+// fp32, and each thread then walks, roi by roi, the nonzero bins of its voxel.  Needs at most 64
+// bins per axis and 384 in all (else the atomic path below is used).
+constexpr int kGTZ = 4, kGTY = 8, kGTX = 8;   // tile: 256 voxels, a thread each
+constexpr int kGPos = kGTZ + kGTY + kGTX;      // tile positions over the three axes
+constexpr int kGCC = 16;                       // channels per block (registers per thread)
+constexpr int kGMaxAxisBins = 64, kGMaxBins = 384;
+constexpr int kGGroup = 8;                     // rois examined per group
+constexpr int kGTab = 2048;                    // weight-table arena (floats)
+constexpr int kGList = 128;                    // rois per compaction batch
+
+__host__ __device__ inline bool gather_fits(int PD, int PH, int PW) {
+  return PD <= kGMaxAxisBins && PH <= kGMaxAxisBins && PW <= kGMaxAxisBins && PD * PH * PW <= kGMaxBins;
+}
+
+// Whether a roi's taps on one axis can reach [t0, t0 + T): its samples lie in [start, end]
+// (coordinates), their taps in [floor(max(start, 0)), floor(max(end, 0)) + 1], none if
+// start > size.
+__device__ __forceinline__ bool axis_reaches(float start, float end, int size, int t0, int T) {
+  if (start > (float)size) return false;
+  const float lo = floorf(fmaxf(start, 0.f)), hi = floorf(fmaxf(end, 0.f)) + 1.f;
+  return !(hi < (float)t0 || lo > (float)(t0 + T - 1));
+}
+
+// A roi's parameters in LDS (the Roi fields the gather needs).
+struct GatherRoi {
+  float s[3], bin[3], inv_count;   // z, y, x
+  int grid[3];
+};
+// Bin ranges of one roi of a group: [first, last] bin reaching the tile per axis, and per tile
+// position (z positions, then y, then x).
+struct GatherRanges {
+  int box[3][2];
+  int pos[kGPos][2];
+};
+constexpr int kGRangeInts = (int)(sizeof(GatherRanges) / sizeof(int));
+
+// (axis, position, bin) of entry f of a roi's full table (all PD / PH / PW bins per position)
+__device__ __forceinline__ void table_entry(int f, int PD, int PH, int PW, int &ax, int &pos, int &p) {
+  if (f < kGTZ * PD) {
+    ax = 0, pos = f / PD, p = f - pos * PD;
+  } else if (f < kGTZ * PD + kGTY * PH) {
+    f -= kGTZ * PD;
+    ax = 1, pos = f / PH, p = f - pos * PH;
+  } else {
+    f -= kGTZ * PD + kGTY * PH;
+    ax = 2, pos = f / PW, p = f - pos * PW;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void roi_align3d_backward_gather_kernel(const T *top, const T *rois, T *grad, int N,
+                                                                          int C, int D, int H, int W, int R, int PD,
+                                                                          int PH, int PW, float scale, int sr,
+                                                                          int order) {
+#pragma clang fp contract(off)
+  __shared__ float4 g_l[kGCC / 4][kGMaxBins];   // [channel quad][bin of the group's boxes]
+  __shared__ float tab_l[kGTab];                // the group's weight tables
+  __shared__ GatherRoi roi_l[kGList];
+  __shared__ int rid_l[kGList];
+  __shared__ GatherRanges rng_l[kGGroup];
+  __shared__ int goff_l[kGGroup + 1][2];         // per group roi: first bin, first table entry
+  __shared__ int cnt_l[4], gsize_l;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int ntx = (W + kGTX - 1) / kGTX, nty = (H + kGTY - 1) / kGTY, ntz = (D + kGTZ - 1) / kGTZ;
+  const int ncc = (C + kGCC - 1) / kGCC;
+  int64_t bid = blockIdx.x;
+  const int txi = (int)(bid % ntx);
+  bid /= ntx;
+  const int tyi = (int)(bid % nty);
+  bid /= nty;
+  const int tzi = (int)(bid % ntz);
+  bid /= ntz;
+  const int cc = (int)(bid % ncc), n = (int)(bid / ncc);
+  const int t0[3] = {tzi * kGTZ, tyi * kGTY, txi * kGTX};
+  const int c0 = cc * kGCC;
+  const int zl = tid / (kGTY * kGTX), yl = (tid / kGTX) % kGTY, xl = tid % kGTX;
+  const int P[3] = {PD, PH, PW}, S[3] = {D, H, W}, TT[3] = {kGTZ, kGTY, kGTX};
+  const int pos0[3] = {0, kGTZ, kGTZ + kGTY};     // first position of each axis in the ranges
+  const int E = kGTZ * PD + kGTY * PH + kGTX * PW;   // entries of a roi's full table
+  const int64_t pvol = (int64_t)PD * PH * PW;
+
+  float acc[kGCC];
+#pragma unroll
+  for (int k = 0; k < kGCC; ++k) acc[k] = 0.f;
+  for (int rb = 0; rb < R; rb += kGList) {
+    // the rois of batch item n whose taps can reach the tile, in index order, with their
+    // parameters in LDS
+    const int r = rb + tid;
+    bool hit = false;
+    Roi q;
+    if (tid < kGList && r < R) {
+      q = roi_setup(rois, r, scale, sr, PD, PH, PW);
+      hit = q.b == n && axis_reaches(q.sd, q.sd + q.bd * (float)PD, D, t0[0], kGTZ) &&
+            axis_reaches(q.sh, q.sh + q.bh * (float)PH, H, t0[1], kGTY) &&
+            axis_reaches(q.sw, q.sw + q.bw * (float)PW, W, t0[2], kGTX);
+    }
+    const uint64_t m = __ballot(hit);
+    if (lane == 0) cnt_l[wv] = __popcll(m);
+    __syncthreads();
+    int off = 0, tot = 0;
+    for (int w = 0; w < 4; ++w) {
+      off += w < wv ? cnt_l[w] : 0;
+      tot += cnt_l[w];
+    }
+    if (hit) {
+      const int i = off + __popcll(m & ((1ull << lane) - 1ull));
+      rid_l[i] = r;
+      GatherRoi g;
+      g.s[0] = q.sd, g.s[1] = q.sh, g.s[2] = q.sw;
+      g.bin[0] = q.bd, g.bin[1] = q.bh, g.bin[2] = q.bw;
+      g.grid[0] = q.gd, g.grid[1] = q.gh, g.grid[2] = q.gw;
+      g.inv_count = 1.f / q.count;
+      roi_l[i] = g;
+    }
+    for (int li = 0; li < tot;) {
+      const int gmax = min(kGGroup, tot - li);
+      for (int i = tid; i < kGGroup * kGRangeInts; i += 256)
+        reinterpret_cast<int *>(rng_l)[i] = (i & 1) ? -1 : (1 << 30);
+      __syncthreads();   // (also: the previous group's sums are done with the LDS state)
+      // 1. bin ranges of the next gmax rois: a thread per (roi, position, bin)
+      for (int e = tid; e < gmax * E; e += 256) {
+        const int w = e / E;
+        int ax, pos, p;
+        table_entry(e - w * E, PD, PH, PW, ax, pos, p);
+        const GatherRoi &g = roi_l[li + w];
+        const int at = t0[ax] + pos;
+        if (at < S[ax] && axis_weight_at(at, g.s[ax], p, g.bin[ax], g.grid[ax], S[ax], order) != 0.f) {
+          atomicMin(&rng_l[w].box[ax][0], p);
+          atomicMax(&rng_l[w].box[ax][1], p);
+          atomicMin(&rng_l[w].pos[pos0[ax] + pos][0], p);
+          atomicMax(&rng_l[w].pos[pos0[ax] + pos][1], p);
+        }
+      }
+      __syncthreads();
+      // 2. the group: the longest prefix whose boxes and tables fit (at least one roi)
+      if (tid == 0) {
+        int nbin = 0, ntab = 0, gs = 0;
+        for (; gs < gmax; ++gs) {
+          const GatherRanges &rg = rng_l[gs];
+          int b = 1, t = 0;
+          for (int ax = 0; ax < 3; ++ax) {
+            const int nb = rg.box[ax][1] < 0 ? 0 : rg.box[ax][1] - rg.box[ax][0] + 1;
+            b *= nb;
+            t += TT[ax] * nb;
+          }
+          if (b == 0) t = 0;   // reaches nothing: no table, no bins
+          if (gs > 0 && (nbin + b > kGMaxBins || ntab + t > kGTab)) break;
+          goff_l[gs][0] = nbin;
+          goff_l[gs][1] = ntab;
+          nbin += b;
+          ntab += t;
+        }
+        goff_l[gs][0] = nbin;
+        goff_l[gs][1] = ntab;
+        gsize_l = gs;
+      }
+      __syncthreads();
+      const int gs = gsize_l;
+      // 3. the group's tables (weights of the box bins at the tile positions) ...
+      const int ntab = goff_l[gs][1], nbin = goff_l[gs][0];
+      for (int e = tid; e < ntab; e += 256) {
+        int w = 0;
+        while (goff_l[w + 1][1] <= e) ++w;
+        const GatherRanges &rg = rng_l[w];
+        const GatherRoi &g = roi_l[li + w];
+        int f = e - goff_l[w][1], ax = 0;
+        for (; ax < 2; ++ax) {
+          const int sz = TT[ax] * (rg.box[ax][1] - rg.box[ax][0] + 1);
+          if (f < sz) break;
+          f -= sz;
+        }
+        const int nb = rg.box[ax][1] - rg.box[ax][0] + 1;
+        const int pos = f / nb, p = rg.box[ax][0] + (f - pos * nb);
+        const int at = t0[ax] + pos;
+        tab_l[e] = at < S[ax] ? axis_weight_at(at, g.s[ax], p, g.bin[ax], g.grid[ax], S[ax], order) : 0.f;
+      }
+      // ... and top for their boxes of bins and the block's channels, as fp32 (consecutive
+      // threads on consecutive bins of one channel quad)
+      for (int e = tid; e < nbin * (kGCC / 4); e += 256) {
+        const int k4 = e / nbin, gb = e - k4 * nbin;
+        int w = 0;
+        while (goff_l[w + 1][0] <= gb) ++w;
+        const GatherRanges &rg = rng_l[w];
+        const int lb = gb - goff_l[w][0];
+        const int nby = rg.box[1][1] - rg.box[1][0] + 1, nbx = rg.box[2][1] - rg.box[2][0] + 1;
+        const int bx = lb % nbx, bzy = lb / nbx, by = bzy % nby, bz = bzy / nby;
+        const T *src = top + ((int64_t)rid_l[li + w] * C + c0 + 4 * k4) * pvol +
+                       ((int64_t)(rg.box[0][0] + bz) * PH + rg.box[1][0] + by) * PW + rg.box[2][0] + bx;
+        float4 v;
+        v.x = c0 + 4 * k4 + 0 < C ? to_f(src[0]) : 0.f;
+        v.y = c0 + 4 * k4 + 1 < C ? to_f(src[pvol]) : 0.f;
+        v.z = c0 + 4 * k4 + 2 < C ? to_f(src[2 * pvol]) : 0.f;
+        v.w = c0 + 4 * k4 + 3 < C ? to_f(src[3 * pvol]) : 0.f;
+        g_l[k4][gb] = v;
+      }
+      __syncthreads();
+      // 4. this voxel's sums, roi by roi: its bins are a contiguous range per axis
+      for (int w = 0; w < gs; ++w) {
+        const GatherRanges &rg = rng_l[w];
+        if (rg.box[0][1] < 0 || rg.box[1][1] < 0 || rg.box[2][1] < 0) continue;
+        const int pz0 = rg.box[0][0], py0 = rg.box[1][0], px0 = rg.box[2][0];
+        const int nbz = rg.box[0][1] - pz0 + 1, nby = rg.box[1][1] - py0 + 1, nbx = rg.box[2][1] - px0 + 1;
+        const float *tz = tab_l + goff_l[w][1] + zl * nbz - pz0;
+        const float *ty = tab_l + goff_l[w][1] + kGTZ * nbz + yl * nby - py0;
+        const float *tx = tab_l + goff_l[w][1] + kGTZ * nbz + kGTY * nby + xl * nbx - px0;
+        const int gb0 = goff_l[w][0];
+        const float inv_count = roi_l[li + w].inv_count;
+        const int qz0 = rg.pos[zl][0], qz1 = rg.pos[zl][1];
+        const int qy0 = rg.pos[kGTZ + yl][0], qy1 = rg.pos[kGTZ + yl][1];
+        const int qx0 = rg.pos[kGTZ + kGTY + xl][0], qx1 = rg.pos[kGTZ + kGTY + xl][1];
+        for (int pz = qz0; pz <= qz1; ++pz) {
+          const float wz = tz[pz] * inv_count;
+          for (int py = qy0; py <= qy1; ++py) {
+            const float wzy = wz * ty[py];
+            const int lrow = gb0 + ((pz - pz0) * nby + (py - py0)) * nbx - px0;
+            for (int px = qx0; px <= qx1; ++px) {
+              const float wgt = wzy * tx[px];
+#pragma unroll
+              for (int k4 = 0; k4 < kGCC / 4; ++k4) {
+                const float4 gv = g_l[k4][lrow + px];
+                acc[4 * k4 + 0] += wgt * gv.x;
+                acc[4 * k4 + 1] += wgt * gv.y;
+                acc[4 * k4 + 2] += wgt * gv.z;
+                acc[4 * k4 + 3] += wgt * gv.w;
+              }
+            }
+          }
+        }
+      }
+      li += gs;
+      __syncthreads();   // the sums are done with the group's LDS state
+    }
+    __syncthreads();   // the batch's counts are read before the next batch writes them
+  }
+  const int z = t0[0] + zl, y = t0[1] + yl, x = t0[2] + xl;
+  if (z < D && y < H && x < W) {
+    const int64_t vol = (int64_t)D * H * W, v = ((int64_t)z * H + y) * W + x;
+#pragma unroll
+    for (int k = 0; k < kGCC; ++k)
+      if (c0 + k < C) grad[((int64_t)n * C + c0 + k) * vol + v] = from_f<T>(acc[k]);
   }
 }
 
@@ -217,17 +616,26 @@ int forward(const void *features, const void *rois, void *output, int N, int C, 
 template <typename T>
 int backward(const void *grad_output, const void *rois, void *grad_input, float *acc, int N, int C, int D, int H,
              int W, int R, int PD, int PH, int PW, float scale, int sr, int order, hipStream_t st) {
+  if (gather_fits(PD, PH, PW)) {
+    const int64_t blocks = (int64_t)N * ((C + kGCC - 1) / kGCC) * ((D + kGTZ - 1) / kGTZ) * ((H + kGTY - 1) / kGTY) *
+                           ((W + kGTX - 1) / kGTX);
+    hipLaunchKernelGGL((roi_align3d_backward_gather_kernel<T>), dim3((unsigned)blocks), dim3(256), 0, st,
+                       static_cast<const T *>(grad_output), static_cast<const T *>(rois), static_cast<T *>(grad_input),
+                       N, C, D, H, W, R, PD, PH, PW, scale, sr, order);
+    return hipGetLastError() == hipSuccess ? OPS3D_FDA_OK : OPS3D_FDA_ERUNTIME;
+  }
   const int64_t nin = (int64_t)N * C * D * H * W;
-  const int64_t nout = (int64_t)R * C * PD * PH * PW;
+  const int64_t vol = (int64_t)D * H * W;
+  const int64_t nwaves = (int64_t)R * ((C + 63) / 64) * PD * PH;
   const int64_t fg = (nin + 255) / 256;
   const unsigned fill_grid = (unsigned)(fg < 65536 ? (fg > 0 ? fg : 1) : 65536);
   hipLaunchKernelGGL(fill_zero_kernel, dim3(fill_grid), dim3(256), 0, st, acc, nin);
-  if (nout > 0)
-    hipLaunchKernelGGL((roi_align3d_backward_kernel<T>), dim3((unsigned)((nout + 255) / 256)), dim3(256), 0, st,
-                       static_cast<const T *>(grad_output), static_cast<const T *>(rois), acc, N, C, D, H, W, R, PD, PH,
-                       PW, scale, sr, order);
-  if constexpr (!std::is_same<T, float>::value)
-    hipLaunchKernelGGL((cast_kernel<T>), dim3(fill_grid), dim3(256), 0, st, acc, static_cast<T *>(grad_input), nin);
+  if (nwaves > 0)
+    hipLaunchKernelGGL((roi_align3d_backward_kernel<T>), dim3((unsigned)((nwaves + kBwdWaves - 1) / kBwdWaves)),
+                       dim3(64 * kBwdWaves), 0, st, static_cast<const T *>(grad_output), static_cast<const T *>(rois),
+                       acc, N, C, D, H, W, R, PD, PH, PW, scale, sr, order);
+  hipLaunchKernelGGL((channels_last_to_ncdhw_kernel<T>), dim3((unsigned)((vol + 63) / 64), (unsigned)((C + 63) / 64), N),
+                     dim3(256), 0, st, acc, static_cast<T *>(grad_input), C, vol);
   return hipGetLastError() == hipSuccess ? OPS3D_FDA_OK : OPS3D_FDA_ERUNTIME;
 }
 
@@ -261,8 +669,10 @@ int ops3d_roi_align3d_forward(const void *features, const void *rois, void *outp
   }
 }
 
-size_t ops3d_roi_align3d_backward_workspace_bytes(int dtype, int N, int C, int D, int H, int W) {
-  if (dtype == OPS3D_FDA_F32 || N <= 0 || C <= 0 || D <= 0 || H <= 0 || W <= 0) return 0;
+size_t ops3d_roi_align3d_backward_workspace_bytes(int dtype, int N, int C, int D, int H, int W, int PD, int PH,
+                                                 int PW) {
+  (void)dtype;
+  if (N <= 0 || C <= 0 || D <= 0 || H <= 0 || W <= 0 || gather_fits(PD, PH, PW)) return 0;
   return (size_t)N * C * D * H * W * sizeof(float);
 }
 
@@ -272,13 +682,13 @@ int ops3d_roi_align3d_backward(const void *grad_output, const void *rois, void *
   if (!valid(dtype, N, C, D, H, W, R, PD, PH, PW, order)) return OPS3D_FDA_EINVAL;
   if ((int64_t)N * C == 0) return OPS3D_FDA_OK;
   if (!grad_input || ((int64_t)R > 0 && (!grad_output || !rois))) return OPS3D_FDA_EINVAL;
-  if (workspace_bytes < ops3d_roi_align3d_backward_workspace_bytes(dtype, N, C, D, H, W) ||
-      (dtype != OPS3D_FDA_F32 && (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 3u))))
+  const size_t need = ops3d_roi_align3d_backward_workspace_bytes(dtype, N, C, D, H, W, PD, PH, PW);
+  if (need > 0 && (workspace_bytes < need || !workspace || (reinterpret_cast<uintptr_t>(workspace) & 3u)))
     return OPS3D_FDA_EINVAL;
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (dtype) {
     case OPS3D_FDA_F32:
-      return backward<float>(grad_output, rois, grad_input, static_cast<float *>(grad_input), N, C, D, H, W, R, PD, PH,
+      return backward<float>(grad_output, rois, grad_input, static_cast<float *>(workspace), N, C, D, H, W, R, PD, PH,
                              PW, spatial_scale, sampling_ratio, order, st);
     case OPS3D_FDA_F16:
       return backward<__half>(grad_output, rois, grad_input, static_cast<float *>(workspace), N, C, D, H, W, R, PD, PH,

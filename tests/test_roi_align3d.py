@@ -90,6 +90,10 @@ CASES = [
     (1, 3, (5, 6, 7), 15, (2, 2, 2), 1.0, 1, 0, torch.float32),         # nearest, C % 4 != 0
     (2, 16, (10, 10, 10), 30, (4, 4, 4), 1.0, 2, 1, torch.bfloat16),
     (1, 4, (6, 8, 8), 12, (3, 2, 2), 2.0, 0, 1, torch.float16),
+    (1, 70, (6, 7, 9), 10, (2, 2, 3), 1.0, 2, 1, torch.float32),       # a partial 64-channel group
+    (2, 130, (5, 9, 11), 8, (3, 2, 2), 1.0, 3, 0, torch.bfloat16),     # nearest, 130 channels
+    (1, 5, (6, 7, 9), 6, (9, 8, 8), 1.0, 1, 1, torch.float32),          # 576 bins: atomic backward
+    (1, 3, (6, 7, 9), 6, (2, 65, 2), 1.0, 1, 0, torch.bfloat16),        # 65 bins on y: atomic backward
 ]
 
 
@@ -118,6 +122,63 @@ def test_gpu_matches_oracle(gpu_device, case):
     assert_close("roi_align output", out.detach(), want, rtol, atol)
     # gradients: fp32 sums of up to count * 8 terms per voxel, added by atomics in any order
     assert_close("roi_align grad", xg.grad, gwant, rtol, atol * (10 if dt == torch.float32 else 1))
+
+
+def test_workspace_only_for_the_atomic_backward():
+    """The gather backward (at most 64 bins per axis and 384 in all) needs no workspace; the
+    atomic one an fp32 buffer of grad_input's size (the C ABI, no GPU needed)."""
+    from ops3d_amd import _extension
+
+    lib = _extension.load_library()
+    f = lib.ops3d_roi_align3d_backward_workspace_bytes
+    assert f(2, 2, 256, 32, 64, 64, 7, 7, 7) == 0
+    assert f(0, 1, 5, 6, 7, 9, 6, 8, 8) == 0
+    assert f(0, 1, 5, 6, 7, 9, 7, 8, 8) == 5 * 6 * 7 * 9 * 4
+    assert f(2, 1, 3, 6, 7, 9, 2, 65, 2) == 3 * 6 * 7 * 9 * 4
+
+
+@pytest.mark.gpu
+def test_gpu_backward_repeatable(gpu_device):
+    """The gather backward sums each voxel's rois in roi order: the same bits on every run."""
+    from ops3d_amd.roi_align import roi_align_3d
+
+    r = np.random.default_rng(3)
+    x = torch.from_numpy(r.normal(size=(2, 20, 8, 12, 16)).astype(np.float32)).to(gpu_device)
+    rois = torch.from_numpy(_rois(40, 2, (8, 12, 16), seed=9)).to(gpu_device)
+    g = torch.randn(40, 20, 3, 3, 3, device=gpu_device)
+    grads = []
+    for _ in range(3):
+        xg = x.clone().requires_grad_(True)
+        roi_align_3d(xg, rois, (3, 3, 3), 1.0, 2, 1).backward(g)
+        grads.append(xg.grad)
+    torch.cuda.synchronize()
+    assert torch.equal(grads[0], grads[1]) and torch.equal(grads[0], grads[2])
+
+
+@pytest.mark.gpu
+def test_gpu_wide_bins(gpu_device):
+    """Rows whose bins span more than 64 voxels on y (adaptive grid, one bin): the backward's
+    per-sample path; and bins of one voxel or less (many samples per tap) on the same volume."""
+    from fda_helpers import assert_close, log
+
+    from ops3d_amd.roi_align import roi_align_3d
+
+    log("[case] roi_align3d wide bins (per-sample path) and dense samples")
+    r = np.random.default_rng(7)
+    x = torch.from_numpy(r.normal(size=(1, 3, 4, 80, 6)).astype(np.float32))
+    rois = torch.tensor([[0, 0.0, 0.0, 0.0, 5.0, 79.0, 3.0],      # y extent 79, one bin: 79 samples
+                         [0, 1.0, -0.5, 0.5, 4.5, 78.5, 2.5],
+                         [0, 2.0, 10.0, 1.0, 2.5, 10.8, 1.4]])     # sub-voxel roi, 8 samples per axis
+    for pooled, sr in (((1, 1, 1), 0), ((2, 1, 2), 0), ((1, 2, 1), 8)):
+        xg = x.to(gpu_device).requires_grad_(True)
+        out = roi_align_3d(xg, rois.to(gpu_device), pooled, 1.0, sr, 1)
+        g = torch.from_numpy(r.normal(size=tuple(out.shape)).astype(np.float32))
+        out.backward(g.to(gpu_device))
+        torch.cuda.synchronize()
+        want = O.forward(x.double().numpy(), rois.double().numpy(), pooled, 1.0, sr, 1)
+        gwant = O.backward(g.double().numpy(), rois.double().numpy(), x.shape, 1.0, sr, 1)
+        assert_close(f"wide-bin output {pooled} sr={sr}", out.detach(), want, 1e-5, 1e-6)
+        assert_close(f"wide-bin grad {pooled} sr={sr}", xg.grad, gwant, 1e-5, 1e-5)
 
 
 @pytest.mark.gpu
