@@ -17,7 +17,8 @@ extern "C" {
 #endif
 
 /* Bytes of device workspace ops3d_nms3d needs for n boxes: the n x ceil(n/64) 64-bit IoU mask
- * (0 for n <= 0). */
+ * and, per row, a bitmap of its nonzero mask words (n x ceil(n/4096) 64-bit words); 0 for
+ * n <= 0. */
 OPS3D_FDA_API size_t ops3d_nms3d_workspace_bytes(int n);
 
 /*
