@@ -688,22 +688,19 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
 // are scheduled coarse levels first (their tiles hold the most entries), and with G % 8 == 0
 // the tiles of head g run on XCD g % 8, whose L2 then holds that head's grad_output rows.
 
-// Exclusive scan across the NT threads of a block; tmp holds NT/64 words.
-template <int NT>
-__device__ __forceinline__ uint32_t block_exclusive_scan_tile(uint32_t x, uint32_t *tmp) {
-  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
-  uint32_t inc = x;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const uint32_t y = __shfl_up(inc, o, kWave);
-    if (lane >= o) inc += y;
-  }
-  if (lane == kWave - 1) tmp[w] = inc;
-  __syncthreads();
-  uint32_t wofs = 0;
-  for (int ww = 0; ww < w; ++ww) wofs += tmp[ww];
-  __syncthreads();
-  return wofs + inc - x;
+// Inclusive prefix sum over the 64 lanes of a wave: a Hillis-Steele scan inside each row of 16
+// lanes (DPP row shifts; lanes shifted in from outside the row read 0), then the totals of the
+// rows before added from lanes 15, 31, 47.
+__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v) {
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, true);   // row_shr:1
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, true);   // row_shr:2
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, true);   // row_shr:4
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, true);   // row_shr:8
+  const uint32_t t0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 15);
+  const uint32_t t1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 31);
+  const uint32_t t2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 47);
+  const int row = (int)(threadIdx.x & (kWave - 1)) >> 4;
+  return v + (row > 0 ? t0 : 0u) + (row > 1 ? t1 : 0u) + (row > 2 ? t2 : 0u);
 }
 
 // Waves per SIMD the tile kernel runs at: its LDS chunk sizing puts three 256-thread blocks, two
@@ -718,7 +715,6 @@ __global__ __launch_bounds__(tile_threads(LPU)) __attribute__((amdgpu_waves_per_
 void fda_bwd_tile_kernel(const Args a) {
   constexpr int NT = tile_threads(LPU);
   extern __shared__ __align__(16) unsigned char tsm[];
-  __shared__ uint32_t scan_tmp[NT / kWave];
   constexpr int EB = CPL * (int)sizeof(T);      // bytes of a lane's channels
   constexpr int NW = EB / 4;
   const int tid = threadIdx.x;
@@ -955,14 +951,14 @@ void fda_bwd_tile_kernel(const Args a) {
           pE[e] = a.entries[nc0 + ((uint32_t)(tid + e * NT) < nn ? (uint32_t)(tid + e * NT) : 0u)];
       }
       __syncthreads();
-      // 2. bin starts: thread tid scans bins [tid*per, (tid+1)*per)
-      {
-        const int per = (nb + NT - 1) / NT;
+      // 2. bin starts, by wave 0 alone (one barrier): lane k scans bins [k*per, (k+1)*per)
+      if (tid < kWave) {
+        const int per = (nb + kWave - 1) / kWave;
         const int b0 = tid * per;
         uint32_t sum = 0;
         for (int i = 0; i < per; ++i)
           if (b0 + i < nb) sum += cur_l[b0 + i];
-        uint32_t run = block_exclusive_scan_tile<NT>(sum, scan_tmp);
+        uint32_t run = wave_inclusive_scan(sum) - sum;
         for (int i = 0; i < per; ++i)
           if (b0 + i < nb) {
             const uint32_t c = cur_l[b0 + i];
@@ -970,7 +966,7 @@ void fda_bwd_tile_kernel(const Args a) {
             cur_l[b0 + i] = run;
             run += c;
           }
-        if (tid == NT - 1) start_l[nb] = (uint32_t)n;
+        if (tid == 0) start_l[nb] = (uint32_t)n;
       }
       __syncthreads();
       // 3. counting sort by bin: each entry's stash and row index go to its sorted position
