@@ -820,8 +820,8 @@ void fda_bwd_tile_kernel(const Args a) {
   // ahead and read three ahead, so its round trip hides behind a whole tile even when tiles are
   // tiny), so blocks that drew light tiles take more of them.
   // Software pipeline: the entries of the block's next chunk are loaded when a chunk starts and
-  // their stash before its rows are loaded, so both arrive during the owner phase; tile headers
-  // (first entry, count) are loaded two tiles before they are read.
+  // their stash once its rows have arrived, so the stash arrives during the owner phase; tile
+  // headers (first entry, count) are loaded two tiles before they are read.
   __shared__ uint32_t grab_l[4];   // claim made at tile position p in slot p & 3 (~0u: none)
   // Tile headers (first entry, count) live in a 4-slot LDS ring indexed by the tile's position in
   // the block's sequence.  Thread 0 loads the header of the tile two ahead into registers at the
@@ -978,11 +978,6 @@ void fda_bwd_tile_kernel(const Args a) {
           rowi_l[pos] = ri[e];
         }
       __syncthreads();
-      if (npf) {   // the next chunk's stash (its entries have arrived by now)
-#pragma unroll
-        for (int e = 0; e < KPT; ++e) pS[e] = a.stash[pE[e]];
-      }
-      pf = npf;
       // 3b. grad_output rows into LDS in sorted order: 16-byte pieces loaded by the memory unit
       // straight into LDS (global_load_lds_dwordx4: lane k of a wave fills base + 16*k), no
       // registers held; piece i is part i % PPR of the row of sorted entry i / PPR.  A wave's
@@ -1002,6 +997,16 @@ void fda_bwd_tile_kernel(const Args a) {
         __builtin_amdgcn_s_waitcnt(0);   // the pieces are in LDS before the barrier below
       }
       __syncthreads();
+      // The next chunk's stash, issued now, after the row loads' wait: it arrives during the owner
+      // phase, which no wait ends (the next wait is the next chunk's).  Issued before the row
+      // loads, it was waited for with them (c4 tile kernel 250 -> 241 us, c5 2932 -> 2841 us).
+      // Touching the next chunk's grad_output rows here as well, so that their sorted loads would
+      // find them in L2, was slower (c4 +10 us, c5 +700 us: the touches compete with the misses).
+      if (npf) {
+#pragma unroll
+        for (int e = 0; e < KPT; ++e) pS[e] = a.stash[pE[e]];
+      }
+      pf = npf;
       // 4. owners gather from LDS
       if (live) {
 #pragma unroll
