@@ -688,21 +688,6 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
 // are scheduled coarse levels first (their tiles hold the most entries), and with G % 8 == 0
 // the tiles of head g run on XCD g % 8, whose L2 then holds that head's grad_output rows.
 
-// Inclusive prefix sum over the 64 lanes of a wave: a Hillis-Steele scan inside each row of 16
-// lanes (DPP row shifts; lanes shifted in from outside the row read 0), then the totals of the
-// rows before added from lanes 15, 31, 47.
-__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v) {
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, true);   // row_shr:1
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, true);   // row_shr:2
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, true);   // row_shr:4
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, true);   // row_shr:8
-  const uint32_t t0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 15);
-  const uint32_t t1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 31);
-  const uint32_t t2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 47);
-  const int row = (int)(threadIdx.x & (kWave - 1)) >> 4;
-  return v + (row > 0 ? t0 : 0u) + (row > 1 ? t1 : 0u) + (row > 2 ? t2 : 0u);
-}
-
 // Waves per SIMD the tile kernel runs at: its LDS chunk sizing puts three 256-thread blocks, two
 // 512-thread blocks or one 1024-thread block on a CU (3, 4, 4 waves per SIMD); compiling for no
 // more than that leaves the register allocator all the registers those waves can have.

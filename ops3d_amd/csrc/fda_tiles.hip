@@ -177,12 +177,7 @@ __device__ __forceinline__ uint32_t block_scan(const uint32_t *cnt, uint32_t n, 
   uint32_t sum = 0;
   for (uint32_t i = 0; i < per; ++i)
     if (b0 + i < n) sum += cnt[b0 + i];
-  uint32_t inc = sum;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const uint32_t y = __shfl_up(inc, o, kWave);
-    if (lane >= o) inc += y;
-  }
+  uint32_t inc = wave_inclusive_scan(sum);
   if (lane == kWave - 1) scan_tmp[wv] = inc;
   __syncthreads();
   if (tid == 0) {
@@ -277,13 +272,8 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
       for (uint32_t t0 = 0; t0 < T_h; t0 += kBucketThreads) {
         const uint32_t t = t0 + (uint32_t)tid;
         const uint32_t x = t < T_h ? __hip_atomic_load(&a.counts[w0 + t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
-        uint32_t inc = x;
+        const uint32_t inc = wave_inclusive_scan(x);
         const int lane = tid & (kWave - 1), wv = tid / kWave;
-#pragma unroll
-        for (int o = 1; o < kWave; o <<= 1) {
-          const uint32_t y = __shfl_up(inc, o, kWave);
-          if (lane >= o) inc += y;
-        }
         if (lane == kWave - 1) scan_tmp[wv] = inc;
         __syncthreads();
         uint32_t wofs = 0, all = 0;
@@ -451,12 +441,7 @@ __global__ __launch_bounds__(kScanThreads) void tile_headscan_kernel(const Bucke
   for (uint32_t base = 0; base < T_h; base += kScanThreads) {
     const uint32_t t = base + (uint32_t)tid;
     const uint32_t x = t < T_h ? a.counts[bg * T_h + t] : 0u;
-    uint32_t inc = x;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-      const uint32_t y = __shfl_up(inc, o, kWave);
-      if (lane >= o) inc += y;
-    }
+    uint32_t inc = wave_inclusive_scan(x);
     if (lane == kWave - 1) tmp[w] = inc;
     __syncthreads();
     uint32_t wofs = 0, all = 0;
