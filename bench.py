@@ -317,6 +317,35 @@ def measure_dcnv4(steps, warmup, device, dtype="bf16"):
             "samples": B * D_ * H_ * W_ * G * K}
 
 
+def measure_atomic_baseline(w, steps, warmup, device):
+    """grad_value by the reference's scheme (one fp32 atomic add per sample, corner and channel;
+    ops3d_fda_scatter_baseline, with its clearing of the fp32 buffer) against the library's whole
+    backward (which also computes grad_sampling_loc_attn), both on device-resident inputs of `w`."""
+    import torch
+
+    from ops3d_amd import _C
+    from ops3d_amd.workloads import make_inputs
+
+    x = make_inputs(w, seed=0, device=device)
+    args = (x["value"], x["spatial_shapes"], x["level_start_index"], x["sampling_loc_attn"], x["grad_output"])
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        for a, b in evs:
+            a.record()
+            fn()
+            b.record()
+        torch.cuda.synchronize()
+        return statistics.median(a.elapsed_time(b) for a, b in evs)
+
+    atomic = timed(lambda: _C.scatter_baseline(*args, w.K))
+    gather = timed(lambda: _C.flash_deform_attn_backward(*args, 64, w.K))
+    adds = w.samples() * 8 * w.D   # upper bound: corners outside the volume add nothing
+    return {"atomic_ms": atomic, "backward_ms": gather, "atomic_adds": adds}
+
+
 def measure(w, dtype, steps, warmup, device, with_kernels=True, fwd_only=False):
     b = Bench(w, dtype, device)
     res = {"workload": w.name, "dtype": dtype}
@@ -442,6 +471,9 @@ def main():
     ap.add_argument("--dcn", action="store_true", help="only DCNv4-3D fwd and fwd+bwd (stderr)")
     ap.add_argument("--offsets", action="store_true",
                     help="only the offset-mode op against the unfused caller at --config (stderr)")
+    ap.add_argument("--atomic-baseline", action="store_true",
+                    help="only grad_value by the reference's fp32 atomic scatter against the library's "
+                         "backward, at --config (stderr)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB, 5 times (HBM counter calibration)")
     args = ap.parse_args()
@@ -499,6 +531,14 @@ def main():
         log(f" {args.config} offsets | fwd+bwd fused (FlashDeformAttnFromOffsets) {o['fused']['median'] * 1e3:8.1f} us"
             f" | unfused caller (ref + off/size, cat, packed op) {o['unfused']['median'] * 1e3:8.1f} us")
         return
+    if args.atomic_baseline or args.all:
+        name = args.config if args.atomic_baseline else "c4"
+        o = measure_atomic_baseline(WORKLOADS[name], max(3, min(args.steps, 10)), 2, dev)
+        log(f" {name} grad_value by fp32 atomics (reference scheme) {o['atomic_ms'] * 1e3:9.1f} us "
+            f"({o['atomic_adds'] / (o['atomic_ms'] * 1e-3) / 1e9:.0f} G adds/s) | library backward (all "
+            f"gradients) {o['backward_ms'] * 1e3:8.1f} us")
+        if args.atomic_baseline:
+            return
     if args.kernels_only:
         w = WORKLOADS[args.config]
         b = Bench(w, w.dtype, dev)
