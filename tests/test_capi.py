@@ -160,3 +160,19 @@ def test_offsets_argument_errors_before_device_work(lib):
     # nothing to do (Q = 0): no check of the reference points, success
     rc = lib.ops3d_fda_forward_offsets(p, p, p, p, None, 1, p, None, 0, 2, 1, 576, 8, 32, 2, 0, 4, 64, None)
     assert rc == 0
+
+
+def test_scatter_baseline_argument_errors_before_device_work(lib):
+    """The atomic-scatter measurement baseline validates like the other entry points."""
+    f = lib.ops3d_fda_scatter_baseline
+    args = dict(dtype=2, B=1, S=576, G=8, D=32, L=2, Q=576, K=4)
+
+    def call(**kw):
+        a = {**args, **kw}
+        return f(None, None, None, None, None, a["dtype"], a["B"], a["S"], a["G"], a["D"], a["L"], a["Q"],
+                 a["K"], None)
+
+    assert call(D=20) == 1 and b"unsupported channels" in lib.ops3d_fda_last_error()
+    assert call(L=6) == 1
+    assert call(dtype=7) == 1
+    assert call() == 1 and b"NULL" in lib.ops3d_fda_last_error()
