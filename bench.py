@@ -370,7 +370,7 @@ def measure(w, dtype, steps, warmup, device, with_kernels=True, fwd_only=False):
     return res
 
 
-def cpu_baseline(w, target_s=4.0, reps=3):
+def cpu_baseline(w, target_s=4.0, reps=5, warmup=2):
     """fp32 PyTorch naive path on the host CPU, fwd+bwd over a query slice of `w`."""
     import torch
 
@@ -393,6 +393,8 @@ def cpu_baseline(w, target_s=4.0, reps=3):
         if dt >= target_s / 4 or nq >= w.nq:
             break
         nq = min(w.nq, nq * max(2, int(target_s / 4 / max(dt, 1e-3))))
+    for _ in range(warmup):   # the sizing run above was the first
+        torch_port.forward_backward(inp["value"], inp["shapes"], inp["sampling_loc_attn"], inp["grad_output"], w.K)
     ts = []
     for _ in range(reps):
         t0 = time.perf_counter()
@@ -411,10 +413,10 @@ def cpu_baseline(w, target_s=4.0, reps=3):
     except OSError:
         pass
     if scaled:
-        what = (f"on {nq} of {w.nq} queries of {w.name}, median of {reps}, {t:.2f} s per rep, scaled "
+        what = (f"on {nq} of {w.nq} queries of {w.name}, median of {reps} after {warmup + 1} untimed, {t:.2f} s per rep, scaled "
                 f"linearly to the full query count ({t_full * 1e3:.0f} ms)")
     else:
-        what = f"on all {w.nq} queries of {w.name}, median of {reps}, {t:.2f} s per rep"
+        what = f"on all {w.nq} queries of {w.name}, median of {reps} after {warmup + 1} untimed, {t:.2f} s per rep"
     return {
         "value": round(by / t_full / 1e9, 4),
         "unit": "GB/s",
