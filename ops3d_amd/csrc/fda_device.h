@@ -369,10 +369,17 @@ __device__ __forceinline__ void add_ref_grad(const Args &a, int64_t bq, int j, c
   }
 }
 
+// Modes of the query-major kernels, fixed at compile time so that the packed path carries no
+// branch of the others: packed normalised locations, offsets around reference points (Args::ref)
+// and DCNv4-3D (Args::dcn).
+constexpr int kModePlain = 0, kModeOffsets = 1, kModeDcn = 2;
+
 // Element offset of unit (b*Q + q)*G + g's record in loc_attn / grad_loc_attn: P per unit, or
 // (DCNv4-3D) rows of rec_stride per (b, q).
+template <int MODE>
 __device__ __forceinline__ int64_t record_offset(const Args &a, int64_t unit) {
-  return a.rec_stride ? (unit / a.G) * a.rec_stride + (unit % a.G) * a.P : unit * a.P;
+  if constexpr (MODE == kModeDcn) return (unit / a.G) * a.rec_stride + (unit % a.G) * a.P;
+  return unit * a.P;
 }
 
 // DCNv4-3D mode: turn the staged offsets of unit (b, q) into pixel coordinates of the input

@@ -80,7 +80,7 @@ __device__ __forceinline__ void load_global_elems(const T *p, float *f) {
 }
 
 // ---------------------------------------------------------------------------------------------
-template <typename T, int CPL, int LPU>
+template <typename T, int CPL, int LPU, int MODE>
 __global__ __launch_bounds__(kBlock) void fda_forward_kernel(const Args a) {
   extern __shared__ float lds[];
   constexpr int UPW = kWave / LPU, UPB = kWavesPerBlock * UPW;
@@ -95,17 +95,17 @@ __global__ __launch_bounds__(kBlock) void fda_forward_kernel(const Args a) {
   float *rec = lds + ub * (P + 1);
   const int64_t unit = ((int64_t)b * a.Q + (live ? q : 0)) * a.G + g;
 
-  stage_record<T, LPU>(static_cast<const T *>(a.loc_attn) + record_offset(a, unit), P, j, live, rec);
+  stage_record<T, LPU>(static_cast<const T *>(a.loc_attn) + record_offset<MODE>(a, unit), P, j, live, rec);
   wave_lds_sync();
-  if (a.ref) {
+  if constexpr (MODE == kModeOffsets) {
     offsets_to_locations<T, LPU>(a, unit / a.G, j, live, rec);
     wave_lds_sync();
   }
-  if (a.dcn) {
+  if constexpr (MODE == kModeDcn) {
     dcn_to_pixels<LPU>(a, live ? q : 0, j, rec);
     wave_lds_sync();
   }
-  if (!a.dcn || a.dcn_softmax) unit_softmax<LPU>(rec + 3 * LK, LK, j);
+  if (MODE != kModeDcn || a.dcn_softmax) unit_softmax<LPU>(rec + 3 * LK, LK, j);
   wave_lds_sync();
 
   float acc[CPL];
@@ -129,7 +129,7 @@ __global__ __launch_bounds__(kBlock) void fda_forward_kernel(const Args a) {
       const int kj = k0 + (j < NG ? j : 0);
       const int sj = l * K + (kj < K ? kj : K - 1);
       Sample ms;
-      sample_setup(rec[3 * sj], rec[3 * sj + 1], rec[3 * sj + 2], Wl, Hl, Dl, RST, ms, a.dcn != 0);
+      sample_setup(rec[3 * sj], rec[3 * sj + 1], rec[3 * sj + 2], Wl, Hl, Dl, RST, ms, MODE == kModeDcn);
       if (!live) {   // a dead unit loads zeros
 #pragma unroll
         for (int c = 0; c < 8; ++c) ms.off[c] = OOB_ELEM;
@@ -180,7 +180,7 @@ __global__ __launch_bounds__(kBlock) void fda_forward_kernel(const Args a) {
 // two 64-byte loads when x0 is even.  Gathers of random rows cost per distinct 128-byte line,
 // not per byte, so this halves the gather work per sample.  Each half accumulates its own x-row
 // over all samples; the halves are summed once at the end.
-template <typename T, int CPL, bool kPairs>
+template <typename T, int CPL, bool kPairs, int MODE>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kFwdWavesPerEU))) void fda_forward_pair_kernel(const Args a) {
   extern __shared__ float lds[];
   constexpr int LPU = 4, UL = 2 * LPU;
@@ -199,17 +199,17 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kFwdWave
   float *rec = lds + ub * (P + 1);
   const int64_t unit = ((int64_t)b * a.Q + (live ? q : 0)) * a.G + g;
 
-  stage_record<T, UL>(static_cast<const T *>(a.loc_attn) + record_offset(a, unit), P, ju, live, rec);
+  stage_record<T, UL>(static_cast<const T *>(a.loc_attn) + record_offset<MODE>(a, unit), P, ju, live, rec);
   wave_lds_sync();
-  if (a.ref) {
+  if constexpr (MODE == kModeOffsets) {
     offsets_to_locations<T, UL>(a, unit / a.G, ju, live, rec);
     wave_lds_sync();
   }
-  if (a.dcn) {
+  if constexpr (MODE == kModeDcn) {
     dcn_to_pixels<UL>(a, live ? q : 0, ju, rec);
     wave_lds_sync();
   }
-  if (!a.dcn || a.dcn_softmax) unit_softmax<UL>(rec + 3 * LK, LK, ju);
+  if (MODE != kModeDcn || a.dcn_softmax) unit_softmax<UL>(rec + 3 * LK, LK, ju);
   wave_lds_sync();
 
   float acc[CPL];
@@ -235,7 +235,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kFwdWave
       const int kj = k0 + (ju & 3);
       const int sj = l * K + (kj < K ? kj : K - 1);
       Sample ms;
-      sample_setup(rec[3 * sj], rec[3 * sj + 1], rec[3 * sj + 2], Wl, Hl, Dl, RST, ms, a.dcn != 0);
+      sample_setup(rec[3 * sj], rec[3 * sj + 1], rec[3 * sj + 2], Wl, Hl, Dl, RST, ms, MODE == kModeDcn);
       uint32_t off4[4];
       float w4[4];
       // corner weights times the sample's attention weight (made once per set-up, not per channel)
@@ -286,7 +286,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kFwdWave
 // set-ups are made once per quad (lane k of a quad sets up sample k0+k) and broadcast by DPP;
 // the lane that made a set-up also records that sample's stash and base corner.  The partials
 // of grad_loc / grad_attn of a lane's x-row are summed over the unit's 8 lanes.
-template <typename T, int CPL, bool kPairs>
+template <typename T, int CPL, bool kPairs, int MODE>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kQueryWavesPerEU))) void fda_bwd_query_pair_kernel(const Args a) {
   extern __shared__ float lds[];
   constexpr int UL = 8;
@@ -324,17 +324,17 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kQueryWa
   }
   __syncthreads();
 
-  stage_record<T, UL>(static_cast<const T *>(a.loc_attn) + record_offset(a, unit), P, ju, live, rec);
+  stage_record<T, UL>(static_cast<const T *>(a.loc_attn) + record_offset<MODE>(a, unit), P, ju, live, rec);
   wave_lds_sync();
-  if (a.ref) {
+  if constexpr (MODE == kModeOffsets) {
     offsets_to_locations<T, UL>(a, unit / a.G, ju, live, rec);
     wave_lds_sync();
   }
-  if (a.dcn) {
+  if constexpr (MODE == kModeDcn) {
     dcn_to_pixels<UL>(a, live ? q : 0, ju, rec);
     wave_lds_sync();
   }
-  if (!a.dcn || a.dcn_softmax) unit_softmax<UL>(rec + 3 * LK, LK, ju);
+  if (MODE != kModeDcn || a.dcn_softmax) unit_softmax<UL>(rec + 3 * LK, LK, ju);
   wave_lds_sync();
 
   constexpr int NW = CPL * (int)sizeof(T) / 4;
@@ -370,7 +370,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kQueryWa
       const bool have = kq < K;
       const int sj = l * K + (have ? kq : K - 1);
       Sample ms;
-      const bool in_s = sample_setup(rec[3 * sj], rec[3 * sj + 1], rec[3 * sj + 2], Wl, Hl, Dl, RST, ms, a.dcn != 0) && live;
+      const bool in_s = sample_setup(rec[3 * sj], rec[3 * sj + 1], rec[3 * sj + 2], Wl, Hl, Dl, RST, ms, MODE == kModeDcn) && live;
       if (dxl == 0 && have) {
         cx_s[sj] = in_s ? (uint32_t)(ms.x0 + 1) : kKeyInvalid;
         cy_s[sj] = (uint32_t)(ms.y0 + 1);
@@ -425,9 +425,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kQueryWa
             const float at = rec[3 * LK + su];
             // d(pixel)/d(loc) = size (grid_sample: size/2 per unit of grid, grid = 2*loc - 1);
             // offset mode: d(pixel)/d(offset) = 1; DCNv4-3D: d(pixel)/d(offset) = offset_scale
-            rec[3 * su] = gx * at * (a.dcn ? a.offset_scale : (a.ref ? 1.f : (float)Wl));
-            rec[3 * su + 1] = gy * at * (a.dcn ? a.offset_scale : (a.ref ? 1.f : (float)Hl));
-            rec[3 * su + 2] = gz * at * (a.dcn ? a.offset_scale : (a.ref ? 1.f : (float)Dl));
+            rec[3 * su] = gx * at * (MODE == kModeDcn ? a.offset_scale : (MODE == kModeOffsets ? 1.f : (float)Wl));
+            rec[3 * su + 1] = gy * at * (MODE == kModeDcn ? a.offset_scale : (MODE == kModeOffsets ? 1.f : (float)Hl));
+            rec[3 * su + 2] = gz * at * (MODE == kModeDcn ? a.offset_scale : (MODE == kModeOffsets ? 1.f : (float)Dl));
             gat_s[su] = ga;
           }
         }
@@ -468,18 +468,19 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kQueryWa
   float dot = 0.f;
   for (int t = ju; t < LK; t += UL) dot = fmaf(rec[3 * LK + t], gat_s[t], dot);
   dot = unit_sum<UL>(dot);
-  const bool raw_mask = a.dcn && !a.dcn_softmax;   // DCNv4-3D without softmax: d(mask) = d(attn)
+  const bool raw_mask = MODE == kModeDcn && !a.dcn_softmax;   // DCNv4-3D without softmax: d(mask) = d(attn)
   for (int t = ju; t < LK; t += UL) {
     const float at = rec[3 * LK + t];
     rec[3 * LK + t] = raw_mask ? gat_s[t] : at * (gat_s[t] - dot);
   }
   wave_lds_sync();
-  if (live && a.grad_ref) add_ref_grad<UL>(a, unit / a.G, ju, rec);
-  if (live) write_record<T, UL>(static_cast<T *>(a.grad_loc_attn) + record_offset(a, unit), P, ju, rec);
+  if constexpr (MODE == kModeOffsets)
+    if (live && a.grad_ref) add_ref_grad<UL>(a, unit / a.G, ju, rec);
+  if (live) write_record<T, UL>(static_cast<T *>(a.grad_loc_attn) + record_offset<MODE>(a, unit), P, ju, rec);
   clear_tile_counts(a);
 }
 
-template <typename T, int CPL, int LPU>
+template <typename T, int CPL, int LPU, int MODE>
 __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
   extern __shared__ float lds[];
   constexpr int UPW = kWave / LPU, UPB = kWavesPerBlock * UPW;
@@ -513,17 +514,17 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
   }
   __syncthreads();
 
-  stage_record<T, LPU>(static_cast<const T *>(a.loc_attn) + record_offset(a, unit), P, j, live, rec);
+  stage_record<T, LPU>(static_cast<const T *>(a.loc_attn) + record_offset<MODE>(a, unit), P, j, live, rec);
   wave_lds_sync();
-  if (a.ref) {
+  if constexpr (MODE == kModeOffsets) {
     offsets_to_locations<T, LPU>(a, unit / a.G, j, live, rec);
     wave_lds_sync();
   }
-  if (a.dcn) {
+  if constexpr (MODE == kModeDcn) {
     dcn_to_pixels<LPU>(a, live ? q : 0, j, rec);
     wave_lds_sync();
   }
-  if (!a.dcn || a.dcn_softmax) unit_softmax<LPU>(rec + 3 * LK, LK, j);
+  if (MODE != kModeDcn || a.dcn_softmax) unit_softmax<LPU>(rec + 3 * LK, LK, j);
   wave_lds_sync();
 
   // the unit's grad_output channels as raw words (dot products run on the packed elements)
@@ -566,7 +567,7 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
         const float lx = rec[3 * su], ly = rec[3 * su + 1], lz = rec[3 * su + 2];
         at[u] = rec[3 * LK + su];
         // branch-free: a sample outside the volume (or of a dead unit) loads zeros, weighs zero
-        in[u] = sample_setup(lx, ly, lz, Wl, Hl, Dl, RST, sm[u], a.dcn != 0) && live && u < nk;
+        in[u] = sample_setup(lx, ly, lz, Wl, Hl, Dl, RST, sm[u], MODE == kModeDcn) && live && u < nk;
         if (!live || u >= nk) {
 #pragma unroll
           for (int c = 0; c < 8; ++c) sm[u].off[c] = OOB_ELEM;
@@ -607,9 +608,9 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
           const int su = s + u;
           // d(pixel)/d(loc) = size (grid_sample: size/2 per unit of grid, grid = 2*loc - 1);
           // offset mode: d(pixel)/d(offset) = 1; DCNv4-3D: d(pixel)/d(offset) = offset_scale
-          rec[3 * su] = gx * at[u] * (a.dcn ? a.offset_scale : (a.ref ? 1.f : (float)Wl));
-          rec[3 * su + 1] = gy * at[u] * (a.dcn ? a.offset_scale : (a.ref ? 1.f : (float)Hl));
-          rec[3 * su + 2] = gz * at[u] * (a.dcn ? a.offset_scale : (a.ref ? 1.f : (float)Dl));
+          rec[3 * su] = gx * at[u] * (MODE == kModeDcn ? a.offset_scale : (MODE == kModeOffsets ? 1.f : (float)Wl));
+          rec[3 * su + 1] = gy * at[u] * (MODE == kModeDcn ? a.offset_scale : (MODE == kModeOffsets ? 1.f : (float)Hl));
+          rec[3 * su + 2] = gz * at[u] * (MODE == kModeDcn ? a.offset_scale : (MODE == kModeOffsets ? 1.f : (float)Dl));
           gat_s[su] = ga;
           cx_s[su] = in[u] ? (uint32_t)(m.x0 + 1) : kKeyInvalid;
           cy_s[su] = (uint32_t)(m.y0 + 1);
@@ -657,14 +658,15 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
   float dot = 0.f;
   for (int t = j; t < LK; t += LPU) dot = fmaf(rec[3 * LK + t], gat_s[t], dot);
   dot = unit_sum<LPU>(dot);
-  const bool raw_mask = a.dcn && !a.dcn_softmax;   // DCNv4-3D without softmax: d(mask) = d(attn)
+  const bool raw_mask = MODE == kModeDcn && !a.dcn_softmax;   // DCNv4-3D without softmax: d(mask) = d(attn)
   for (int t = j; t < LK; t += LPU) {
     const float at = rec[3 * LK + t];
     rec[3 * LK + t] = raw_mask ? gat_s[t] : at * (gat_s[t] - dot);
   }
   wave_lds_sync();
-  if (live && a.grad_ref) add_ref_grad<LPU>(a, unit / a.G, j, rec);
-  if (live) write_record<T, LPU>(static_cast<T *>(a.grad_loc_attn) + record_offset(a, unit), P, j, rec);
+  if constexpr (MODE == kModeOffsets)
+    if (live && a.grad_ref) add_ref_grad<LPU>(a, unit / a.G, j, rec);
+  if (live) write_record<T, LPU>(static_cast<T *>(a.grad_loc_attn) + record_offset<MODE>(a, unit), P, j, rec);
   clear_tile_counts(a);
 }
 
@@ -1127,7 +1129,7 @@ __global__ __launch_bounds__(kBlock) void fda_scatter_baseline_kernel(const Args
   const int L = a.L, K = a.K, LK = L * K, P = a.P;
   float *rec = lds + ub * (P + 1);
   const int64_t unit = ((int64_t)b * a.Q + (live ? q : 0)) * a.G + g;
-  stage_record<T, UL>(static_cast<const T *>(a.loc_attn) + record_offset(a, unit), P, ju, live, rec);
+  stage_record<T, UL>(static_cast<const T *>(a.loc_attn) + record_offset<kModePlain>(a, unit), P, ju, live, rec);
   wave_lds_sync();
   unit_softmax<UL>(rec + 3 * LK, LK, ju);
   wave_lds_sync();
@@ -1234,27 +1236,37 @@ __global__ __launch_bounds__(tile_threads(LPU)) void fda_bwd_split_combine_kerne
 }
 
 // which: 0 forward, 1 backward phase 1 (query-major), 2 backward phase 3 (tile-major)
-template <typename T, int CPL, int LPU>
-hipError_t launch_one(int which, const Args &a, unsigned grid, size_t lds, hipStream_t st) {
+template <typename T, int CPL, int LPU, int MODE>
+void launch_query_major(int which, const Args &a, unsigned grid, size_t lds, hipStream_t st) {
   if (which == 0) {
     if constexpr (fwd_pairs(CPL, LPU, (int)sizeof(T))) {
       if (a.pair_levels)
-        hipLaunchKernelGGL((fda_forward_pair_kernel<T, CPL, true>), dim3(grid), dim3(kBlock), lds, st, a);
+        hipLaunchKernelGGL((fda_forward_pair_kernel<T, CPL, true, MODE>), dim3(grid), dim3(kBlock), lds, st, a);
       else
-        hipLaunchKernelGGL((fda_forward_pair_kernel<T, CPL, false>), dim3(grid), dim3(kBlock), lds, st, a);
+        hipLaunchKernelGGL((fda_forward_pair_kernel<T, CPL, false, MODE>), dim3(grid), dim3(kBlock), lds, st, a);
+    } else {
+      hipLaunchKernelGGL((fda_forward_kernel<T, CPL, LPU, MODE>), dim3(grid), dim3(kBlock), lds, st, a);
     }
-    else
-      hipLaunchKernelGGL((fda_forward_kernel<T, CPL, LPU>), dim3(grid), dim3(kBlock), lds, st, a);
-  }
-  else if (which == 1) {
+  } else {
     if constexpr (fwd_pairs(CPL, LPU, (int)sizeof(T))) {
       if (a.pair_levels)
-        hipLaunchKernelGGL((fda_bwd_query_pair_kernel<T, CPL, true>), dim3(grid), dim3(kBlock), lds, st, a);
+        hipLaunchKernelGGL((fda_bwd_query_pair_kernel<T, CPL, true, MODE>), dim3(grid), dim3(kBlock), lds, st, a);
       else
-        hipLaunchKernelGGL((fda_bwd_query_pair_kernel<T, CPL, false>), dim3(grid), dim3(kBlock), lds, st, a);
+        hipLaunchKernelGGL((fda_bwd_query_pair_kernel<T, CPL, false, MODE>), dim3(grid), dim3(kBlock), lds, st, a);
+    } else {
+      hipLaunchKernelGGL((fda_bwd_query_kernel<T, CPL, LPU, MODE>), dim3(grid), dim3(kBlock), lds, st, a);
     }
-    else
-      hipLaunchKernelGGL((fda_bwd_query_kernel<T, CPL, LPU>), dim3(grid), dim3(kBlock), lds, st, a);
+  }
+}
+
+// which: 0 forward, 1 backward phase 1 (query-major), 2 backward phase 3 (tile-major),
+// 3 split-tile combine, 5 the atomic-scatter measurement baseline
+template <typename T, int CPL, int LPU>
+hipError_t launch_one(int which, const Args &a, unsigned grid, size_t lds, hipStream_t st) {
+  if (which == 0 || which == 1) {
+    if (a.dcn) launch_query_major<T, CPL, LPU, kModeDcn>(which, a, grid, lds, st);
+    else if (a.ref) launch_query_major<T, CPL, LPU, kModeOffsets>(which, a, grid, lds, st);
+    else launch_query_major<T, CPL, LPU, kModePlain>(which, a, grid, lds, st);
   }
   else if (which == 5) {
     hipLaunchKernelGGL((fda_scatter_baseline_kernel<T, CPL, LPU>), dim3(grid), dim3(kBlock), lds, st, a);
