@@ -29,7 +29,7 @@ OPS3D_FDA_API int ops3d_roi_align3d_forward(const void *features, const void *ro
                                             float spatial_scale, int sampling_ratio, int order, void *stream);
 
 /* Bytes of fp32 workspace ops3d_roi_align3d_backward needs for output bins PD x PH x PW: 0 when
- * PD, PH, PW <= 64 and PD*PH*PW <= 512 (the backward is then a gather straight into grad_input),
+ * PD, PH, PW <= 64 and PD*PH*PW <= 384 (the backward is then a gather straight into grad_input),
  * else N*C*D*H*W*4 (the gradient is accumulated channels-last in fp32 by atomics, then
  * transposed into grad_input). */
 OPS3D_FDA_API size_t ops3d_roi_align3d_backward_workspace_bytes(int dtype, int N, int C, int D, int H, int W, int PD,
@@ -37,7 +37,9 @@ OPS3D_FDA_API size_t ops3d_roi_align3d_backward_workspace_bytes(int dtype, int N
 
 /*
  * Backward: grad_input [N,C,D,H,W] = the adjoint of the forward applied to grad_output
- * [R,C,PD,PH,PW]; every element of grad_input is written.  With the bin limits above it is a
+ * [R,C,PD,PH,PW]; every element of grad_input is written: its old contents are overwritten
+ * (the reference's kernel adds into a buffer its caller zeroed; a caller accumulating gradients
+ * adds the result itself).  With the bin limits above it is a
  * gather: each voxel sums the rois that reach it in roi order, the same bits on every run; else
  * the samples' corner contributions are added by fp32 atomics into the cleared workspace, whose
  * order -- and so the last bit -- can differ between runs, as with the reference's atomics.

@@ -9,10 +9,10 @@
 // (std::invalid_argument, as the reference's), OPS3D_FDA_ERUNTIME raises RuntimeError.
 #include <torch/extension.h>
 
-// torch's ROCm build reports HIP devices as device type cuda: the guard and stream accessors
-// are the "masquerading" ones
-#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
-#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+// torch's current HIP stream of a device (c10's native HIP API); the device is made current
+// with HIP's own calls (DeviceGuard below)
+#include <c10/hip/HIPStream.h>
+#include <hip/hip_runtime_api.h>
 
 #include <stdexcept>
 #include <string>
@@ -86,8 +86,28 @@ void raise(int rc, const char *what) {
 }
 
 hipStream_t stream_of(const at::Tensor &value) {
-  return c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(value.device().index()).stream();
+  return c10::hip::getCurrentHIPStream(value.device().index()).stream();
 }
+
+// Makes value's device current for the call and restores the previous one (the reference's
+// entry points rely on the current device; torch's own guard types for ROCm label HIP devices
+// as cuda, so plain HIP calls are used here).
+class DeviceGuard {
+ public:
+  explicit DeviceGuard(const c10::Device &d) {
+    if (hipGetDevice(&prev_) != hipSuccess) prev_ = -1;
+    if (d.has_index() && d.index() != prev_ && hipSetDevice(d.index()) == hipSuccess) set_ = true;
+  }
+  ~DeviceGuard() {
+    if (set_ && prev_ >= 0) (void)hipSetDevice(prev_);
+  }
+  DeviceGuard(const DeviceGuard &) = delete;
+  DeviceGuard &operator=(const DeviceGuard &) = delete;
+
+ private:
+  int prev_ = -1;
+  bool set_ = false;
+};
 
 void *ptr(const at::Tensor &t) { return t.defined() && t.numel() > 0 ? t.data_ptr() : nullptr; }
 
@@ -105,7 +125,7 @@ std::tuple<at::Tensor, c10::optional<at::Tensor>> forward_keep_head_major(
     const at::Tensor &value, const at::Tensor &shapes, const at::Tensor &lsi, const at::Tensor &sla,
     int64_t im2col_step, int64_t K) {
   const Sizes z = common(value, shapes, lsi, sla, K);
-  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(value.device());
+  const DeviceGuard guard(value.device());
   at::Tensor out = at::empty({z.B, z.Q, (int64_t)z.G * z.D}, value.options());
   const size_t n = ops3d_fda_forward_workspace_bytes(z.code, z.B, z.S, z.G, z.D, z.L, z.Q, z.K);
   c10::optional<at::Tensor> ws;
@@ -133,7 +153,7 @@ std::vector<at::Tensor> backward_with_head_major(const at::Tensor &value,
       throw std::invalid_argument("value_head_major is not a forward workspace of this value");
     vhm = h.data_ptr();
   }
-  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(value.device());
+  const DeviceGuard guard(value.device());
   at::Tensor grad_value = at::empty_like(value);
   at::Tensor grad_sla = at::empty_like(sla);
   const size_t n = ops3d_fda_backward_workspace_bytes(z.code, z.B, z.S, z.G, z.D, z.L, z.Q, z.K);
@@ -163,7 +183,7 @@ std::tuple<at::Tensor, c10::optional<at::Tensor>> forward_offsets(
     const at::Tensor &reference_points, int64_t im2col_step, int64_t K) {
   const Sizes z = common(value, shapes, lsi, offset_attn, K);
   const int R = ref_levels_of(reference_points, value, z);
-  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(value.device());
+  const DeviceGuard guard(value.device());
   at::Tensor out = at::empty({z.B, z.Q, (int64_t)z.G * z.D}, value.options());
   const size_t n = ops3d_fda_forward_workspace_bytes(z.code, z.B, z.S, z.G, z.D, z.L, z.Q, z.K);
   c10::optional<at::Tensor> ws;
@@ -194,7 +214,7 @@ std::vector<at::Tensor> backward_offsets(const at::Tensor &value, const c10::opt
       throw std::invalid_argument("value_head_major is not a forward workspace of this value");
     vhm = h.data_ptr();
   }
-  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(value.device());
+  const DeviceGuard guard(value.device());
   at::Tensor grad_value = at::empty_like(value);
   at::Tensor grad_oa = at::empty_like(offset_attn);
   at::Tensor grad_ref;
@@ -237,7 +257,7 @@ at::Tensor nms_3d(const at::Tensor &dets, const at::Tensor &scores, double thres
   if (dets.dim() != 2 || dets.size(1) != 6) throw std::invalid_argument("dets must be [N, 6] (x1,y1,z1,x2,y2,z2)");
   if (scores.dim() != 1 || scores.size(0) != dets.size(0) || scores.device() != dets.device())
     throw std::invalid_argument("scores must be [N] on the boxes' device");
-  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(dets.device());
+  const DeviceGuard guard(dets.device());
   const at::Tensor order = std::get<1>(scores.sort(/*stable=*/true, /*dim=*/0, /*descending=*/true));
   const at::Tensor boxes = dets.index_select(0, order).to(at::kFloat).contiguous();
   const int n = (int)boxes.size(0);
@@ -272,7 +292,7 @@ void roi_align_3d_forward(const at::Tensor &input, const at::Tensor &rois, at::T
   if (output.dim() != 5 || output.size(0) != r.size(0) || output.size(1) != f.size(1) || output.size(2) != pd ||
       output.size(3) != ph || output.size(4) != pw)
     throw std::invalid_argument("output must be [R, C, out_d, out_h, out_w]");
-  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(input.device());
+  const DeviceGuard guard(input.device());
   const int rc = ops3d_roi_align3d_forward(ptr(f), ptr(r), ptr(output), code, (int)f.size(0), (int)f.size(1),
                                            (int)f.size(2), (int)f.size(3), (int)f.size(4), (int)r.size(0), (int)pd,
                                            (int)ph, (int)pw, (float)spatial_scale, (int)sampling_ratio, (int)order,
@@ -291,7 +311,7 @@ void roi_align_3d_backward(const at::Tensor &top_grad, const at::Tensor &rois, a
   if (g.dim() != 5 || g.size(0) != r.size(0) || g.size(1) != C || g.size(2) != pd || g.size(3) != ph ||
       g.size(4) != pw)
     throw std::invalid_argument("top_grad must be [R, C, out_d, out_h, out_w]");
-  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(top_grad.device());
+  const DeviceGuard guard(top_grad.device());
   const size_t wsb = ops3d_roi_align3d_backward_workspace_bytes(code, N, C, D, H, W, (int)pd, (int)ph, (int)pw);
   at::Tensor ws;
   if (wsb) ws = at::empty({(int64_t)(wsb / 4)}, top_grad.options().dtype(at::kFloat));
@@ -332,7 +352,7 @@ at::Tensor dcnv4_forward(const at::Tensor &value, const at::Tensor &p_offset, in
   const int Wout = (z.Win + 2 * (int)pw - ((int)dw * ((int)kw - 1) + 1)) / (int)sw + 1;
   if (p_offset.size(0) != z.B || p_offset.size(1) != Dout || p_offset.size(2) != Hout || p_offset.size(3) != Wout)
     throw std::invalid_argument("p_offset must be [B, Dout, Hout, Wout, padded_offset_dim]");
-  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(value.device());
+  const DeviceGuard guard(value.device());
   at::Tensor out = at::empty({z.B, Dout, Hout, Wout, group * group_channels}, value.options());
   const size_t wsb = ops3d_dcnv4_workspace_bytes(z.code, z.B, z.Din, z.Hin, z.Win, (int)group, (int)group_channels,
                                                  (int)kd, (int)kh, (int)kw, (int)sd, (int)sh, (int)sw, (int)pd,
@@ -356,7 +376,7 @@ std::vector<at::Tensor> dcnv4_backward(const at::Tensor &value, const at::Tensor
   const DcnArgs z = dcn_check(value, p_offset, group, group_channels);
   if (!grad_output.is_cuda() || !grad_output.is_contiguous() || grad_output.scalar_type() != value.scalar_type())
     throw std::runtime_error("grad_output tensor has to be a contiguous CUDA tensor of the value dtype");
-  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(value.device());
+  const DeviceGuard guard(value.device());
   at::Tensor grad_value = at::empty_like(value);
   at::Tensor grad_offset = at::zeros_like(p_offset);   // the row padding stays zero
   const size_t wsb = ops3d_dcnv4_workspace_bytes(z.code, z.B, z.Din, z.Hin, z.Win, (int)group, (int)group_channels,

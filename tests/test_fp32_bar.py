@@ -6,9 +6,10 @@ The plain bar rtol 1e-5 / atol 1e-6 holds for the fp32 forward output, grad_valu
 logit gradients, but not for the location gradients: they are sums of cancelling corner
 differences, and fp32 PyTorch breaks the plain bar on some of them by several times.  What it
 needs beyond the plain bar is a small fraction of the random-walk rounding size sqrt(n) u M;
-the allowance oracle.fp32_loc_allowance grants (FP32_LOC_ALLOWANCE_K = 0.15 of it) is sized so
-that fp32 PyTorch uses most of it (between half and all), and the GPU tests hold the kernel to
-the same bar."""
+the allowance oracle.fp32_loc_allowance grants (FP32_LOC_ALLOWANCE_K = 0.15 of it) was sized on
+fp32 PyTorch (torch 2.10: on c1, 113 of 110592 location gradients beyond the plain bar, up to
+4.8x), and the GPU tests hold the kernel to the same bar.  Only the upper bound is asserted:
+how many elements another torch build puts beyond the plain bar is printed, not tested."""
 from __future__ import annotations
 
 import numpy as np
@@ -44,8 +45,8 @@ def _case(name, q_limit):
     }
 
 
-@pytest.mark.parametrize("name,q_limit,min_breaks,min_ratio", [("c1", None, 50, 3.0), ("c4", 1024, 200, 10.0)])
-def test_torch_fp32_needs_the_loc_allowance(name, q_limit, min_breaks, min_ratio):
+@pytest.mark.parametrize("name,q_limit", [("c1", None), ("c4", 1024)])
+def test_torch_fp32_within_the_loc_allowance(name, q_limit):
     res = _case(name, q_limit)
     for key in ("out", "grad_value", "grad_logit"):   # the plain bar holds
         got, exp, _ = res[key]
@@ -56,8 +57,8 @@ def test_torch_fp32_needs_the_loc_allowance(name, q_limit, min_breaks, min_ratio
     raw = ATOL + RTOL * np.abs(exp)
     breaks = int((err > raw).sum())
     ratio = float((err / raw).max())
-    # fp32 PyTorch misses the plain bar on location gradients (c1: 113 of 110592, 4.8x) ...
-    assert breaks >= min_breaks and ratio >= min_ratio, (breaks, ratio)
-    # ... but stays inside it plus the allowance, using most of the allowance
     use = float(((err - raw) / allow).max())
-    assert 0.5 <= use <= 1.0, use
+    print(f"[fp32 bar] {name}: {breaks} location gradients beyond the plain bar (up to {ratio:.1f}x), "
+          f"{use:.2f} of the allowance used", flush=True)
+    # fp32 PyTorch stays inside the plain bar plus the allowance
+    assert use <= 1.0, use

@@ -200,3 +200,28 @@ def test_gpu_module_edges(gpu_device):
         _C.roi_align_3d_forward(x.cpu(), rois.cpu(), torch.empty(2, 4, 2, 2, 2), 2, 2, 2, 1.0, 2, 1)
     with pytest.raises(RuntimeError, match="size_rois should be 7"):
         _C.roi_align_3d_forward(x, rois[:, :6], torch.empty(2, 4, 2, 2, 2, device=gpu_device), 2, 2, 2, 1.0, 2, 1)
+
+
+@pytest.mark.gpu
+def test_gpu_many_overlapping_rois(gpu_device):
+    """The gather backward's grouping at the shape the benchmark times: more than 128 rois (one
+    staging batch holds 128) with 7x7x7 bins, all overlapping one small volume, so every voxel is
+    reached by many rois and the groups are cut by the 384-bin and weight-table limits."""
+    from fda_helpers import assert_close, log
+
+    from ops3d_amd.roi_align import roi_align_3d
+
+    N, C, size, R, pooled = 1, 8, (9, 10, 12), 150, (7, 7, 7)
+    log(f"[case] roi_align3d many overlapping rois: R={R} pooled={pooled} size={size}")
+    r = np.random.default_rng(11)
+    x = torch.from_numpy(r.normal(size=(N, C) + size).astype(np.float32))
+    rois = torch.from_numpy(_rois(R, N, size, seed=12, lo=-1.0, hi=9.0))
+    xg = x.to(gpu_device).requires_grad_(True)
+    out = roi_align_3d(xg, rois.to(gpu_device), pooled, 1.0, 1, 1)
+    g = torch.from_numpy(r.normal(size=tuple(out.shape)).astype(np.float32))
+    out.backward(g.to(gpu_device))
+    torch.cuda.synchronize()
+    want = O.forward(x.double().numpy(), rois.double().numpy(), pooled, 1.0, 1, 1)
+    gwant = O.backward(g.double().numpy(), rois.double().numpy(), x.shape, 1.0, 1, 1)
+    assert_close("overlapping rois output", out.detach(), want, 1e-5, 1e-6)
+    assert_close("overlapping rois grad", xg.grad, gwant, 1e-5, 1e-5)
