@@ -331,12 +331,14 @@ def measure_dcnv4(steps, warmup, device, dtype="bf16"):
 
 
 def measure_atomic_baseline(w, steps, warmup, device):
-    """grad_value by the reference's scheme (one fp32 atomic add per sample, corner and channel;
-    ops3d_fda_scatter_baseline, with its clearing of the fp32 buffer) against the library's whole
-    backward (which also computes grad_sampling_loc_attn), both on device-resident inputs of `w`."""
+    """grad_value by the reference's scheme at the reference's lane layout (one fp32 atomic add per
+    sample, corner and channel, one lane per channel; libops3d_fda_bench.so, with its clearing of
+    the fp32 buffer) against the library's whole backward (which also computes
+    grad_sampling_loc_attn), both on device-resident inputs of `w`; and the LDS float-atomic rate
+    (ds_add_f32), which bounds any scheme that pre-combines the same adds in LDS."""
     import torch
 
-    from ops3d_amd import _C
+    from ops3d_amd import _C, _bench_lib
     from ops3d_amd.workloads import make_inputs
 
     x = make_inputs(w, seed=0, device=device)
@@ -353,10 +355,19 @@ def measure_atomic_baseline(w, steps, warmup, device):
         torch.cuda.synchronize()
         return statistics.median(a.elapsed_time(b) for a, b in evs)
 
-    atomic = timed(lambda: _C.scatter_baseline(*args, w.K))
+    atomic = timed(lambda: _bench_lib.ref_scatter(*args, w.K))
     gather = timed(lambda: _C.flash_deform_attn_backward(*args, 64, w.K))
     adds = w.samples() * 8 * w.D   # upper bound: corners outside the volume add nothing
-    return {"atomic_ms": atomic, "backward_ms": gather, "atomic_adds": adds}
+    blocks, iters = 256 * 8, 4096
+    out = torch.empty(blocks, dtype=torch.float32, device=device)
+    lds = {}
+    for pattern in (0, 1):
+        lds[pattern] = timed(lambda: _bench_lib.lds_atomic(out, blocks, iters, pattern))
+        torch.cuda.synchronize()
+        assert bool((out == 256.0 * iters).all()), "LDS atomic probe lost adds"
+    lds_rate = blocks * 256 * iters / (min(lds.values()) * 1e-3)
+    return {"atomic_ms": atomic, "backward_ms": gather, "atomic_adds": adds, "lds_adds_per_s": lds_rate,
+            "lds_ms": lds, "lds_bound_ms": adds / lds_rate * 1e3}
 
 
 def measure(w, dtype, steps, warmup, device, with_kernels=True, fwd_only=False):
@@ -570,9 +581,11 @@ def main():
     if args.atomic_baseline or args.all:
         name = args.config if args.atomic_baseline else "c4"
         o = measure_atomic_baseline(WORKLOADS[name], max(3, min(args.steps, 10)), 2, dev)
-        log(f" {name} grad_value by fp32 atomics (reference scheme) {o['atomic_ms'] * 1e3:9.1f} us "
+        log(f" {name} grad_value by fp32 atomics (reference scheme and lane layout) {o['atomic_ms'] * 1e3:9.1f} us "
             f"({o['atomic_adds'] / (o['atomic_ms'] * 1e-3) / 1e9:.0f} G adds/s) | library backward (all "
-            f"gradients) {o['backward_ms'] * 1e3:8.1f} us")
+            f"gradients) {o['backward_ms'] * 1e3:8.1f} us | LDS ds_add_f32 {o['lds_adds_per_s'] / 1e9:.0f} G adds/s "
+            f"(consecutive {o['lds_ms'][0]:.2f} ms, random {o['lds_ms'][1]:.2f} ms for {256 * 8 * 256 * 4096:d} adds): "
+            f"the same adds pre-combined in LDS take at least {o['lds_bound_ms'] * 1e3:.0f} us")
         if args.atomic_baseline:
             return
     if args.kernels_only:

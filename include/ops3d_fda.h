@@ -225,19 +225,6 @@ OPS3D_FDA_API int ops3d_fda_backward_noalloc(const void *value, const int64_t *s
 OPS3D_FDA_API int ops3d_fda_profile_enable(int on);
 OPS3D_FDA_API int ops3d_fda_profile_read(int which, float *ms, int n);
 
-/*
- * Measurement baseline (not a replacement of any reference entry point, and not used by the
- * op): grad_value computed by the reference's own scheme, one fp32 atomic add per sample, corner
- * and channel (csrc/cuda/flash_deform_col2im_cuda.cuh:347-412 with common.h:141-262, i.e. the
- * scatter inside the reference's flash_deform_attn_backward, csrc/vision.cpp:24), into the fp32
- * buffer grad_value_f32 [B, S, G, D], which the call clears first.  It exists to time that scheme
- * on gfx950 against the tile-gather backward (bench.py --atomic-baseline).
- */
-OPS3D_FDA_API int ops3d_fda_scatter_baseline(const int64_t *spatial_shapes, const int64_t *level_start_index,
-                       const void *sampling_loc_attn, const void *grad_output, float *grad_value_f32,
-                       int dtype, int batch, int spatial_size, int num_heads, int channels,
-                       int num_levels, int num_query, int num_point, void *stream);
-
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,47 @@
+/*
+ * ops3d_fda_bench.h -- C ABI of libops3d_fda_bench.so: measurement baselines for the backward's
+ * value gradient on gfx950.  Not part of the op: nothing in libops3d_fda.so calls these, and
+ * they replace no reference entry point.  Return codes: 0 ok, 1 bad argument, 2 HIP failure
+ * (message: ops3d_fda_bench_last_error()).  Pointers are device memory; `stream` a hipStream_t.
+ */
+#ifndef OPS3D_FDA_BENCH_H
+#define OPS3D_FDA_BENCH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OPS3D_FDA_BENCH_API __attribute__((visibility("default")))
+
+OPS3D_FDA_BENCH_API const char *ops3d_fda_bench_last_error(void);
+
+/*
+ * grad_value [B, S, G, D] in fp32 by the reference's own scheme and lane layout: one fp32 atomic
+ * add per sample, corner inside the volume and channel, one lane per channel, so one wave
+ * instruction adds a corner's contiguous row of D floats for 64 / D (b, q, g) units
+ * (csrc/cuda/flash_deform_col2im_cuda.cuh:248-429 with csrc/cuda/common.h:141-262 at the
+ * d_stride 1 of ops3d/flash_deform_attn.py:44-62).  The buffer is cleared first.  Layouts and
+ * dtype codes (0 fp32, 1 fp16, 2 bf16) as in ops3d_fda.h; D in {8, 16, 32, 64}.
+ */
+OPS3D_FDA_BENCH_API int ops3d_fda_bench_ref_scatter(const int64_t *spatial_shapes, const int64_t *level_start_index,
+                                                    const void *sampling_loc_attn, const void *grad_output,
+                                                    float *grad_value_f32, int dtype, int batch, int spatial_size,
+                                                    int num_heads, int channels, int num_levels, int num_query,
+                                                    int num_point, void *stream);
+
+/*
+ * LDS float-atomic throughput probe: `blocks` blocks of 256 threads, each thread `iters`
+ * ds_add_f32 (no return) of 1.0 into a 4096-float LDS array (pattern 0: consecutive addresses per
+ * wave; 1: pseudo-random); out[block] receives the block's sum (256 * iters).  The rate bounds
+ * any scheme that pre-combines value-gradient terms with LDS atomics.
+ */
+OPS3D_FDA_BENCH_API int ops3d_fda_bench_lds_atomic(float *out, int blocks, int iters, int pattern, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OPS3D_FDA_BENCH_H */

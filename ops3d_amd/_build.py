@@ -19,6 +19,9 @@ LIB_NAME = "libops3d_fda.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 TORCH_EXT_NAME = "_fda_torch"
 SOURCES = ["fda_capi.hip", "fda_tiles.hip", "fda_f32.hip", "fda_f16.hip", "fda_bf16.hip", "nms3d.hip", "roi_align3d.hip"]
+# measurement baselines (not part of the op): a library of their own
+BENCH_SOURCE = "bench_scatter.hip"
+BENCH_LIB_PATH = os.path.join(PKG_DIR, "libops3d_fda_bench.so")
 ARCH = "gfx950"
 
 # -packed-fp32-ops off: hipcc must not form v_pk_{add,mul,fma}_f32 on its own.
@@ -85,7 +88,8 @@ def _torch_ext_cmds(build_dir: str) -> tuple[list[str], list[str], str]:
 
 def build(out_path: str = LIB_PATH, build_dir: str | None = None) -> str:
     """Compile every source for gfx950 and link ``libops3d_fda.so``, then the PyTorch
-    extension module over it; return the library's path."""
+    extension module over it and the measurement library ``libops3d_fda_bench.so``; return the
+    library's path."""
     hipcc = _hipcc()
     build_dir = build_dir or os.path.join(PKG_DIR, "_build")
     os.makedirs(build_dir, exist_ok=True)
@@ -97,14 +101,18 @@ def build(out_path: str = LIB_PATH, build_dir: str | None = None) -> str:
         cmds.append([hipcc, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
     ext_cc, ext_link, ext_out = _torch_ext_cmds(build_dir)
     cmds.append(ext_cc)
+    main = out_path == LIB_PATH
+    if main:
+        cmds.append([hipcc, *HIP_FLAGS, "-shared", os.path.join(CSRC, BENCH_SOURCE), "-o", BENCH_LIB_PATH + ".tmp"])
     with ThreadPoolExecutor(max_workers=min(len(cmds), os.cpu_count() or 1)) as ex:
         list(ex.map(_run, cmds))
     tmp = out_path + ".tmp"
     _run([hipcc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp])
     os.replace(tmp, out_path)
-    if out_path == LIB_PATH:
+    if main:
         _run(ext_link)
         os.replace(ext_out + ".tmp", ext_out)
+        os.replace(BENCH_LIB_PATH + ".tmp", BENCH_LIB_PATH)
     return out_path
 
 

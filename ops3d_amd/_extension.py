@@ -50,7 +50,6 @@ EXPORTED_SYMBOLS = (
     "ops3d_roi_align3d_backward",
     "ops3d_fda_profile_enable",
     "ops3d_fda_profile_read",
-    "ops3d_fda_scatter_baseline",
 )
 
 
@@ -99,8 +98,6 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ops3d_roi_align3d_backward.restype = _i
     lib.ops3d_roi_align3d_backward.argtypes = [_vp] * 4 + [_sz] + [_i] * 10 + [ctypes.c_float, _i, _i, _vp]
     lib.ops3d_fda_backward_offsets.argtypes = [_vp] * 6 + [_i] + [_vp] * 5 + [_sz] + [_i] * 9 + [_vp]
-    lib.ops3d_fda_scatter_baseline.restype = _i
-    lib.ops3d_fda_scatter_baseline.argtypes = [_vp] * 5 + [_i] * 8 + [_vp]
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -110,7 +107,7 @@ def _ptr(t: torch.Tensor | None) -> int | None:
 class _NativeFDA:
     """Host side of the flash-deform-attn extension, bound to libops3d_fda.so."""
 
-    ABI_VERSION = 5
+    ABI_VERSION = 6
 
     def __init__(self, lib: ctypes.CDLL, path: str, ext=None):
         self._lib = lib
@@ -284,24 +281,6 @@ class _NativeFDA:
         if rc != OPS3D_FDA_OK:
             self._raise(rc, "flash_deform_attn_backward_accumulate failed")
         return grad_sla
-
-    def scatter_baseline(self, value, spatial_shapes, level_start_index, sampling_loc_attn, grad_output, K):
-        """grad_value (fp32, [B,S,G,D]) by the reference's scheme, one fp32 atomic add per sample,
-        corner and channel: a measurement baseline for the tile-gather backward, not the op's
-        path (ops3d_fda_scatter_baseline)."""
-        B, S, G, D, L, Q = self._common(
-            value, spatial_shapes, level_start_index, sampling_loc_attn, K, {"grad_output": grad_output}
-        )
-        grad_value = torch.empty(value.shape, dtype=torch.float32, device=value.device)
-        stream = torch.cuda.current_stream(value.device).cuda_stream
-        with torch.cuda.device(value.device):
-            rc = self._lib.ops3d_fda_scatter_baseline(
-                _ptr(spatial_shapes), _ptr(level_start_index), _ptr(sampling_loc_attn), _ptr(grad_output),
-                _ptr(grad_value), _DTYPE_CODE[value.dtype], B, S, G, D, L, Q, int(K), stream,
-            )
-        if rc != OPS3D_FDA_OK:
-            self._raise(rc, "scatter_baseline failed")
-        return grad_value
 
     def _ref_levels(self, reference_points, value, B, Q, L):
         self._check_inputs({"reference_points": reference_points}, value)

@@ -367,11 +367,6 @@ __global__ __launch_bounds__(256) void head_major_kernel(const uint32_t *src, ui
 }
 
 // Zero `n` 32-bit words (a kernel, not hipMemsetAsync, so the call is capture-safe).
-__global__ __launch_bounds__(256) void fill_words_kernel(uint32_t *p, int64_t n) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
-    p[i] = 0u;
-}
-
 hipError_t launch_head_major(const void *src, void *dst, int64_t B, int64_t N, int G, int D, int esize,
                              const int64_t *shapes, const int64_t *lsi, int L, hipStream_t st) {
   const int R = D * esize / 4;
@@ -425,7 +420,7 @@ void *scratch_address() {
 
 extern "C" {
 
-int ops3d_fda_abi_version(void) { return 5; }
+int ops3d_fda_abi_version(void) { return 6; }
 
 const char *ops3d_fda_last_error(void) { return g_last_error.c_str(); }
 
@@ -647,43 +642,6 @@ static int backward_impl(const void *value, const void *value_head_major, const 
   }
   prof_mark(5, st);
   if (g_prof_on) g_prof_recorded[0] = true;
-  return OPS3D_FDA_OK;
-}
-
-int ops3d_fda_scatter_baseline(const int64_t *spatial_shapes, const int64_t *level_start_index,
-                               const void *sampling_loc_attn, const void *grad_output, float *grad_value_f32,
-                               int dtype, int batch, int spatial_size, int num_heads, int channels,
-                               int num_levels, int num_query, int num_point, void *stream) {
-  g_last_error.clear();
-  Geometry geo;
-  int rc = common_checks(dtype, batch, spatial_size, num_heads, channels, num_levels, num_query, num_point, 1,
-                         false, geo);
-  if (rc) return rc;
-  const int64_t nval = (int64_t)batch * spatial_size * num_heads * channels;
-  if (nval > 0 && !grad_value_f32) return fail(OPS3D_FDA_EINVAL, "grad_value_f32 is NULL");
-  if ((int64_t)batch * num_query > 0 && (!sampling_loc_attn || !grad_output || !spatial_shapes || !level_start_index))
-    return fail(OPS3D_FDA_EINVAL, "NULL pointer argument");
-  if (misaligned(sampling_loc_attn) || misaligned(grad_output) || misaligned(grad_value_f32))
-    return fail(OPS3D_FDA_EINVAL, "tensor data pointers must be 4-byte aligned");
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (nval > 0) {
-    const int64_t words = nval;
-    const unsigned blocks = (unsigned)((words + 255) / 256 < 16384 ? (words + 255) / 256 : 16384);
-    hipLaunchKernelGGL(fill_words_kernel, dim3(blocks), dim3(256), 0, st, reinterpret_cast<uint32_t *>(grad_value_f32),
-                       words);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return fail(OPS3D_FDA_ERUNTIME, "clear failed: %s", hipGetErrorString(e));
-  }
-  if ((int64_t)batch * num_query == 0 || nval == 0) return OPS3D_FDA_OK;
-  geo.a.shapes = spatial_shapes;
-  geo.a.lsi = level_start_index;
-  geo.a.loc_attn = sampling_loc_attn;
-  geo.a.grad_out = grad_output;
-  geo.a.grad_value = grad_value_f32;
-  hipError_t e = launch(dtype, 5, geo, st);
-  if (e != hipSuccess)
-    return fail(OPS3D_FDA_ERUNTIME, "scatter baseline launch failed: %s (grid=%u, lds=%zu)", hipGetErrorString(e),
-                geo.grid, geo.lds);
   return OPS3D_FDA_OK;
 }
 

@@ -1106,60 +1106,6 @@ void fda_bwd_tile_kernel(const Args a) {
   }
 }
 
-// Measurement baseline, not on the op's path: grad_value by the reference's scatter
-// (col2im.cuh:347-412 calling ms_deform_attn_col2im_trilinear, common.h:141-262): for every
-// sample and corner inside the volume, attn * w_corner * grad_out[c] is added to grad_value with
-// an fp32 atomic per channel.  Here the atomics are raw buffer atomics whose out-of-volume
-// corners get an out-of-range offset (the hardware drops them).  Same units and lanes as the
-// forward: a unit's lanes split its channels (LPU chunks) and, for 64-byte rows, its corners
-// (x0 row / x0+1 row).  grad_value is fp32 [B,S,G,D], zeroed by the caller.
-template <typename T, int CPL, int LPU>
-__global__ __launch_bounds__(kBlock) void fda_scatter_baseline_kernel(const Args a) {
-  extern __shared__ float lds[];
-  constexpr int UL = fwd_pairs(CPL, LPU, (int)sizeof(T)) ? 2 * LPU : LPU;
-  constexpr int NS = UL / LPU;   // corner subsets per unit
-  constexpr int UPW = kWave / UL, UPB = kWavesPerBlock * UPW;
-  int b, g, qb;
-  if (!map_tile(a, blockIdx.x, b, g, qb)) return;
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  const int ju = lane & (UL - 1), j = ju % LPU, sub = ju / LPU;
-  const int ub = wave * UPW + lane / UL;
-  const int q = qb * UPB + ub;
-  const bool live = q < a.Q;
-  const int L = a.L, K = a.K, LK = L * K, P = a.P;
-  float *rec = lds + ub * (P + 1);
-  const int64_t unit = ((int64_t)b * a.Q + (live ? q : 0)) * a.G + g;
-  stage_record<T, UL>(static_cast<const T *>(a.loc_attn) + record_offset<kModePlain>(a, unit), P, ju, live, rec);
-  wave_lds_sync();
-  unit_softmax<UL>(rec + 3 * LK, LK, ju);
-  wave_lds_sync();
-  if (!live) return;
-  float tg[CPL];
-  load_global_elems<T, CPL>(static_cast<const T *>(a.grad_out) + unit * a.D + j * CPL, tg);
-  const int GD = a.G * a.D;
-  const __amdgpu_buffer_rsrc_t rg =
-      make_rsrc(a.grad_value + (int64_t)b * a.S * GD, (uint32_t)((int64_t)a.S * GD * 4));
-  for (int l = 0; l < L; ++l) {
-    const int Dl = (int)a.shapes[3 * l], Hl = (int)a.shapes[3 * l + 1], Wl = (int)a.shapes[3 * l + 2];
-    const uint32_t lbase = (uint32_t)(a.lsi[l] * GD) + (uint32_t)(g * a.D + j * CPL);
-    for (int k = 0; k < K; ++k) {
-      const int s = l * K + k;
-      Sample ms;
-      sample_setup(rec[3 * s], rec[3 * s + 1], rec[3 * s + 2], Wl, Hl, Dl, GD, ms);
-      const float at = rec[3 * LK + s];
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        if (c % NS != sub) continue;
-        const float w = at * ((ms.wx[c & 1] * ms.wy[(c >> 1) & 1]) * ms.wz[c >> 2]);
-        const uint32_t off = ms.off[c] == OOB_ELEM ? 0x80000000u : (ms.off[c] + lbase) * 4u;
-#pragma unroll
-        for (int e = 0; e < CPL; ++e)
-          __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(w * tg[e], rg, off + 4u * (uint32_t)e, 0, 0);
-      }
-    }
-  }
-}
-
 // Split tiles (see the tile kernel): one block per tile of every group adds the F parts'
 // partial sums of each of its voxels and writes the rows (in T, or added to the caller's fp32
 // buffer).  Runs after the tile kernel, so plain loads see the parts; exits when F == 1.
@@ -1260,16 +1206,13 @@ void launch_query_major(int which, const Args &a, unsigned grid, size_t lds, hip
 }
 
 // which: 0 forward, 1 backward phase 1 (query-major), 2 backward phase 3 (tile-major),
-// 3 split-tile combine, 5 the atomic-scatter measurement baseline
+// 3 split-tile combine
 template <typename T, int CPL, int LPU>
 hipError_t launch_one(int which, const Args &a, unsigned grid, size_t lds, hipStream_t st) {
   if (which == 0 || which == 1) {
     if (a.dcn) launch_query_major<T, CPL, LPU, kModeDcn>(which, a, grid, lds, st);
     else if (a.ref) launch_query_major<T, CPL, LPU, kModeOffsets>(which, a, grid, lds, st);
     else launch_query_major<T, CPL, LPU, kModePlain>(which, a, grid, lds, st);
-  }
-  else if (which == 5) {
-    hipLaunchKernelGGL((fda_scatter_baseline_kernel<T, CPL, LPU>), dim3(grid), dim3(kBlock), lds, st, a);
   }
   else if (which == 3) {
     // one block per tile of every group (`grid` = the bound on tiles times the groups)

@@ -505,7 +505,7 @@ __global__ __launch_bounds__(256) void roi_align3d_backward_gather_kernel(const 
   const int t0[3] = {tzi * kGTZ, tyi * kGTY, txi * kGTX};
   const int c0 = cc * kGCC;
   const int zl = tid / (kGTY * kGTX), yl = (tid / kGTX) % kGTY, xl = tid % kGTX;
-  const int P[3] = {PD, PH, PW}, S[3] = {D, H, W}, TT[3] = {kGTZ, kGTY, kGTX};
+  const int S[3] = {D, H, W}, TT[3] = {kGTZ, kGTY, kGTX};
   const int pos0[3] = {0, kGTZ, kGTZ + kGTY};     // first position of each axis in the ranges
   const int E = kGTZ * PD + kGTY * PH + kGTX * PW;   // entries of a roi's full table
   const int64_t pvol = (int64_t)PD * PH * PW;

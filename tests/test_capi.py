@@ -1,4 +1,4 @@
-"""The C ABI library loads, exports every function include/ops3d_fda.h declares, and rejects
+"""The C ABI library loads, exports every function include/*.h declares, and rejects
 bad arguments before touching the GPU (no compute calls here)."""
 from __future__ import annotations
 
@@ -37,8 +37,22 @@ def test_library_exports_every_declared_symbol(lib):
         assert hasattr(lib, name), name
 
 
+def test_bench_library_exports_every_declared_symbol():
+    """libops3d_fda_bench.so (measurement baselines, include/ops3d_fda_bench.h)."""
+    from ops3d_amd import _bench_lib
+
+    if not os.path.exists(_bench_lib.LIB_PATH):
+        pytest.skip("libops3d_fda_bench.so not built")
+    text = open(os.path.join(ROOT, "include", "ops3d_fda_bench.h")).read()
+    names = sorted(set(re.findall(r"OPS3D_FDA_BENCH_API\s+[\w\s\*]*?\b(ops3d_\w+)\s*\(", text)))
+    assert len(names) == 3
+    blib = _bench_lib.load()
+    for name in names:
+        assert hasattr(blib, name), name
+
+
 def test_abi_version_and_support_table(lib):
-    assert lib.ops3d_fda_abi_version() == 5
+    assert lib.ops3d_fda_abi_version() == 6
     F32, F16, BF16 = 0, 1, 2
     for d in (8, 16, 24, 32, 48, 64, 96, 128, 192, 256):
         assert lib.ops3d_fda_supported(BF16, d) == 1, d
@@ -162,9 +176,13 @@ def test_offsets_argument_errors_before_device_work(lib):
     assert rc == 0
 
 
-def test_scatter_baseline_argument_errors_before_device_work(lib):
-    """The atomic-scatter measurement baseline validates like the other entry points."""
-    f = lib.ops3d_fda_scatter_baseline
+def test_bench_library_argument_errors_before_device_work():
+    """The measurement library (libops3d_fda_bench.so, not part of the op) validates before any
+    device work, and the op's library no longer exports the baseline."""
+    from ops3d_amd import _bench_lib, _extension
+
+    blib = _bench_lib.load()
+    f = blib.ops3d_fda_bench_ref_scatter
     args = dict(dtype=2, B=1, S=576, G=8, D=32, L=2, Q=576, K=4)
 
     def call(**kw):
@@ -172,7 +190,9 @@ def test_scatter_baseline_argument_errors_before_device_work(lib):
         return f(None, None, None, None, None, a["dtype"], a["B"], a["S"], a["G"], a["D"], a["L"], a["Q"],
                  a["K"], None)
 
-    assert call(D=20) == 1 and b"unsupported channels" in lib.ops3d_fda_last_error()
+    assert call(D=20) == 1 and b"unsupported channels" in blib.ops3d_fda_bench_last_error()
     assert call(L=6) == 1
     assert call(dtype=7) == 1
-    assert call() == 1 and b"NULL" in lib.ops3d_fda_last_error()
+    assert call() == 1 and b"NULL" in blib.ops3d_fda_bench_last_error()
+    assert blib.ops3d_fda_bench_lds_atomic(None, 1, 1, 0, None) == 1
+    assert not hasattr(_extension.load_library(), "ops3d_fda_scatter_baseline")

@@ -337,16 +337,17 @@ def test_backward_accumulate_f32(gpu_device, dt):
 
 
 @pytest.mark.parametrize("dt,G,D,lo,hi", [(torch.bfloat16, 8, 32, 0.0, 1.0), (torch.float32, 8, 32, -0.1, 1.1),
-                                          (torch.float32, 3, 16, -0.1, 1.1), (torch.float16, 2, 48, 0.0, 1.0)])
+                                          (torch.float32, 3, 16, -0.1, 1.1), (torch.float16, 2, 64, 0.0, 1.0)])
 def test_scatter_baseline(gpu_device, dt, G, D, lo, hi):
-    """The measurement baseline (the reference's fp32 atomic scatter of grad_value) computes the
-    same value gradient as the oracle, to fp32 rounding of its sums."""
-    from ops3d_amd import _C
+    """The measurement baseline (the reference's fp32 atomic scatter of grad_value at its own lane
+    layout, libops3d_fda_bench.so) computes the same value gradient as the oracle, to fp32
+    rounding of its sums."""
+    from ops3d_amd import _bench_lib
 
     inp = random_inputs([(6, 5, 8), (3, 3, 4)], 2, 150, G, D, 4, dt, seed=5, lo=lo, hi=hi)
     st, lsi = level_meta(inp["shapes"], gpu_device)
-    gv = _C.scatter_baseline(inp["value"].to(gpu_device), st, lsi, inp["sampling_loc_attn"].to(gpu_device),
-                             inp["grad_output"].to(gpu_device), 4)
+    gv = _bench_lib.ref_scatter(inp["value"].to(gpu_device), st, lsi, inp["sampling_loc_attn"].to(gpu_device),
+                                inp["grad_output"].to(gpu_device), 4)
     torch.cuda.synchronize()
     _, rgv, _ = run_oracle(inp)
     assert gv.dtype == torch.float32
