@@ -314,6 +314,22 @@ __global__ __launch_bounds__(256) void head_major_kernel(const uint32_t *src, ui
   const int Rc = vec ? R / 4 : R;                  // chunks per row
   const int64_t total = B * N * G * Rc;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  if (!pair_levels && total < ((int64_t)1 << 31)) {
+    // no level is paired: heads N rows apart; 32-bit index arithmetic (64-bit divisions made
+    // the copy VALU-bound)
+    const uint32_t rc = (uint32_t)Rc, gg = (uint32_t)G, nn = (uint32_t)N;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < (uint32_t)total; i += (uint32_t)stride) {
+      const uint32_t row = i / rc, c = i - row * rc;   // (b, n, g), chunk
+      const uint32_t bn = row / gg, g = row - bn * gg;
+      const uint32_t b = bn / nn, n = bn - b * nn;
+      const uint32_t o = ((b * gg + g) * nn + n) * rc + c;
+      if (vec)
+        reinterpret_cast<u32x4 *>(dst)[o] = reinterpret_cast<const u32x4 *>(src)[i];
+      else
+        dst[o] = src[i];
+    }
+    return;
+  }
   if (!pair_levels) {   // no level is paired: heads N rows apart
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
       const int64_t c = i % Rc;
@@ -339,6 +355,34 @@ __global__ __launch_bounds__(256) void head_major_kernel(const uint32_t *src, ui
   }
   __syncthreads();
   const int64_t HS = head_rows;
+  if (total < ((int64_t)1 << 31) && (B * G * HS + 2) * Rc < ((int64_t)1 << 31)) {
+    // the same in 32-bit index arithmetic
+    const uint32_t rc = (uint32_t)Rc, gg = (uint32_t)G, nn = (uint32_t)N, hs = (uint32_t)HS;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < (uint32_t)total; i += (uint32_t)stride) {
+      const uint32_t row = i / rc, c = i - row * rc;   // (b, n, g), chunk
+      const uint32_t bn = row / gg, g = row - bn * gg;
+      const uint32_t b = bn / nn, n = bn - b * nn;
+      const uint32_t si = i;
+      const uint32_t head = (b * gg + g) * hs;
+      int l = L - 1;
+      while (l > 0 && (int64_t)n < lv_src[l]) --l;
+      const uint32_t v = n - (uint32_t)lv_src[l];
+      uint32_t r0 = (uint32_t)lv_dst[l] + v;
+      const bool two = lv_pair[l];
+      const uint32_t r1 = (uint32_t)lv_dst[l] + 2 * v + 1;
+      if (two) r0 = (uint32_t)lv_dst[l] + 2 * v + 2;
+      if (vec) {
+        const u32x4 x = reinterpret_cast<const u32x4 *>(src)[si];
+        reinterpret_cast<u32x4 *>(dst)[(head + r0) * rc + c] = x;
+        if (two) reinterpret_cast<u32x4 *>(dst)[(head + r1) * rc + c] = x;
+      } else {
+        const uint32_t x = src[si];
+        dst[(head + r0) * rc + c] = x;
+        if (two) dst[(head + r1) * rc + c] = x;
+      }
+    }
+    return;
+  }
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
     const int64_t c = i % Rc;
     const int64_t row = i / Rc;                      // (b, n, g)
