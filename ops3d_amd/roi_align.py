@@ -1,5 +1,10 @@
 """3-D RoI Align (reference ops3d/roi_align_nd.py:26-117; kernels in csrc/roi_align3d.hip).
 
+The Function / module interface (names, arguments, the order-0 sampling rule and two error
+messages) follows the reference's ops3d/roi_align_nd.py, which comes from MedVision
+(https://github.com/TimothyZero/MedVision, medvision/ops/roi_align_nd.py) under the Apache
+License 2.0; the bodies here are this package's own.
+
 Same API: ``RoIAlign3DFunction`` / ``roi_align_3d(features, rois, output_size, spatial_scale,
 sampling_ratio=0, order=1)`` and the ``RoIAlign`` module.  features [N, C, D, H, W]; rois
 [R, 7] (batch index, x1, y1, z1, x2, y2, z2); output [R, C, d, h, w].  Gradients flow to the
