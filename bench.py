@@ -298,8 +298,15 @@ def measure_roi_align(steps, warmup, device, dtype="bf16"):
     b = Bench.__new__(Bench)
     b.torch = torch
     out_bytes = R * C * 343 * x.element_size()
+    # the same forward on features already in channels_last_3d memory (no transposed copy)
+    xcl = x.detach().contiguous(memory_format=torch.channels_last_3d)
+
+    def fwd_cl():
+        with torch.no_grad():
+            roi_align_3d(xcl, rois, pooled, 1.0, 2, 1)
+
     return {"fwd": b.time_loop(fwd, steps, warmup), "step": b.time_loop(step, steps, warmup),
-            "samples": R * C * 343 * 8, "out_bytes": out_bytes}
+            "fwd_cl": b.time_loop(fwd_cl, steps, warmup), "samples": R * C * 343 * 8, "out_bytes": out_bytes}
 
 
 def measure_dcnv4(steps, warmup, device, dtype="bf16"):
@@ -565,7 +572,8 @@ def main():
         o = measure_roi_align(args.steps, args.warmup, dev)
         f, st = o["fwd"]["mean"], o["step"]["mean"]
         log(f" roi_align3d bf16 [2,256,32,64,64] x 512 rois, 7^3 bins, 8 samples | fwd {f * 1e3:8.1f} us "
-            f"({o['samples'] / f / 1e6:.3g} G samples/s) | fwd+bwd {st * 1e3:8.1f} us")
+            f"({o['samples'] / f / 1e6:.3g} G samples/s) | fwd+bwd {st * 1e3:8.1f} us | fwd on channels_last_3d "
+            f"features {o['fwd_cl']['mean'] * 1e3:8.1f} us")
         if args.roi:
             return
     if args.nms or args.all:

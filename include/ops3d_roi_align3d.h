@@ -28,6 +28,23 @@ OPS3D_FDA_API int ops3d_roi_align3d_forward(const void *features, const void *ro
                                             int C, int D, int H, int W, int R, int PD, int PH, int PW,
                                             float spatial_scale, int sampling_ratio, int order, void *stream);
 
+/*
+ * Channels-last forward (no counterpart in the reference, whose kernel reads [N,C,D,H,W]; same
+ * results as ops3d_roi_align3d_forward, bit for bit).  features_cl is [N,D,H,W,C] (PyTorch's
+ * channels_last_3d layout of an [N,C,D,H,W] tensor), 16-byte aligned; output [R,C,PD,PH,PW] as
+ * above.  A voxel's channels are one contiguous row there, so each corner of a sample is one
+ * 16-byte load of 8 channels.  Supported when C % 8 == 0, C <= 2048 and D*H*W*C < 2^32
+ * (ops3d_roi_align3d_channels_last_supported: 1 or 0); otherwise it returns OPS3D_FDA_EINVAL.
+ */
+OPS3D_FDA_API int ops3d_roi_align3d_channels_last_supported(int dtype, int C, int D, int H, int W, int PW);
+OPS3D_FDA_API int ops3d_roi_align3d_forward_channels_last(const void *features_cl, const void *rois, void *output,
+                                                          int dtype, int N, int C, int D, int H, int W, int R, int PD,
+                                                          int PH, int PW, float spatial_scale, int sampling_ratio,
+                                                          int order, void *stream);
+/* features [N,C,D,H,W] -> features_cl [N,D,H,W,C] (N <= 65535), for the forward above. */
+OPS3D_FDA_API int ops3d_roi_align3d_to_channels_last(const void *features, void *features_cl, int dtype, int N, int C,
+                                                     int D, int H, int W, void *stream);
+
 /* Bytes of fp32 workspace ops3d_roi_align3d_backward needs for output bins PD x PH x PW: 0 when
  * PD, PH, PW <= 64 and PD*PH*PW <= 384 (the backward is then a gather straight into grad_input),
  * else N*C*D*H*W*4 (the gradient is accumulated channels-last in fp32 by atomics, then

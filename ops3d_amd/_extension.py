@@ -23,6 +23,9 @@ _PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG_DIR, "libops3d_fda.so")
 
 OPS3D_FDA_OK, OPS3D_FDA_EINVAL, OPS3D_FDA_ERUNTIME = 0, 1, 2
+# RoI Align forward: below this many output elements the NCDHW kernel is as fast as the
+# transposed copy of the features plus the channels-last kernel
+ROI_CL_MIN_OUTPUTS = 1 << 19
 _DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
 _vp, _i, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
@@ -48,6 +51,9 @@ EXPORTED_SYMBOLS = (
     "ops3d_roi_align3d_forward",
     "ops3d_roi_align3d_backward_workspace_bytes",
     "ops3d_roi_align3d_backward",
+    "ops3d_roi_align3d_channels_last_supported",
+    "ops3d_roi_align3d_forward_channels_last",
+    "ops3d_roi_align3d_to_channels_last",
     "ops3d_fda_profile_enable",
     "ops3d_fda_profile_read",
 )
@@ -97,6 +103,12 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ops3d_roi_align3d_backward_workspace_bytes.argtypes = [_i] * 9
     lib.ops3d_roi_align3d_backward.restype = _i
     lib.ops3d_roi_align3d_backward.argtypes = [_vp] * 4 + [_sz] + [_i] * 10 + [ctypes.c_float, _i, _i, _vp]
+    lib.ops3d_roi_align3d_channels_last_supported.restype = _i
+    lib.ops3d_roi_align3d_channels_last_supported.argtypes = [_i] * 6
+    lib.ops3d_roi_align3d_forward_channels_last.restype = _i
+    lib.ops3d_roi_align3d_forward_channels_last.argtypes = [_vp] * 3 + [_i] * 10 + [ctypes.c_float, _i, _i, _vp]
+    lib.ops3d_roi_align3d_to_channels_last.restype = _i
+    lib.ops3d_roi_align3d_to_channels_last.argtypes = [_vp] * 2 + [_i] * 6 + [_vp]
     lib.ops3d_fda_backward_offsets.argtypes = [_vp] * 6 + [_i] + [_vp] * 5 + [_sz] + [_i] * 9 + [_vp]
 
 
@@ -420,14 +432,32 @@ class _NativeFDA:
         """RoI Align 3-D forward into `output` [R, C, out_d, out_h, out_w] (reference
         csrc/roi_align_3d.h:97-115)."""
         code = self._roi_checks(features, rois, output)
-        f, r = features.contiguous(), rois.contiguous()
-        N, C, D, H, W = f.shape
-        if tuple(output.shape) != (r.shape[0], C, out_d, out_h, out_w):
+        r = rois.contiguous()
+        N, C, D, H, W = features.shape
+        R = r.shape[0]
+        if tuple(output.shape) != (R, C, out_d, out_h, out_w):
             raise ValueError("output must be [R, C, out_d, out_h, out_w]")
-        with torch.cuda.device(f.device):
-            rc = self._lib.ops3d_roi_align3d_forward(
-                _ptr(f), _ptr(r), _ptr(output), code, N, C, D, H, W, r.shape[0], out_d, out_h, out_w,
-                float(spatial_scale), int(sampling_ratio), int(order), torch.cuda.current_stream(f.device).cuda_stream)
+        cl_in = (not features.is_contiguous() and features.is_contiguous(memory_format=torch.channels_last_3d)
+                 and features.data_ptr() % 16 == 0)
+        use_cl = (N <= 65535 and self._lib.ops3d_roi_align3d_channels_last_supported(code, C, D, H, W, out_w)
+                  and (cl_in or R * C * out_d * out_h * out_w >= ROI_CL_MIN_OUTPUTS))
+        with torch.cuda.device(features.device):
+            st = torch.cuda.current_stream(features.device).cuda_stream
+            args = (code, N, C, D, H, W, R, out_d, out_h, out_w, float(spatial_scale), int(sampling_ratio),
+                    int(order), st)
+            if use_cl:
+                # the channels-last kernel, on the caller's channels_last_3d memory or a transposed copy
+                fc = features
+                if not cl_in:
+                    f = features.contiguous()
+                    fc = torch.empty((N, D, H, W, C), dtype=f.dtype, device=f.device)
+                    rc = self._lib.ops3d_roi_align3d_to_channels_last(_ptr(f), _ptr(fc), code, N, C, D, H, W, st)
+                    if rc != OPS3D_FDA_OK:
+                        raise RuntimeError("roi_align_3d_forward: channels-last copy failed")
+                rc = self._lib.ops3d_roi_align3d_forward_channels_last(_ptr(fc), _ptr(r), _ptr(output), *args)
+            else:
+                f = features.contiguous()
+                rc = self._lib.ops3d_roi_align3d_forward(_ptr(f), _ptr(r), _ptr(output), *args)
         if rc == OPS3D_FDA_EINVAL:
             raise ValueError("roi_align_3d_forward: invalid sizes or order")
         if rc != OPS3D_FDA_OK:

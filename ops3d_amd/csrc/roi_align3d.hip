@@ -672,6 +672,156 @@ __global__ __launch_bounds__(256) void roi_align3d_backward_gather_kernel(const 
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Channels-last forward.  With features [N, D, H, W, C] a voxel's C channels are one contiguous
+// row, so a sample's corner is one 16-byte (8-channel) load per lane and the 32 lanes of a
+// 256-channel bin read whole 128-byte lines; from [N, C, D, H, W] every corner of every channel
+// is a separate 2- or 4-byte access.  A block owns bpb consecutive bins of the (ph, pw) plane
+// of one (roi, pd): lane group cg takes channels 8 cg .. 8 cg + 7 of one bin, the rounded
+// results are staged in LDS and written out as [R, C, PD, PH, PW] runs of bpb elements per
+// channel.  The blocks of a roi run on one XCD, whose L2 then serves the overlap of their taps.
+// The arithmetic is the NCDHW kernel's, term by term, so both give the same bits.
+constexpr int kClChannels = 8;                  // channels per lane
+
+template <typename T>
+__device__ __forceinline__ void load8(const T *p, float f[8]) {
+  if constexpr (sizeof(T) == 4) {
+    const float4 a = reinterpret_cast<const float4 *>(p)[0], b = reinterpret_cast<const float4 *>(p)[1];
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+    f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+  } else {
+    const uint4 u = *reinterpret_cast<const uint4 *>(p);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const unsigned short s = (unsigned short)((k & 1) ? (w[k >> 1] >> 16) : (w[k >> 1] & 0xffffu));
+      f[k] = to_f(__builtin_bit_cast(T, s));
+    }
+  }
+}
+
+// Bins per block: one per lane group (256 / (C / 8) groups), the (ph, pw) plane of a (roi, pd)
+// cut into equal parts.  One bin per thread measured fastest (more blocks in flight; bench
+// workload, rows of 7 bins: 1, 2, 7 rows per block 415, 453, 448 us).
+inline void cl_split(int C, int PHW, int &bpb, int &parts) {
+  const int slots = 256 / (C / kClChannels);
+  parts = (PHW + slots - 1) / slots;
+  bpb = (PHW + parts - 1) / parts;
+}
+
+inline bool cl_supported(int C) { return C > 0 && C % kClChannels == 0 && C / kClChannels <= 256; }
+
+template <typename T>
+__global__ __launch_bounds__(256) void roi_align3d_forward_cl_kernel(const T *feat, const T *rois, T *out, int N, int C,
+                                                                     int D, int H, int W, int PD, int PH, int PW,
+                                                                     float scale, int sr, int order, int bpb, int parts,
+                                                                     int nblk) {
+#pragma clang fp contract(off)
+  extern __shared__ __align__(16) unsigned char cl_lds[];
+  T *res = reinterpret_cast<T *>(cl_lds);   // [C][bpb]
+  // block i runs on XCD i % 8: XCD x takes the x-th eighth of the (roi, pd, row) blocks, so a
+  // roi's blocks share one L2 (gridDim.x is a multiple of 8; nblk blocks are real)
+  const unsigned blk = (blockIdx.x & 7u) * (gridDim.x / 8u) + (blockIdx.x >> 3);
+  if (blk >= (unsigned)nblk) return;
+  const int r = (int)(blk / (unsigned)(PD * parts));
+  const int rem = (int)(blk % (unsigned)(PD * parts));
+  const int pd = rem / parts, b0 = (rem - pd * parts) * bpb;
+  const int nbin = min(bpb, PH * PW - b0);
+  const int CG = C / kClChannels, slots = 256 / CG;
+  const int tid = threadIdx.x, cg = tid % CG, slot = tid / CG;
+  const Roi q = roi_setup(rois, r, scale, sr, PD, PH, PW);
+  const bool inb = q.b >= 0 && q.b < N;
+  const int64_t vol = (int64_t)D * H * W;
+  const T *base = feat + (int64_t)(inb ? q.b : 0) * vol * C + cg * kClChannels;
+  const bool sep = q.gd <= 2 && q.gh <= 2 && q.gw <= 2;
+  AxisTaps4 tz;
+  if (inb && sep) tz = bin_taps(q.sd, pd, q.bd, q.gd, D, order);
+  for (int bin = slot; slot < slots && bin < nbin; bin += slots) {
+    const int ph = (b0 + bin) / PW, pw = (b0 + bin) % PW;
+    float acc[kClChannels];
+#pragma unroll
+    for (int c = 0; c < kClChannels; ++c) acc[c] = 0.f;
+    if (inb && sep) {
+      const AxisTaps4 ty = bin_taps(q.sh, ph, q.bh, q.gh, H, order);
+      const AxisTaps4 tx = bin_taps(q.sw, pw, q.bw, q.gw, W, order);
+#pragma unroll
+      for (int kz = 0; kz < 4; ++kz) {
+        if (kz >= tz.n) break;
+#pragma unroll
+        for (int ky = 0; ky < 4; ++ky) {
+          if (ky >= ty.n) break;
+          const float wzy = tz.w[kz] * ty.w[ky];
+          const uint32_t rowo = ((uint32_t)tz.pos[kz] * (uint32_t)H + (uint32_t)ty.pos[ky]) * (uint32_t)W;
+#pragma unroll
+          for (int kx = 0; kx < 4; ++kx) {
+            if (kx >= tx.n) break;
+            const float wgt = wzy * tx.w[kx];
+            float v[kClChannels];
+            load8(base + (rowo + (uint32_t)tx.pos[kx]) * (uint32_t)C, v);
+#pragma unroll
+            for (int c = 0; c < kClChannels; ++c) acc[c] = acc[c] + wgt * v[c];
+          }
+        }
+      }
+    }
+    for (int iz = 0; inb && !sep && iz < q.gd; ++iz) {
+      const float z = sample_coord(q.sd, pd, q.bd, iz, q.gd);
+      for (int iy = 0; iy < q.gh; ++iy) {
+        const float y = sample_coord(q.sh, ph, q.bh, iy, q.gh);
+        for (int ix = 0; ix < q.gw; ++ix) {
+          const float x = sample_coord(q.sw, pw, q.bw, ix, q.gw);
+          int64_t off[8];
+          float w[8];
+          if (!corners(z, y, x, D, H, W, order, off, w)) continue;
+          float s[kClChannels];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            float v[kClChannels];
+            load8(base + (uint32_t)off[k] * (uint32_t)C, v);
+#pragma unroll
+            for (int c = 0; c < kClChannels; ++c) s[c] = k == 0 ? w[0] * v[c] : s[c] + w[k] * v[c];
+          }
+#pragma unroll
+          for (int c = 0; c < kClChannels; ++c) acc[c] = acc[c] + s[c];
+        }
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < kClChannels; ++c) res[(cg * kClChannels + c) * nbin + bin] = from_f<T>(acc[c] / q.count);
+  }
+  __syncthreads();
+  // channel c's bins b0 .. b0 + nbin - 1 of plane pd are nbin consecutive output elements
+  T *o = out + ((int64_t)r * C * PD + pd) * PH * PW + b0;
+  const int64_t cs = (int64_t)PD * PH * PW;
+  for (int e = tid; e < C * nbin; e += 256) {
+    const int c = e / nbin, k = e - c * nbin;
+    o[c * cs + k] = res[e];
+  }
+}
+
+// [N, C, V] -> [N, V, C] in T, through 64 x 64 LDS tiles.
+template <typename T>
+__global__ __launch_bounds__(256) void ncdhw_to_channels_last_kernel(const T *src, T *dst, int C, int64_t V) {
+  __shared__ T t[64][65];
+  const int tid = threadIdx.x, lane = tid & 63, row = tid >> 6;
+  const int64_t v0 = (int64_t)blockIdx.x * 64;
+  const int c0 = blockIdx.y * 64;
+  const int64_t n = blockIdx.z;
+  const T *s = src + n * C * V;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int cc = i * 4 + row;
+    if (c0 + cc < C && v0 + lane < V) t[cc][lane] = s[(int64_t)(c0 + cc) * V + v0 + lane];
+  }
+  __syncthreads();
+  T *d = dst + n * V * C;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int vv = i * 4 + row;
+    if (v0 + vv < V && c0 + lane < C) d[(v0 + vv) * C + c0 + lane] = t[lane][vv];
+  }
+}
+
 template <typename T>
 int forward(const void *features, const void *rois, void *output, int N, int C, int D, int H, int W, int R, int PD,
             int PH, int PW, float scale, int sr, int order, hipStream_t st) {
@@ -691,6 +841,28 @@ int forward(const void *features, const void *rois, void *output, int N, int C, 
   else
     hipLaunchKernelGGL((roi_align3d_forward_kernel<T, 1>), dim3(grid), dim3(256), 0, st, f, ro, o, N, C, D, H, W, R, PD,
                        PH, PW, scale, sr, order);
+  return hipGetLastError() == hipSuccess ? OPS3D_FDA_OK : OPS3D_FDA_ERUNTIME;
+}
+
+template <typename T>
+int forward_cl(const void *features_cl, const void *rois, void *output, int N, int C, int D, int H, int W, int R, int PD,
+               int PH, int PW, float scale, int sr, int order, hipStream_t st) {
+  int bpb = 0, parts = 0;
+  cl_split(C, PH * PW, bpb, parts);
+  const int64_t blocks = (int64_t)R * PD * parts;
+  const int64_t grid = (blocks + 7) / 8 * 8;   // a multiple of 8: the kernel maps blocks to XCDs
+  if (grid >= ((int64_t)1 << 31)) return OPS3D_FDA_EINVAL;
+  const size_t lds = (size_t)C * bpb * sizeof(T);
+  hipLaunchKernelGGL((roi_align3d_forward_cl_kernel<T>), dim3((unsigned)grid), dim3(256), lds, st,
+                     static_cast<const T *>(features_cl), static_cast<const T *>(rois), static_cast<T *>(output), N, C,
+                     D, H, W, PD, PH, PW, scale, sr, order, bpb, parts, (int)blocks);
+  return hipGetLastError() == hipSuccess ? OPS3D_FDA_OK : OPS3D_FDA_ERUNTIME;
+}
+
+template <typename T>
+int to_channels_last(const void *features, void *features_cl, int N, int C, int64_t V, hipStream_t st) {
+  hipLaunchKernelGGL((ncdhw_to_channels_last_kernel<T>), dim3((unsigned)((V + 63) / 64), (unsigned)((C + 63) / 64), N),
+                     dim3(256), 0, st, static_cast<const T *>(features), static_cast<T *>(features_cl), C, V);
   return hipGetLastError() == hipSuccess ? OPS3D_FDA_OK : OPS3D_FDA_ERUNTIME;
 }
 
@@ -747,6 +919,50 @@ int ops3d_roi_align3d_forward(const void *features, const void *rois, void *outp
     default:
       return forward<__hip_bfloat16>(features, rois, output, N, C, D, H, W, R, PD, PH, PW, spatial_scale, sampling_ratio,
                                      order, st);
+  }
+}
+
+int ops3d_roi_align3d_channels_last_supported(int dtype, int C, int D, int H, int W, int PW) {
+  const int e = dtype == OPS3D_FDA_F32 ? 4 : (dtype == OPS3D_FDA_F16 || dtype == OPS3D_FDA_BF16 ? 2 : 0);
+  // element offsets inside one batch item are 32-bit
+  return e > 0 && PW > 0 && D > 0 && H > 0 && W > 0 && cl_supported(C) &&
+                 (int64_t)D * H * W * C < ((int64_t)1 << 32)
+             ? 1
+             : 0;
+}
+
+int ops3d_roi_align3d_to_channels_last(const void *features, void *features_cl, int dtype, int N, int C, int D, int H,
+                                       int W, void *stream) {
+  if (!valid(dtype, N, C, D, H, W, 0, 1, 1, 1, 1) || N > 65535 || (C + 63) / 64 > 65535) return OPS3D_FDA_EINVAL;
+  const int64_t V = (int64_t)D * H * W;
+  if ((int64_t)N * C * V == 0) return OPS3D_FDA_OK;
+  if (!features || !features_cl || (V + 63) / 64 >= ((int64_t)1 << 31)) return OPS3D_FDA_EINVAL;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case OPS3D_FDA_F32: return to_channels_last<float>(features, features_cl, N, C, V, st);
+    case OPS3D_FDA_F16: return to_channels_last<__half>(features, features_cl, N, C, V, st);
+    default: return to_channels_last<__hip_bfloat16>(features, features_cl, N, C, V, st);
+  }
+}
+
+int ops3d_roi_align3d_forward_channels_last(const void *features_cl, const void *rois, void *output, int dtype, int N,
+                                            int C, int D, int H, int W, int R, int PD, int PH, int PW,
+                                            float spatial_scale, int sampling_ratio, int order, void *stream) {
+  if (!valid(dtype, N, C, D, H, W, R, PD, PH, PW, order)) return OPS3D_FDA_EINVAL;
+  if (!ops3d_roi_align3d_channels_last_supported(dtype, C, D, H, W, PW)) return OPS3D_FDA_EINVAL;
+  if ((int64_t)R * C == 0) return OPS3D_FDA_OK;
+  if (!features_cl || !rois || !output || (reinterpret_cast<uintptr_t>(features_cl) & 15u)) return OPS3D_FDA_EINVAL;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case OPS3D_FDA_F32:
+      return forward_cl<float>(features_cl, rois, output, N, C, D, H, W, R, PD, PH, PW, spatial_scale, sampling_ratio,
+                               order, st);
+    case OPS3D_FDA_F16:
+      return forward_cl<__half>(features_cl, rois, output, N, C, D, H, W, R, PD, PH, PW, spatial_scale, sampling_ratio,
+                                order, st);
+    default:
+      return forward_cl<__hip_bfloat16>(features_cl, rois, output, N, C, D, H, W, R, PD, PH, PW, spatial_scale,
+                                        sampling_ratio, order, st);
   }
 }
 

@@ -284,19 +284,54 @@ int roi_checks(const at::Tensor &data, const at::Tensor &rois, const at::Tensor 
   return dtype_code(data);
 }
 
+// Features already in channels_last_3d memory ([N,D,H,W,C] order, 16-byte aligned).
+bool is_channels_last_input(const at::Tensor &input) {
+  return !input.is_contiguous() && input.is_contiguous(at::MemoryFormat::ChannelsLast3d) &&
+         (reinterpret_cast<uintptr_t>(input.data_ptr()) & 15u) == 0;
+}
+
+// Whether the forward runs the channels-last kernel: always on channels-last input it supports;
+// on [N,C,D,H,W] input when the output has at least kRoiClMinOutputs elements, so that the
+// transposed copy of the features is repaid (below that the NCDHW kernel is as fast).
+constexpr int64_t kRoiClMinOutputs = (int64_t)1 << 19;
+bool roi_channels_last(const at::Tensor &input, int code, int R, int pd, int ph, int pw) {
+  const int C = (int)input.size(1);
+  if (!ops3d_roi_align3d_channels_last_supported(code, C, (int)input.size(2), (int)input.size(3),
+                                                 (int)input.size(4), pw) ||
+      input.size(0) > 65535)
+    return false;
+  return is_channels_last_input(input) || (int64_t)R * C * pd * ph * pw >= kRoiClMinOutputs;
+}
+
 void roi_align_3d_forward(const at::Tensor &input, const at::Tensor &rois, at::Tensor output, int64_t pd, int64_t ph,
                           int64_t pw, double spatial_scale, int64_t sampling_ratio, int64_t order) {
   const int code = roi_checks(input, rois, output);
   if (input.dim() != 5) throw std::invalid_argument("features must be [N, C, D, H, W]");
-  const at::Tensor f = input.contiguous(), r = rois.contiguous();
-  if (output.dim() != 5 || output.size(0) != r.size(0) || output.size(1) != f.size(1) || output.size(2) != pd ||
+  const at::Tensor r = rois.contiguous();
+  if (output.dim() != 5 || output.size(0) != r.size(0) || output.size(1) != input.size(1) || output.size(2) != pd ||
       output.size(3) != ph || output.size(4) != pw)
     throw std::invalid_argument("output must be [R, C, out_d, out_h, out_w]");
   const DeviceGuard guard(input.device());
-  const int rc = ops3d_roi_align3d_forward(ptr(f), ptr(r), ptr(output), code, (int)f.size(0), (int)f.size(1),
-                                           (int)f.size(2), (int)f.size(3), (int)f.size(4), (int)r.size(0), (int)pd,
-                                           (int)ph, (int)pw, (float)spatial_scale, (int)sampling_ratio, (int)order,
-                                           stream_of(input));
+  const int N = (int)input.size(0), C = (int)input.size(1), D = (int)input.size(2), H = (int)input.size(3),
+            W = (int)input.size(4), R = (int)r.size(0);
+  int rc;
+  if (roi_channels_last(input, code, R, (int)pd, (int)ph, (int)pw)) {
+    // channels-last kernel: on the caller's channels_last_3d memory, or on a transposed copy
+    at::Tensor fc = input;
+    if (!is_channels_last_input(input)) {
+      const at::Tensor f = input.contiguous();
+      fc = at::empty({N, D, H, W, C}, input.options());
+      rc = ops3d_roi_align3d_to_channels_last(ptr(f), ptr(fc), code, N, C, D, H, W, stream_of(input));
+      if (rc != OPS3D_FDA_OK) throw std::runtime_error("roi_align_3d_forward: channels-last copy failed");
+    }
+    rc = ops3d_roi_align3d_forward_channels_last(ptr(fc), ptr(r), ptr(output), code, N, C, D, H, W, R, (int)pd,
+                                                 (int)ph, (int)pw, (float)spatial_scale, (int)sampling_ratio,
+                                                 (int)order, stream_of(input));
+  } else {
+    const at::Tensor f = input.contiguous();
+    rc = ops3d_roi_align3d_forward(ptr(f), ptr(r), ptr(output), code, N, C, D, H, W, R, (int)pd, (int)ph, (int)pw,
+                                   (float)spatial_scale, (int)sampling_ratio, (int)order, stream_of(input));
+  }
   if (rc == OPS3D_FDA_EINVAL) throw std::invalid_argument("roi_align_3d_forward: invalid sizes or order");
   if (rc != OPS3D_FDA_OK) throw std::runtime_error("roi_align_3d_forward: kernel launch failed");
 }

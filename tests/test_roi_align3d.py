@@ -225,3 +225,100 @@ def test_gpu_many_overlapping_rois(gpu_device):
     gwant = O.backward(g.double().numpy(), rois.double().numpy(), x.shape, 1.0, 1, 1)
     assert_close("overlapping rois output", out.detach(), want, 1e-5, 1e-6)
     assert_close("overlapping rois grad", xg.grad, gwant, 1e-5, 1e-5)
+
+
+# --- channels-last forward ----------------------------------------------------------------------
+CL_CASES = [
+    # N, C, (D, H, W), R, pooled, scale, sampling_ratio, order, dtype
+    (2, 8, (8, 12, 16), 20, (3, 3, 3), 1.0, 2, 1, torch.float32),
+    (2, 16, (8, 12, 16), 20, (2, 3, 4), 0.5, 0, 1, torch.bfloat16),     # adaptive grid
+    (1, 24, (5, 6, 7), 15, (2, 2, 2), 1.0, 3, 0, torch.float16),        # per-sample path, nearest
+    (1, 256, (6, 10, 12), 40, (7, 7, 7), 1.0, 2, 1, torch.bfloat16),    # the benchmark's bins
+    (1, 256, (6, 10, 12), 12, (3, 5, 6), 1.0, 2, 1, torch.float32),
+    (2, 2048, (4, 4, 4), 6, (2, 3, 4), 1.0, 2, 1, torch.bfloat16),      # one bin per block
+    (1, 40, (9, 10, 12), 150, (7, 7, 7), 1.0, 1, 1, torch.float32),     # many overlapping rois
+]
+
+
+def test_channels_last_support_and_argument_errors():
+    """Which shapes the channels-last forward takes, and its argument checks (no GPU needed)."""
+    from ops3d_amd import _extension
+
+    lib = _extension.load_library()
+    ok = lib.ops3d_roi_align3d_channels_last_supported
+    assert ok(2, 256, 32, 64, 64, 7) == 1 and ok(0, 8, 1, 1, 1, 1) == 1 and ok(1, 2048, 4, 4, 4, 4) == 1
+    assert ok(2, 12, 4, 4, 4, 4) == 0                  # C % 8 != 0
+    assert ok(2, 2056, 4, 4, 4, 4) == 0                # C > 2048
+    assert ok(2, 256, 256, 256, 256, 7) == 0           # D*H*W*C >= 2^32
+    assert ok(3, 256, 4, 4, 4, 4) == 0                 # dtype
+    f = lib.ops3d_roi_align3d_forward_channels_last
+    import ctypes
+    a = (2, 1, 256, 4, 4, 4, 3, 2, 2, 2, ctypes.c_float(1.0), 2, 1, None)
+    assert f(None, None, None, *a) == 1                # NULL pointers
+    assert f(None, None, None, 2, 1, 12, 4, 4, 4, 3, 2, 2, 2, ctypes.c_float(1.0), 2, 1, None) == 1
+    assert f(None, None, None, 2, 1, 256, 4, 4, 4, 0, 2, 2, 2, ctypes.c_float(1.0), 2, 1, None) == 0   # no rois
+    t = lib.ops3d_roi_align3d_to_channels_last
+    assert t(None, None, 2, 1, 8, 4, 4, 4, None) == 1
+    assert t(None, None, 2, 0, 8, 4, 4, 4, None) == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", range(len(CL_CASES)))
+def test_gpu_channels_last_same_bits(gpu_device, case):
+    """The channels-last forward computes the NCDHW kernel's terms in its order: the same bits,
+    through the C ABI; and the copy into [N,D,H,W,C] is an exact permutation."""
+    import ctypes
+
+    from fda_helpers import log
+
+    from ops3d_amd import _extension
+
+    lib = _extension.load_library()
+    N, C, size, R, pooled, scale, sr, order, dt = CL_CASES[case]
+    log(f"[case] roi_align3d channels-last #{case}: N={N} C={C} size={size} R={R} pooled={pooled} sr={sr} {dt}")
+    code = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[dt]
+    r = np.random.default_rng(50 + case)
+    x = torch.from_numpy(r.normal(size=(N, C) + size).astype(np.float32)).to(dt).to(gpu_device)
+    rois_np = _rois(R, N, tuple(int(v / scale) for v in size), seed=150 + case)
+    rois_np[0, 0] = N + 3                              # a batch item that does not exist: zeros
+    rois = torch.from_numpy(rois_np).to(dt).to(gpu_device)
+    xc = torch.empty((N,) + size + (C,), dtype=dt, device=gpu_device)
+    o1 = torch.empty((R, C) + pooled, dtype=dt, device=gpu_device)
+    o2 = torch.full_like(o1, 7.0)
+    st = torch.cuda.current_stream().cuda_stream
+    args = (code, N, C, *size, R, *pooled, ctypes.c_float(scale), sr, order, st)
+    assert lib.ops3d_roi_align3d_forward(x.data_ptr(), rois.data_ptr(), o1.data_ptr(), *args) == 0
+    assert lib.ops3d_roi_align3d_to_channels_last(x.data_ptr(), xc.data_ptr(), code, N, C, *size, st) == 0
+    assert lib.ops3d_roi_align3d_forward_channels_last(xc.data_ptr(), rois.data_ptr(), o2.data_ptr(), *args) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(xc, x.permute(0, 2, 3, 4, 1))
+    assert torch.equal(o1, o2)
+    assert torch.all(o2[0] == 0)
+
+
+@pytest.mark.gpu
+def test_gpu_channels_last_through_the_op(gpu_device):
+    """roi_align_3d takes the channels-last kernel for large outputs (here 40 x 64 x 7^3 elements)
+    and for channels_last_3d input: checked against the oracle, and the channels_last_3d input
+    gives the contiguous input's output and gradient bit for bit."""
+    from fda_helpers import assert_close, log
+
+    from ops3d_amd.roi_align import roi_align_3d
+
+    N, C, size, R, pooled = 1, 64, (6, 8, 10), 40, (7, 7, 7)
+    log(f"[case] roi_align3d channels-last op: N={N} C={C} size={size} R={R} pooled={pooled}")
+    r = np.random.default_rng(11)
+    x = torch.from_numpy(r.normal(size=(N, C) + size).astype(np.float32))
+    rois = torch.from_numpy(_rois(R, N, size, seed=12))
+    outs, grads = [], []
+    g = torch.from_numpy(r.normal(size=(R, C) + pooled).astype(np.float32)).to(gpu_device)
+    for fmt in (torch.contiguous_format, torch.channels_last_3d):
+        xg = x.to(gpu_device).contiguous(memory_format=fmt).requires_grad_(True)
+        out = roi_align_3d(xg, rois.to(gpu_device), pooled, 1.0, 2, 1)
+        out.backward(g)
+        outs.append(out.detach())
+        grads.append(xg.grad.contiguous())
+    torch.cuda.synchronize()
+    want = O.forward(x.double().numpy(), rois.double().numpy(), pooled, 1.0, 2, 1)
+    assert_close("channels-last op output", outs[0], want, 1e-5, 1e-6)
+    assert torch.equal(outs[0], outs[1]) and torch.equal(grads[0], grads[1])
