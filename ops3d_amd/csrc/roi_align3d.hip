@@ -799,26 +799,57 @@ __global__ __launch_bounds__(256) void roi_align3d_forward_cl_kernel(const T *fe
   }
 }
 
-// [N, C, V] -> [N, V, C] in T, through 64 x 64 LDS tiles.
+// [N, C, V] -> [N, V, C] in T, through 64 x 64 LDS tiles.  Global accesses are 16-byte pieces
+// (E = 16 / sizeof(T) elements: E voxels of a channel on the way in, E channels of a voxel on
+// the way out, 8 lanes per 128-byte line) when `vec` (C and V multiples of E, both buffers
+// 16-byte aligned); element by element otherwise.
 template <typename T>
-__global__ __launch_bounds__(256) void ncdhw_to_channels_last_kernel(const T *src, T *dst, int C, int64_t V) {
-  __shared__ T t[64][65];
-  const int tid = threadIdx.x, lane = tid & 63, row = tid >> 6;
+__global__ __launch_bounds__(256) void ncdhw_to_channels_last_kernel(const T *src, T *dst, int C, int64_t V, bool vec) {
+  constexpr int E = 16 / (int)sizeof(T);
+  __shared__ T t[64][64 + 2];   // [voxel][channel]; rows 4 bytes apart from a multiple of 128
+  const int tid = threadIdx.x;
   const int64_t v0 = (int64_t)blockIdx.x * 64;
   const int c0 = blockIdx.y * 64;
   const int64_t n = blockIdx.z;
   const T *s = src + n * C * V;
+  T *d = dst + n * V * C;
+  if (vec) {
+    constexpr int PPL = 64 / E;   // pieces per 64-element line
+#pragma unroll
+    for (int i = 0; i < 64 * PPL / 256; ++i) {
+      const int p = i * 256 + tid, cc = p / PPL, vv = (p % PPL) * E;
+      if (c0 + cc < C && v0 + vv < V) {
+        const uint4 u = *reinterpret_cast<const uint4 *>(s + (int64_t)(c0 + cc) * V + v0 + vv);
+        const T *e = reinterpret_cast<const T *>(&u);
+#pragma unroll
+        for (int k = 0; k < E; ++k) t[vv + k][cc] = e[k];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 64 * PPL / 256; ++i) {
+      const int p = i * 256 + tid, vv = p / PPL, cc = (p % PPL) * E;
+      if (v0 + vv < V && c0 + cc < C) {
+        uint4 u;
+        T *e = reinterpret_cast<T *>(&u);
+#pragma unroll
+        for (int k = 0; k < E; ++k) e[k] = t[vv][cc + k];
+        *reinterpret_cast<uint4 *>(d + (v0 + vv) * C + c0 + cc) = u;
+      }
+    }
+    return;
+  }
+  const int lane = tid & 63, row = tid >> 6;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int cc = i * 4 + row;
-    if (c0 + cc < C && v0 + lane < V) t[cc][lane] = s[(int64_t)(c0 + cc) * V + v0 + lane];
+    if (c0 + cc < C && v0 + lane < V) t[lane][cc] = s[(int64_t)(c0 + cc) * V + v0 + lane];
   }
   __syncthreads();
-  T *d = dst + n * V * C;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int vv = i * 4 + row;
-    if (v0 + vv < V && c0 + lane < C) d[(v0 + vv) * C + c0 + lane] = t[lane][vv];
+    if (v0 + vv < V && c0 + lane < C) d[(v0 + vv) * C + c0 + lane] = t[vv][lane];
   }
 }
 
@@ -862,7 +893,9 @@ int forward_cl(const void *features_cl, const void *rois, void *output, int N, i
 template <typename T>
 int to_channels_last(const void *features, void *features_cl, int N, int C, int64_t V, hipStream_t st) {
   hipLaunchKernelGGL((ncdhw_to_channels_last_kernel<T>), dim3((unsigned)((V + 63) / 64), (unsigned)((C + 63) / 64), N),
-                     dim3(256), 0, st, static_cast<const T *>(features), static_cast<T *>(features_cl), C, V);
+                     dim3(256), 0, st, static_cast<const T *>(features), static_cast<T *>(features_cl), C, V,
+                     C % (16 / (int)sizeof(T)) == 0 && V % (16 / (int)sizeof(T)) == 0 &&
+                         ((reinterpret_cast<uintptr_t>(features) | reinterpret_cast<uintptr_t>(features_cl)) & 15u) == 0);
   return hipGetLastError() == hipSuccess ? OPS3D_FDA_OK : OPS3D_FDA_ERUNTIME;
 }
 
