@@ -100,7 +100,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ops3d_roi_align3d_forward.restype = _i
     lib.ops3d_roi_align3d_forward.argtypes = [_vp] * 3 + [_i] * 10 + [ctypes.c_float, _i, _i, _vp]
     lib.ops3d_roi_align3d_backward_workspace_bytes.restype = _sz
-    lib.ops3d_roi_align3d_backward_workspace_bytes.argtypes = [_i] * 9
+    lib.ops3d_roi_align3d_backward_workspace_bytes.argtypes = [_i] * 10
     lib.ops3d_roi_align3d_backward.restype = _i
     lib.ops3d_roi_align3d_backward.argtypes = [_vp] * 4 + [_sz] + [_i] * 10 + [ctypes.c_float, _i, _i, _vp]
     lib.ops3d_roi_align3d_channels_last_supported.restype = _i
@@ -119,7 +119,7 @@ def _ptr(t: torch.Tensor | None) -> int | None:
 class _NativeFDA:
     """Host side of the flash-deform-attn extension, bound to libops3d_fda.so."""
 
-    ABI_VERSION = 6
+    ABI_VERSION = 7
 
     def __init__(self, lib: ctypes.CDLL, path: str, ext=None):
         self._lib = lib
@@ -470,7 +470,8 @@ class _NativeFDA:
         code = self._roi_checks(top_grad, rois, bottom_grad)
         g, r = top_grad.contiguous(), rois.contiguous()
         N, C, D, H, W = bottom_grad.shape
-        wsb = self._lib.ops3d_roi_align3d_backward_workspace_bytes(code, N, C, D, H, W, out_d, out_h, out_w)
+        wsb = self._lib.ops3d_roi_align3d_backward_workspace_bytes(code, N, C, D, H, W, r.shape[0], out_d, out_h,
+                                                                   out_w)
         ws = torch.empty(wsb // 4, dtype=torch.float32, device=g.device) if wsb else None
         with torch.cuda.device(g.device):
             rc = self._lib.ops3d_roi_align3d_backward(

@@ -464,7 +464,7 @@ void *scratch_address() {
 
 extern "C" {
 
-int ops3d_fda_abi_version(void) { return 6; }
+int ops3d_fda_abi_version(void) { return 7; }
 
 const char *ops3d_fda_last_error(void) { return g_last_error.c_str(); }
 

@@ -465,21 +465,41 @@ struct GatherRanges {
 };
 constexpr int kGRangeInts = (int)(sizeof(GatherRanges) / sizeof(int));
 
-// (axis, position, bin) of entry f of a roi's full table (all PD / PH / PW bins per position)
-__device__ __forceinline__ void table_entry(int f, int PD, int PH, int PW, int &ax, int &pos, int &p) {
-  if (f < kGTZ * PD) {
-    ax = 0, pos = f / PD, p = f - pos * PD;
-  } else if (f < kGTZ * PD + kGTY * PH) {
-    f -= kGTZ * PD;
-    ax = 1, pos = f / PH, p = f - pos * PH;
-  } else {
-    f -= kGTZ * PD + kGTY * PH;
-    ax = 2, pos = f / PW, p = f - pos * PW;
+// Per-roi axis tables of the gather backward, made once per call instead of in every tile block
+// that the roi reaches (each of them recomputed them per 16-channel block): for roi r and axis a
+// (size S_a, P_a bins), wt[r][a][x][p] = axis_weight_at(x, .., p, ..) for every position x of
+// the axis, and ft[r][a][x] = the first and last bin with a nonzero weight at x (low and high
+// 16 bits; first > last when none).  The gather kernel reads the same values it computed before.
+// Layout per roi: floats D*PD (z), H*PH (y), W*PW (x); ints D, H, W.
+template <typename T>
+__global__ __launch_bounds__(256) void roi_axis_table_kernel(const T *rois, float *wt, uint32_t *ft, int D, int H,
+                                                             int W, int PD, int PH, int PW, float scale, int sr,
+                                                             int order) {
+  const int r = blockIdx.x, ax = blockIdx.y;
+  const Roi q = roi_setup(rois, r, scale, sr, PD, PH, PW);
+  const int S = ax == 0 ? D : (ax == 1 ? H : W), P = ax == 0 ? PD : (ax == 1 ? PH : PW);
+  const float st = ax == 0 ? q.sd : (ax == 1 ? q.sh : q.sw), bn = ax == 0 ? q.bd : (ax == 1 ? q.bh : q.bw);
+  const int gr = ax == 0 ? q.gd : (ax == 1 ? q.gh : q.gw);
+  const size_t wofs = (size_t)r * ((size_t)D * PD + (size_t)H * PH + (size_t)W * PW) +
+                      (ax == 0 ? 0 : (ax == 1 ? (size_t)D * PD : (size_t)D * PD + (size_t)H * PH));
+  const size_t fofs = (size_t)r * ((size_t)D + H + W) + (ax == 0 ? 0 : (ax == 1 ? (size_t)D : (size_t)D + H));
+  for (int x = threadIdx.x; x < S; x += 256) {
+    uint32_t first = 0xffffu, last = 0u;
+    for (int p = 0; p < P; ++p) {
+      const float w = axis_weight_at(x, st, p, bn, gr, S, order);
+      wt[wofs + (size_t)x * P + p] = w;
+      if (w != 0.f) {
+        first = min(first, (uint32_t)p);
+        last = (uint32_t)p;
+      }
+    }
+    ft[fofs + x] = first | (last << 16);
   }
 }
 
 template <typename T>
-__global__ __launch_bounds__(256) void roi_align3d_backward_gather_kernel(const T *top, const T *rois, T *grad, int N,
+__global__ __launch_bounds__(256) void roi_align3d_backward_gather_kernel(const T *top, const T *rois, T *grad,
+                                                                          const float *wt, const uint32_t *ft, int N,
                                                                           int C, int D, int H, int W, int R, int PD,
                                                                           int PH, int PW, float scale, int sr,
                                                                           int order) {
@@ -507,8 +527,10 @@ __global__ __launch_bounds__(256) void roi_align3d_backward_gather_kernel(const 
   const int zl = tid / (kGTY * kGTX), yl = (tid / kGTX) % kGTY, xl = tid % kGTX;
   const int S[3] = {D, H, W}, TT[3] = {kGTZ, kGTY, kGTX};
   const int pos0[3] = {0, kGTZ, kGTZ + kGTY};     // first position of each axis in the ranges
-  const int E = kGTZ * PD + kGTY * PH + kGTX * PW;   // entries of a roi's full table
   const int64_t pvol = (int64_t)PD * PH * PW;
+  const size_t wroi = (size_t)D * PD + (size_t)H * PH + (size_t)W * PW, froi = (size_t)D + H + W;
+  const size_t wax[3] = {0, (size_t)D * PD, (size_t)D * PD + (size_t)H * PH}, fax[3] = {0, (size_t)D, (size_t)D + H};
+  const int PA[3] = {PD, PH, PW};
 
   float acc[kGCC];
 #pragma unroll
@@ -548,18 +570,20 @@ __global__ __launch_bounds__(256) void roi_align3d_backward_gather_kernel(const 
       for (int i = tid; i < kGGroup * kGRangeInts; i += 256)
         reinterpret_cast<int *>(rng_l)[i] = (i & 1) ? -1 : (1 << 30);
       __syncthreads();   // (also: the previous group's sums are done with the LDS state)
-      // 1. bin ranges of the next gmax rois: a thread per (roi, position, bin)
-      for (int e = tid; e < gmax * E; e += 256) {
-        const int w = e / E;
-        int ax, pos, p;
-        table_entry(e - w * E, PD, PH, PW, ax, pos, p);
-        const GatherRoi &g = roi_l[li + w];
+      // 1. bin ranges of the next gmax rois, from the axis tables: a thread per (roi, position)
+      for (int e = tid; e < gmax * kGPos; e += 256) {
+        const int w = e / kGPos, k = e - w * kGPos;
+        const int ax = k < kGTZ ? 0 : (k < kGTZ + kGTY ? 1 : 2), pos = k - pos0[ax];
         const int at = t0[ax] + pos;
-        if (at < S[ax] && axis_weight_at(at, g.s[ax], p, g.bin[ax], g.grid[ax], S[ax], order) != 0.f) {
-          atomicMin(&rng_l[w].box[ax][0], p);
-          atomicMax(&rng_l[w].box[ax][1], p);
-          atomicMin(&rng_l[w].pos[pos0[ax] + pos][0], p);
-          atomicMax(&rng_l[w].pos[pos0[ax] + pos][1], p);
+        if (at < S[ax]) {
+          const uint32_t fl = ft[(size_t)rid_l[li + w] * froi + fax[ax] + at];
+          const int first = (int)(fl & 0xffffu), last = (int)(fl >> 16);
+          if (first <= last) {
+            atomicMin(&rng_l[w].box[ax][0], first);
+            atomicMax(&rng_l[w].box[ax][1], last);
+            rng_l[w].pos[k][0] = first;
+            rng_l[w].pos[k][1] = last;
+          }
         }
       }
       __syncthreads();
@@ -593,7 +617,6 @@ __global__ __launch_bounds__(256) void roi_align3d_backward_gather_kernel(const 
         int w = 0;
         while (goff_l[w + 1][1] <= e) ++w;
         const GatherRanges &rg = rng_l[w];
-        const GatherRoi &g = roi_l[li + w];
         int f = e - goff_l[w][1], ax = 0;
         for (; ax < 2; ++ax) {
           const int sz = TT[ax] * (rg.box[ax][1] - rg.box[ax][0] + 1);
@@ -603,7 +626,7 @@ __global__ __launch_bounds__(256) void roi_align3d_backward_gather_kernel(const 
         const int nb = rg.box[ax][1] - rg.box[ax][0] + 1;
         const int pos = f / nb, p = rg.box[ax][0] + (f - pos * nb);
         const int at = t0[ax] + pos;
-        tab_l[e] = at < S[ax] ? axis_weight_at(at, g.s[ax], p, g.bin[ax], g.grid[ax], S[ax], order) : 0.f;
+        tab_l[e] = at < S[ax] ? wt[(size_t)rid_l[li + w] * wroi + wax[ax] + (size_t)at * PA[ax] + p] : 0.f;
       }
       // ... and top for their boxes of bins and the block's channels, as fp32 (consecutive
       // threads on consecutive bins of one channel quad)
@@ -905,9 +928,14 @@ int backward(const void *grad_output, const void *rois, void *grad_input, float 
   if (gather_fits(PD, PH, PW)) {
     const int64_t blocks = (int64_t)N * ((C + kGCC - 1) / kGCC) * ((D + kGTZ - 1) / kGTZ) * ((H + kGTY - 1) / kGTY) *
                            ((W + kGTX - 1) / kGTX);
+    float *wt = acc;
+    uint32_t *ft = reinterpret_cast<uint32_t *>(acc + (size_t)R * ((size_t)D * PD + (size_t)H * PH + (size_t)W * PW));
+    if (R > 0)
+      hipLaunchKernelGGL((roi_axis_table_kernel<T>), dim3((unsigned)R, 3), dim3(256), 0, st,
+                         static_cast<const T *>(rois), wt, ft, D, H, W, PD, PH, PW, scale, sr, order);
     hipLaunchKernelGGL((roi_align3d_backward_gather_kernel<T>), dim3((unsigned)blocks), dim3(256), 0, st,
                        static_cast<const T *>(grad_output), static_cast<const T *>(rois), static_cast<T *>(grad_input),
-                       N, C, D, H, W, R, PD, PH, PW, scale, sr, order);
+                       wt, ft, N, C, D, H, W, R, PD, PH, PW, scale, sr, order);
     return hipGetLastError() == hipSuccess ? OPS3D_FDA_OK : OPS3D_FDA_ERUNTIME;
   }
   const int64_t nin = (int64_t)N * C * D * H * W;
@@ -999,10 +1027,12 @@ int ops3d_roi_align3d_forward_channels_last(const void *features_cl, const void 
   }
 }
 
-size_t ops3d_roi_align3d_backward_workspace_bytes(int dtype, int N, int C, int D, int H, int W, int PD, int PH,
-                                                 int PW) {
+size_t ops3d_roi_align3d_backward_workspace_bytes(int dtype, int N, int C, int D, int H, int W, int R, int PD,
+                                                 int PH, int PW) {
   (void)dtype;
-  if (N <= 0 || C <= 0 || D <= 0 || H <= 0 || W <= 0 || gather_fits(PD, PH, PW)) return 0;
+  if (N <= 0 || C <= 0 || D <= 0 || H <= 0 || W <= 0 || R < 0 || PD <= 0 || PH <= 0 || PW <= 0) return 0;
+  if (gather_fits(PD, PH, PW))   // the per-roi axis tables
+    return (size_t)R * ((size_t)D * PD + (size_t)H * PH + (size_t)W * PW + (size_t)D + H + W) * 4;
   return (size_t)N * C * D * H * W * sizeof(float);
 }
 
@@ -1012,7 +1042,7 @@ int ops3d_roi_align3d_backward(const void *grad_output, const void *rois, void *
   if (!valid(dtype, N, C, D, H, W, R, PD, PH, PW, order)) return OPS3D_FDA_EINVAL;
   if ((int64_t)N * C == 0) return OPS3D_FDA_OK;
   if (!grad_input || ((int64_t)R > 0 && (!grad_output || !rois))) return OPS3D_FDA_EINVAL;
-  const size_t need = ops3d_roi_align3d_backward_workspace_bytes(dtype, N, C, D, H, W, PD, PH, PW);
+  const size_t need = ops3d_roi_align3d_backward_workspace_bytes(dtype, N, C, D, H, W, R, PD, PH, PW);
   if (need > 0 && (workspace_bytes < need || !workspace || (reinterpret_cast<uintptr_t>(workspace) & 3u)))
     return OPS3D_FDA_EINVAL;
   hipStream_t st = static_cast<hipStream_t>(stream);

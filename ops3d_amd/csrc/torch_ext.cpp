@@ -347,7 +347,8 @@ void roi_align_3d_backward(const at::Tensor &top_grad, const at::Tensor &rois, a
       g.size(4) != pw)
     throw std::invalid_argument("top_grad must be [R, C, out_d, out_h, out_w]");
   const DeviceGuard guard(top_grad.device());
-  const size_t wsb = ops3d_roi_align3d_backward_workspace_bytes(code, N, C, D, H, W, (int)pd, (int)ph, (int)pw);
+  const size_t wsb =
+      ops3d_roi_align3d_backward_workspace_bytes(code, N, C, D, H, W, (int)r.size(0), (int)pd, (int)ph, (int)pw);
   at::Tensor ws;
   if (wsb) ws = at::empty({(int64_t)(wsb / 4)}, top_grad.options().dtype(at::kFloat));
   const int rc = ops3d_roi_align3d_backward(ptr(g), ptr(r), ptr(bottom_grad), ptr(ws), wsb, code, N, C, D, H, W,

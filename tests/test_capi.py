@@ -52,7 +52,7 @@ def test_bench_library_exports_every_declared_symbol():
 
 
 def test_abi_version_and_support_table(lib):
-    assert lib.ops3d_fda_abi_version() == 6
+    assert lib.ops3d_fda_abi_version() == 7
     F32, F16, BF16 = 0, 1, 2
     for d in (8, 16, 24, 32, 48, 64, 96, 128, 192, 256):
         assert lib.ops3d_fda_supported(BF16, d) == 1, d
