@@ -45,11 +45,12 @@ OPS3D_FDA_API int ops3d_roi_align3d_forward_channels_last(const void *features_c
 OPS3D_FDA_API int ops3d_roi_align3d_to_channels_last(const void *features, void *features_cl, int dtype, int N, int C,
                                                      int D, int H, int W, void *stream);
 
-/* Bytes of workspace ops3d_roi_align3d_backward needs for R rois and output bins PD x PH x PW:
- * when PD, PH, PW <= 64 and PD*PH*PW <= 384 (the backward is then a gather straight into
- * grad_input) R*(D*PD + H*PH + W*PW + D + H + W)*4 for the per-roi axis weight tables; else
- * N*C*D*H*W*4 (the gradient is accumulated channels-last in fp32 by atomics, then transposed
- * into grad_input).  4-byte aligned. */
+/* Bytes of workspace ops3d_roi_align3d_backward needs for R rois and output bins PD x PH x PW,
+ * 16-byte aligned: when PD, PH, PW <= 64 and PD*PH*PW <= 384 (the backward is then a gather
+ * straight into grad_input) the per-roi axis weight tables, R*(D*PD + H*PH + W*PW + D + H + W)*4
+ * bytes rounded up to 16, plus a channels-last copy of grad_output, R*PD*PH*PW*C elements (0
+ * when R = 0); else N*C*D*H*W*4 (the gradient is accumulated channels-last in fp32 by atomics,
+ * then transposed into grad_input). */
 OPS3D_FDA_API size_t ops3d_roi_align3d_backward_workspace_bytes(int dtype, int N, int C, int D, int H, int W, int R,
                                                                 int PD, int PH, int PW);
 
@@ -57,8 +58,8 @@ OPS3D_FDA_API size_t ops3d_roi_align3d_backward_workspace_bytes(int dtype, int N
  * Backward: grad_input [N,C,D,H,W] = the adjoint of the forward applied to grad_output
  * [R,C,PD,PH,PW]; every element of grad_input is written: its old contents are overwritten
  * (the reference's kernel adds into a buffer its caller zeroed; a caller accumulating gradients
- * adds the result itself).  With the bin limits above it is a gather (after a pass that writes
- * each roi's per-axis bin weights to the workspace): each voxel sums the rois that reach it in
+ * adds the result itself).  With the bin limits above it is a gather (after passes that write
+ * each roi's per-axis bin weights and grad_output channels-last to the workspace): each voxel sums the rois that reach it in
  * roi order, the same bits on every run; else
  * the samples' corner contributions are added by fp32 atomics into the cleared workspace, whose
  * order -- and so the last bit -- can differ between runs, as with the reference's atomics.

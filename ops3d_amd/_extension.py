@@ -472,7 +472,7 @@ class _NativeFDA:
         N, C, D, H, W = bottom_grad.shape
         wsb = self._lib.ops3d_roi_align3d_backward_workspace_bytes(code, N, C, D, H, W, r.shape[0], out_d, out_h,
                                                                    out_w)
-        ws = torch.empty(wsb // 4, dtype=torch.float32, device=g.device) if wsb else None
+        ws = torch.empty((wsb + 3) // 4, dtype=torch.float32, device=g.device) if wsb else None
         with torch.cuda.device(g.device):
             rc = self._lib.ops3d_roi_align3d_backward(
                 _ptr(g), _ptr(r), _ptr(bottom_grad), _ptr(ws), wsb, code, N, C, D, H, W, r.shape[0], out_d, out_h,

@@ -498,8 +498,9 @@ __global__ __launch_bounds__(256) void roi_axis_table_kernel(const T *rois, floa
 }
 
 template <typename T>
-__global__ __launch_bounds__(256) void roi_align3d_backward_gather_kernel(const T *top, const T *rois, T *grad,
-                                                                          const float *wt, const uint32_t *ft, int N,
+__global__ __launch_bounds__(256) void roi_align3d_backward_gather_kernel(const T *top_cl, const T *rois, T *grad,
+                                                                          const float *wt, const uint32_t *ft, bool vec4,
+                                                                          int N,
                                                                           int C, int D, int H, int W, int R, int PD,
                                                                           int PH, int PW, float scale, int sr,
                                                                           int order) {
@@ -628,23 +629,41 @@ __global__ __launch_bounds__(256) void roi_align3d_backward_gather_kernel(const 
         const int at = t0[ax] + pos;
         tab_l[e] = at < S[ax] ? wt[(size_t)rid_l[li + w] * wroi + wax[ax] + (size_t)at * PA[ax] + p] : 0.f;
       }
-      // ... and top for their boxes of bins and the block's channels, as fp32 (consecutive
-      // threads on consecutive bins of one channel quad)
+      // ... and top for their boxes of bins and the block's channels, as fp32, from the
+      // channels-last copy [R, bins, C] (consecutive threads on consecutive channel quads of one
+      // bin: the block's 16 channels of a bin are one contiguous run)
       for (int e = tid; e < nbin * (kGCC / 4); e += 256) {
-        const int k4 = e / nbin, gb = e - k4 * nbin;
+        const int gb = e / (kGCC / 4), k4 = e - gb * (kGCC / 4);
         int w = 0;
         while (goff_l[w + 1][0] <= gb) ++w;
         const GatherRanges &rg = rng_l[w];
         const int lb = gb - goff_l[w][0];
         const int nby = rg.box[1][1] - rg.box[1][0] + 1, nbx = rg.box[2][1] - rg.box[2][0] + 1;
         const int bx = lb % nbx, bzy = lb / nbx, by = bzy % nby, bz = bzy / nby;
-        const T *src = top + ((int64_t)rid_l[li + w] * C + c0 + 4 * k4) * pvol +
-                       ((int64_t)(rg.box[0][0] + bz) * PH + rg.box[1][0] + by) * PW + rg.box[2][0] + bx;
+        const int c = c0 + 4 * k4;
+        const T *src = top_cl + ((int64_t)rid_l[li + w] * pvol +
+                                 ((int64_t)(rg.box[0][0] + bz) * PH + rg.box[1][0] + by) * PW + rg.box[2][0] + bx) *
+                                    C + c;
         float4 v;
-        v.x = c0 + 4 * k4 + 0 < C ? to_f(src[0]) : 0.f;
-        v.y = c0 + 4 * k4 + 1 < C ? to_f(src[pvol]) : 0.f;
-        v.z = c0 + 4 * k4 + 2 < C ? to_f(src[2 * pvol]) : 0.f;
-        v.w = c0 + 4 * k4 + 3 < C ? to_f(src[3 * pvol]) : 0.f;
+        if (vec4 && c < C) {   // 4 channels, one 8- or 16-byte load
+          float f[4];
+          if constexpr (sizeof(T) == 4) {
+            const float4 u = *reinterpret_cast<const float4 *>(src);
+            f[0] = u.x; f[1] = u.y; f[2] = u.z; f[3] = u.w;
+          } else {
+            const uint2 u = *reinterpret_cast<const uint2 *>(src);
+            const uint32_t wd[2] = {u.x, u.y};
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+              f[k] = to_f(__builtin_bit_cast(T, (unsigned short)((k & 1) ? (wd[k >> 1] >> 16) : (wd[k >> 1] & 0xffffu))));
+          }
+          v = make_float4(f[0], f[1], f[2], f[3]);
+        } else {
+          v.x = c + 0 < C ? to_f(src[0]) : 0.f;
+          v.y = c + 1 < C ? to_f(src[1]) : 0.f;
+          v.z = c + 2 < C ? to_f(src[2]) : 0.f;
+          v.w = c + 3 < C ? to_f(src[3]) : 0.f;
+        }
         g_l[k4][gb] = v;
       }
       __syncthreads();
@@ -922,20 +941,40 @@ int to_channels_last(const void *features, void *features_cl, int N, int C, int6
   return hipGetLastError() == hipSuccess ? OPS3D_FDA_OK : OPS3D_FDA_ERUNTIME;
 }
 
+// Bytes of the gather backward's per-roi axis tables, rounded up to 16 (the channels-last copy of
+// grad_output follows them).
+inline size_t gather_tables_bytes(int R, int D, int H, int W, int PD, int PH, int PW) {
+  const size_t b = (size_t)R * ((size_t)D * PD + (size_t)H * PH + (size_t)W * PW + (size_t)D + H + W) * 4;
+  return (b + 15) & ~(size_t)15;
+}
+
 template <typename T>
 int backward(const void *grad_output, const void *rois, void *grad_input, float *acc, int N, int C, int D, int H,
              int W, int R, int PD, int PH, int PW, float scale, int sr, int order, hipStream_t st) {
   if (gather_fits(PD, PH, PW)) {
     const int64_t blocks = (int64_t)N * ((C + kGCC - 1) / kGCC) * ((D + kGTZ - 1) / kGTZ) * ((H + kGTY - 1) / kGTY) *
                            ((W + kGTX - 1) / kGTX);
+    // workspace: the per-roi axis tables, then grad_output channels-last [R, bins, C]
     float *wt = acc;
     uint32_t *ft = reinterpret_cast<uint32_t *>(acc + (size_t)R * ((size_t)D * PD + (size_t)H * PH + (size_t)W * PW));
-    if (R > 0)
+    T *top_cl = reinterpret_cast<T *>(reinterpret_cast<char *>(acc) + gather_tables_bytes(R, D, H, W, PD, PH, PW));
+    const int64_t pvol = (int64_t)PD * PH * PW;
+    if (R > 0) {
       hipLaunchKernelGGL((roi_axis_table_kernel<T>), dim3((unsigned)R, 3), dim3(256), 0, st,
                          static_cast<const T *>(rois), wt, ft, D, H, W, PD, PH, PW, scale, sr, order);
-    hipLaunchKernelGGL((roi_align3d_backward_gather_kernel<T>), dim3((unsigned)blocks), dim3(256), 0, st,
-                       static_cast<const T *>(grad_output), static_cast<const T *>(rois), static_cast<T *>(grad_input),
-                       wt, ft, N, C, D, H, W, R, PD, PH, PW, scale, sr, order);
+      for (int r0 = 0; r0 < R; r0 += 65535) {   // grid z: at most 65535 rois per launch
+        const int nr = min(65535, R - r0);
+        const T *src = static_cast<const T *>(grad_output) + (int64_t)r0 * C * pvol;
+        T *dst = top_cl + (int64_t)r0 * C * pvol;
+        hipLaunchKernelGGL((ncdhw_to_channels_last_kernel<T>), dim3((unsigned)((pvol + 63) / 64), (unsigned)((C + 63) / 64), nr),
+                           dim3(256), 0, st, src, dst, C, pvol,
+                           C % (16 / (int)sizeof(T)) == 0 && pvol % (16 / (int)sizeof(T)) == 0 &&
+                               ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15u) == 0);
+      }
+    }
+    hipLaunchKernelGGL((roi_align3d_backward_gather_kernel<T>), dim3((unsigned)blocks), dim3(256), 0, st, top_cl,
+                       static_cast<const T *>(rois), static_cast<T *>(grad_input), wt, ft, C % 4 == 0, N, C, D, H, W, R,
+                       PD, PH, PW, scale, sr, order);
     return hipGetLastError() == hipSuccess ? OPS3D_FDA_OK : OPS3D_FDA_ERUNTIME;
   }
   const int64_t nin = (int64_t)N * C * D * H * W;
@@ -1031,8 +1070,10 @@ size_t ops3d_roi_align3d_backward_workspace_bytes(int dtype, int N, int C, int D
                                                  int PH, int PW) {
   (void)dtype;
   if (N <= 0 || C <= 0 || D <= 0 || H <= 0 || W <= 0 || R < 0 || PD <= 0 || PH <= 0 || PW <= 0) return 0;
-  if (gather_fits(PD, PH, PW))   // the per-roi axis tables
-    return (size_t)R * ((size_t)D * PD + (size_t)H * PH + (size_t)W * PW + (size_t)D + H + W) * 4;
+  if (gather_fits(PD, PH, PW))   // the per-roi axis tables and grad_output channels-last
+    return R == 0 ? 0
+                  : gather_tables_bytes(R, D, H, W, PD, PH, PW) +
+                        (size_t)R * C * PD * PH * PW * (dtype == OPS3D_FDA_F32 ? 4 : 2);
   return (size_t)N * C * D * H * W * sizeof(float);
 }
 
@@ -1043,7 +1084,7 @@ int ops3d_roi_align3d_backward(const void *grad_output, const void *rois, void *
   if ((int64_t)N * C == 0) return OPS3D_FDA_OK;
   if (!grad_input || ((int64_t)R > 0 && (!grad_output || !rois))) return OPS3D_FDA_EINVAL;
   const size_t need = ops3d_roi_align3d_backward_workspace_bytes(dtype, N, C, D, H, W, R, PD, PH, PW);
-  if (need > 0 && (workspace_bytes < need || !workspace || (reinterpret_cast<uintptr_t>(workspace) & 3u)))
+  if (need > 0 && (workspace_bytes < need || !workspace || (reinterpret_cast<uintptr_t>(workspace) & 15u)))
     return OPS3D_FDA_EINVAL;
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (dtype) {

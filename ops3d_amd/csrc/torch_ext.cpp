@@ -350,7 +350,7 @@ void roi_align_3d_backward(const at::Tensor &top_grad, const at::Tensor &rois, a
   const size_t wsb =
       ops3d_roi_align3d_backward_workspace_bytes(code, N, C, D, H, W, (int)r.size(0), (int)pd, (int)ph, (int)pw);
   at::Tensor ws;
-  if (wsb) ws = at::empty({(int64_t)(wsb / 4)}, top_grad.options().dtype(at::kFloat));
+  if (wsb) ws = at::empty({(int64_t)((wsb + 3) / 4)}, top_grad.options().dtype(at::kFloat));
   const int rc = ops3d_roi_align3d_backward(ptr(g), ptr(r), ptr(bottom_grad), ptr(ws), wsb, code, N, C, D, H, W,
                                             (int)r.size(0), (int)pd, (int)ph, (int)pw, (float)spatial_scale,
                                             (int)sampling_ratio, (int)order, stream_of(top_grad));

@@ -126,15 +126,21 @@ def test_gpu_matches_oracle(gpu_device, case):
 
 def test_backward_workspace_sizes():
     """The gather backward (at most 64 bins per axis and 384 in all) needs the per-roi axis
-    weight tables, R * (D*PD + H*PH + W*PW + D + H + W) words; the atomic one an fp32 buffer of
-    grad_input's size (the C ABI, no GPU needed)."""
+    weight tables, R * (D*PD + H*PH + W*PW + D + H + W) words rounded up to 16 bytes, and a
+    channels-last copy of grad_output; the atomic one an fp32 buffer of grad_input's size (the
+    C ABI, no GPU needed)."""
     from ops3d_amd import _extension
 
     lib = _extension.load_library()
     f = lib.ops3d_roi_align3d_backward_workspace_bytes
-    assert f(2, 2, 256, 32, 64, 64, 512, 7, 7, 7) == 512 * (32 * 7 + 64 * 7 + 64 * 7 + 32 + 64 + 64) * 4
-    assert f(0, 1, 5, 6, 7, 9, 6, 6, 8, 8) == 6 * (6 * 6 + 7 * 8 + 9 * 8 + 6 + 7 + 9) * 4
-    assert f(0, 1, 5, 6, 7, 9, 0, 6, 8, 8) == 0                          # no rois: no tables
+
+    def tables(R, D, H, W, PD, PH, PW):
+        return (R * (D * PD + H * PH + W * PW + D + H + W) * 4 + 15) // 16 * 16
+
+    assert f(2, 2, 256, 32, 64, 64, 512, 7, 7, 7) == tables(512, 32, 64, 64, 7, 7, 7) + 512 * 343 * 256 * 2
+    assert f(0, 1, 5, 6, 7, 9, 6, 6, 8, 8) == tables(6, 6, 7, 9, 6, 8, 8) + 6 * 384 * 5 * 4
+    assert f(1, 1, 3, 6, 7, 9, 5, 1, 1, 3) == tables(5, 6, 7, 9, 1, 1, 3) + 5 * 3 * 3 * 2
+    assert f(0, 1, 5, 6, 7, 9, 0, 6, 8, 8) == 0                          # no rois: nothing
     assert f(0, 1, 5, 6, 7, 9, 6, 7, 8, 8) == 5 * 6 * 7 * 9 * 4          # 448 bins: atomic path
     assert f(2, 1, 3, 6, 7, 9, 2, 2, 65, 2) == 3 * 6 * 7 * 9 * 4
     assert f(2, 1, 3, 6, 7, 9, 0, 2, 65, 2) == 3 * 6 * 7 * 9 * 4          # atomic path, no rois
