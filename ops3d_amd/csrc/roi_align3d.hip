@@ -12,12 +12,14 @@
 // corner), and the samples averaged.  All arithmetic is fp32 (16-bit types are widened on load;
 // the reference computes in the element type), rounded step by step (no contraction).
 //
-// Forward: a gather, one thread per (roi, CPT = 4 channels, bin).  With at most 2 samples per
-// bin and axis it is separable: the bin's average is the sum over its distinct z, y and x taps
-// (at most 4 each) of the per-axis weight sums times the value, fewer loads than 8 corners per
-// sample; larger sample grids take the reference's per-sample loop.  Backward: the adjoint, as a gather when
-// the output has at most 64 bins per axis and 384 in all (each voxel sums, in registers, the
-// rois that reach it, in roi order: no atomics, no workspace, the same bits on every run),
+// Forward: a gather, one thread per (roi, CPT = 4 channels, bin), or on channels-last features
+// one lane per (bin, 8 channels) (the same bits).  With at most 2 samples per bin and axis it is
+// separable: the bin's average is the sum over its distinct z, y and x taps (at most 4 each) of
+// the per-axis weight sums times the value, fewer loads than 8 corners per sample; larger sample
+// grids take the reference's per-sample loop.  Backward: the adjoint, as a gather when the
+// output has at most 64 bins per axis and 384 in all (each voxel sums, in registers, the rois
+// that reach it, in roi order: no atomics, the same bits on every run; the workspace holds the
+// rois' axis weight tables and a channels-last copy of grad_output),
 // otherwise by fp32 atomics into a channels-last workspace (64 lanes = 64 contiguous channels
 // per atomic instruction) transposed into grad_input afterwards.  A roi whose batch index is
 // outside [0, N) reads and writes nothing (its output is 0; the reference indexes out of
