@@ -331,3 +331,36 @@ def test_gpu_channels_last_through_the_op(gpu_device):
     want = O.forward(x.double().numpy(), rois.double().numpy(), pooled, 1.0, 2, 1)
     assert_close("channels-last op output", outs[0], want, 1e-5, 1e-6)
     assert torch.equal(outs[0], outs[1]) and torch.equal(grads[0], grads[1])
+
+
+@pytest.mark.gpu
+def test_gpu_backward_more_rois_than_one_grid_dimension(gpu_device):
+    """More than 65535 rois: the gather backward's channels-last copy of grad_output is made in
+    launches of at most 65535 rois.  Checked two ways: the adjoint identity <F(x), g> = <x, F^T g>
+    (float64 sums of the GPU's fp32 results) and against the sum of the two halves' gradients."""
+    from fda_helpers import log
+
+    from ops3d_amd.roi_align import roi_align_3d
+
+    N, C, size, R, pooled = 1, 8, (6, 7, 9), 70000, (1, 2, 1)
+    log(f"[case] roi_align3d backward with R={R} rois")
+    r = np.random.default_rng(21)
+    x = torch.from_numpy(r.normal(size=(N, C) + size).astype(np.float32)).to(gpu_device)
+    rois = torch.from_numpy(_rois(R, N, size, seed=22)).to(gpu_device)
+    g = torch.from_numpy(r.normal(size=(R, C) + pooled).astype(np.float32)).to(gpu_device)
+
+    def grad_of(rr, gg):
+        xg = x.clone().requires_grad_(True)
+        roi_align_3d(xg, rr, pooled, 1.0, 2, 1).backward(gg)
+        return xg.grad
+
+    full = grad_of(rois, g)
+    h = 65535
+    halves = grad_of(rois[:h], g[:h]) + grad_of(rois[h:], g[h:])
+    with torch.no_grad():
+        out = roi_align_3d(x, rois, pooled, 1.0, 2, 1)
+    torch.cuda.synchronize()
+    lhs = float((out.double() * g.double()).sum())
+    rhs = float((x.double() * full.double()).sum())
+    assert abs(lhs - rhs) <= 1e-4 * float((out.double().abs() * g.double().abs()).sum())
+    assert torch.allclose(full, halves, rtol=1e-5, atol=1e-4)
