@@ -305,8 +305,13 @@ def measure_roi_align(steps, warmup, device, dtype="bf16"):
         with torch.no_grad():
             roi_align_3d(xcl, rois, pooled, 1.0, 2, 1)
 
+    def fwd_adaptive():   # sampling_ratio 0: ceil(extent / 7) samples per axis, 1-5 here
+        with torch.no_grad():
+            roi_align_3d(x, rois, pooled, 1.0, 0, 1)
+
     return {"fwd": b.time_loop(fwd, steps, warmup), "step": b.time_loop(step, steps, warmup),
-            "fwd_cl": b.time_loop(fwd_cl, steps, warmup), "samples": R * C * 343 * 8, "out_bytes": out_bytes}
+            "fwd_cl": b.time_loop(fwd_cl, steps, warmup), "fwd_adaptive": b.time_loop(fwd_adaptive, steps, warmup),
+            "samples": R * C * 343 * 8, "out_bytes": out_bytes}
 
 
 def measure_dcnv4(steps, warmup, device, dtype="bf16"):
@@ -573,7 +578,8 @@ def main():
         f, st = o["fwd"]["mean"], o["step"]["mean"]
         log(f" roi_align3d bf16 [2,256,32,64,64] x 512 rois, 7^3 bins, 8 samples | fwd {f * 1e3:8.1f} us "
             f"({o['samples'] / f / 1e6:.3g} G samples/s) | fwd+bwd {st * 1e3:8.1f} us | fwd on channels_last_3d "
-            f"features {o['fwd_cl']['mean'] * 1e3:8.1f} us")
+            f"features {o['fwd_cl']['mean'] * 1e3:8.1f} us | fwd with sampling_ratio 0 (adaptive) "
+            f"{o['fwd_adaptive']['mean'] * 1e3:8.1f} us")
         if args.roi:
             return
     if args.nms or args.all:

@@ -109,25 +109,32 @@ __device__ __forceinline__ bool corners(float z, float y, float x, int D, int H,
   return true;
 }
 
-// The taps of one axis of a bin with at most 2 samples on it: up to 4 distinct positions with
-// their summed weights (weights of invalid samples and collapsed taps are left out).  Static
+// The taps of one axis of a bin: up to NT distinct positions with their summed weights, in the
+// order the samples first reach them (increasing position; weights of invalid samples and
+// collapsed taps are left out); `over` when the samples reach more than NT positions.  Static
 // register indices only (predicated), so nothing spills to scratch.
-struct AxisTaps4 {
+template <int NT>
+struct AxisTaps {
   int n;
-  int pos[4];
-  float w[4];
+  bool over;
+  int pos[NT];
+  float w[NT];
   __device__ __forceinline__ void add(int p, float wt) {
     if (wt == 0.f) return;
     bool done = false;
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
+    for (int k = 0; k < NT; ++k)
       if (!done && k < n && pos[k] == p) {
         w[k] += wt;
         done = true;
       }
     if (!done) {
+      if (n == NT) {
+        over = true;
+        return;
+      }
 #pragma unroll
-      for (int k = 0; k < 4; ++k)
+      for (int k = 0; k < NT; ++k)
         if (k == n) {
           pos[k] = p;
           w[k] = wt;
@@ -135,9 +142,25 @@ struct AxisTaps4 {
       ++n;
     }
   }
+  // drop the first tap (register moves, so a loop over the taps needs no dynamic index)
+  __device__ __forceinline__ void shift() {
+#pragma unroll
+    for (int k = 0; k + 1 < NT; ++k) {
+      pos[k] = pos[k + 1];
+      w[k] = w[k + 1];
+    }
+    --n;
+  }
 };
+using AxisTaps4 = AxisTaps<4>;
+using AxisTaps8 = AxisTaps<8>;
+// Grids of more than 2 samples per axis take the separable sum when every axis of the bin has
+// at most kSepTaps distinct taps, the per-sample loop otherwise.
+constexpr int kSepTaps = 8;
 
 __device__ __forceinline__ AxisTaps4 bin_taps(float start, int p, float bin, int grid, int size, int order);
+template <int NT>
+__device__ __forceinline__ AxisTaps<NT> bin_taps_n(float start, int p, float bin, int grid, int size, int order);
 
 template <typename T, int CPT>
 __global__ __launch_bounds__(256) void roi_align3d_forward_kernel(const T *feat, const T *rois, T *out, int N, int C, int D,
@@ -183,7 +206,32 @@ __global__ __launch_bounds__(256) void roi_align3d_forward_kernel(const T *feat,
       }
     }
   }
-  for (int iz = 0; inb && (q.gd > 2 || q.gh > 2 || q.gw > 2) && iz < q.gd; ++iz) {
+  bool wide = inb && (q.gd > 2 || q.gh > 2 || q.gw > 2);
+  if (wide) {
+    // larger grids: separable too when every axis has at most kSepTaps distinct taps (the same
+    // loop over taps, z and y taps consumed by shifting the lists)
+    AxisTaps8 tz = bin_taps_n<kSepTaps>(q.sd, pd, q.bd, q.gd, D, order);
+    AxisTaps8 ty = bin_taps_n<kSepTaps>(q.sh, ph, q.bh, q.gh, H, order);
+    const AxisTaps8 tx = bin_taps_n<kSepTaps>(q.sw, pw, q.bw, q.gw, W, order);
+    if (!tz.over && !ty.over && !tx.over) {
+      wide = false;
+      for (; tz.n > 0; tz.shift()) {
+        AxisTaps8 tyc = ty;
+        for (; tyc.n > 0; tyc.shift()) {
+          const float wzy = tz.w[0] * tyc.w[0];
+          const int64_t rowo = ((int64_t)tz.pos[0] * H + tyc.pos[0]) * W;
+#pragma unroll
+          for (int kx = 0; kx < kSepTaps; ++kx) {
+            if (kx >= tx.n) break;
+            const float wgt = wzy * tx.w[kx];
+#pragma unroll
+            for (int c = 0; c < CPT; ++c) acc[c] = acc[c] + wgt * to_f(base[(int64_t)c * vol + rowo + tx.pos[kx]]);
+          }
+        }
+      }
+    }
+  }
+  for (int iz = 0; wide && iz < q.gd; ++iz) {
     const float z = sample_coord(q.sd, pd, q.bd, iz, q.gd);
     for (int iy = 0; iy < q.gh; ++iy) {
       const float y = sample_coord(q.sh, ph, q.bh, iy, q.gh);
@@ -275,6 +323,7 @@ __device__ __forceinline__ AxisTap axis_tap(float c, int size, int order) {
 __device__ __forceinline__ AxisTaps4 bin_taps(float start, int p, float bin, int grid, int size, int order) {
   AxisTaps4 t;
   t.n = 0;
+  t.over = false;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     t.pos[k] = 0;
@@ -283,6 +332,26 @@ __device__ __forceinline__ AxisTaps4 bin_taps(float start, int p, float bin, int
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     if (i >= grid) break;
+    const AxisTap a = axis_tap(sample_coord(start, p, bin, i, grid), size, order);
+    if (!a.ok) continue;
+    t.add(a.i0, a.w0);
+    if (a.i1 != a.i0) t.add(a.i1, a.w1);
+  }
+  return t;
+}
+
+// The taps of bin p on one axis for any grid, up to NT of them (t.over beyond that).
+template <int NT>
+__device__ __forceinline__ AxisTaps<NT> bin_taps_n(float start, int p, float bin, int grid, int size, int order) {
+  AxisTaps<NT> t;
+  t.n = 0;
+  t.over = false;
+#pragma unroll
+  for (int k = 0; k < NT; ++k) {
+    t.pos[k] = 0;
+    t.w[k] = 0.f;
+  }
+  for (int i = 0; i < grid && !t.over; ++i) {
     const AxisTap a = axis_tap(sample_coord(start, p, bin, i, grid), size, order);
     if (!a.ok) continue;
     t.add(a.i0, a.w0);
@@ -755,7 +824,9 @@ inline void cl_split(int C, int PHW, int &bpb, int &parts) {
 
 inline bool cl_supported(int C) { return C > 0 && C % kClChannels == 0 && C / kClChannels <= 256; }
 
-template <typename T>
+// WIDE: compiled with the separable path for grids of more than 2 samples per axis (launched
+// when sampling_ratio is adaptive or above 2; without it the kernel needs fewer registers).
+template <typename T, bool WIDE>
 __global__ __launch_bounds__(256) void roi_align3d_forward_cl_kernel(const T *feat, const T *rois, T *out, int N, int C,
                                                                      int D, int H, int W, int PD, int PH, int PW,
                                                                      float scale, int sr, int order, int bpb, int parts,
@@ -780,6 +851,9 @@ __global__ __launch_bounds__(256) void roi_align3d_forward_cl_kernel(const T *fe
   const bool sep = q.gd <= 2 && q.gh <= 2 && q.gw <= 2;
   AxisTaps4 tz;
   if (inb && sep) tz = bin_taps(q.sd, pd, q.bd, q.gd, D, order);
+  AxisTaps8 tz8;   // larger grids: the z taps of plane pd, if they fit
+  tz8.over = true;
+  if (WIDE && inb && !sep) tz8 = bin_taps_n<kSepTaps>(q.sd, pd, q.bd, q.gd, D, order);
   for (int bin = slot; slot < slots && bin < nbin; bin += slots) {
     const int ph = (b0 + bin) / PW, pw = (b0 + bin) % PW;
     float acc[kClChannels];
@@ -808,7 +882,31 @@ __global__ __launch_bounds__(256) void roi_align3d_forward_cl_kernel(const T *fe
         }
       }
     }
-    for (int iz = 0; inb && !sep && iz < q.gd; ++iz) {
+    bool wide = inb && !sep;
+    if (WIDE && wide && !tz8.over) {
+      // separable too when every axis has at most kSepTaps taps (the NCDHW kernel's loop)
+      AxisTaps8 ty = bin_taps_n<kSepTaps>(q.sh, ph, q.bh, q.gh, H, order);
+      const AxisTaps8 tx = bin_taps_n<kSepTaps>(q.sw, pw, q.bw, q.gw, W, order);
+      if (!ty.over && !tx.over) {
+        wide = false;
+        for (AxisTaps8 tzc = tz8; tzc.n > 0; tzc.shift()) {
+          for (AxisTaps8 tyc = ty; tyc.n > 0; tyc.shift()) {
+            const float wzy = tzc.w[0] * tyc.w[0];
+            const uint32_t rowo = ((uint32_t)tzc.pos[0] * (uint32_t)H + (uint32_t)tyc.pos[0]) * (uint32_t)W;
+#pragma unroll
+            for (int kx = 0; kx < kSepTaps; ++kx) {
+              if (kx >= tx.n) break;
+              const float wgt = wzy * tx.w[kx];
+              float v[kClChannels];
+              load8(base + (rowo + (uint32_t)tx.pos[kx]) * (uint32_t)C, v);
+#pragma unroll
+              for (int c = 0; c < kClChannels; ++c) acc[c] = acc[c] + wgt * v[c];
+            }
+          }
+        }
+      }
+    }
+    for (int iz = 0; wide && iz < q.gd; ++iz) {
       const float z = sample_coord(q.sd, pd, q.bd, iz, q.gd);
       for (int iy = 0; iy < q.gh; ++iy) {
         const float y = sample_coord(q.sh, ph, q.bh, iy, q.gh);
@@ -928,9 +1026,14 @@ int forward_cl(const void *features_cl, const void *rois, void *output, int N, i
   const int64_t grid = (blocks + 7) / 8 * 8;   // a multiple of 8: the kernel maps blocks to XCDs
   if (grid >= ((int64_t)1 << 31)) return OPS3D_FDA_EINVAL;
   const size_t lds = (size_t)C * bpb * sizeof(T);
-  hipLaunchKernelGGL((roi_align3d_forward_cl_kernel<T>), dim3((unsigned)grid), dim3(256), lds, st,
-                     static_cast<const T *>(features_cl), static_cast<const T *>(rois), static_cast<T *>(output), N, C,
-                     D, H, W, PD, PH, PW, scale, sr, order, bpb, parts, (int)blocks);
+  if (sr > 0 && sr <= 2)   // every roi's grid is separable with 4 taps per axis
+    hipLaunchKernelGGL((roi_align3d_forward_cl_kernel<T, false>), dim3((unsigned)grid), dim3(256), lds, st,
+                       static_cast<const T *>(features_cl), static_cast<const T *>(rois), static_cast<T *>(output), N,
+                       C, D, H, W, PD, PH, PW, scale, sr, order, bpb, parts, (int)blocks);
+  else
+    hipLaunchKernelGGL((roi_align3d_forward_cl_kernel<T, true>), dim3((unsigned)grid), dim3(256), lds, st,
+                       static_cast<const T *>(features_cl), static_cast<const T *>(rois), static_cast<T *>(output), N,
+                       C, D, H, W, PD, PH, PW, scale, sr, order, bpb, parts, (int)blocks);
   return hipGetLastError() == hipSuccess ? OPS3D_FDA_OK : OPS3D_FDA_ERUNTIME;
 }
 

@@ -94,6 +94,8 @@ CASES = [
     (2, 130, (5, 9, 11), 8, (3, 2, 2), 1.0, 3, 0, torch.bfloat16),     # nearest, 130 channels
     (1, 5, (6, 7, 9), 6, (9, 8, 8), 1.0, 1, 1, torch.float32),          # 576 bins: atomic backward
     (1, 3, (6, 7, 9), 6, (2, 65, 2), 1.0, 1, 0, torch.bfloat16),        # 65 bins on y: atomic backward
+    (1, 6, (12, 14, 16), 10, (2, 3, 2), 1.0, 4, 1, torch.float32),      # 4 samples per axis: separable, 8 taps
+    (1, 5, (12, 14, 16), 10, (1, 2, 1), 1.0, 0, 1, torch.float32),      # adaptive, wide bins: > 8 taps
 ]
 
 
@@ -246,6 +248,8 @@ CL_CASES = [
     (1, 256, (6, 10, 12), 12, (3, 5, 6), 1.0, 2, 1, torch.float32),
     (2, 2048, (4, 4, 4), 6, (2, 3, 4), 1.0, 2, 1, torch.bfloat16),      # one bin per block
     (1, 40, (9, 10, 12), 150, (7, 7, 7), 1.0, 1, 1, torch.float32),     # many overlapping rois
+    (1, 16, (12, 14, 16), 30, (2, 3, 2), 1.0, 4, 1, torch.float32),     # 4 samples per axis (8-tap lists)
+    (2, 32, (12, 14, 16), 30, (1, 2, 1), 0.5, 0, 0, torch.bfloat16),    # adaptive: 8-tap lists and wider
 ]
 
 
