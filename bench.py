@@ -385,6 +385,34 @@ def measure_atomic_baseline(w, steps, warmup, device):
             "lds_ms": lds, "lds_bound_ms": adds / lds_rate * 1e3}
 
 
+def measure_gather_ceiling(device, sizes_mib=(2, 32, 512), groups=(4, 8, 32), blocks=4096, iters=256):
+    """Random-gather ceiling (libops3d_fda_bench.so): TB/s at which waves fetch randomly placed
+    blocks of 16 * group bytes (group lanes, one 16-byte load each) from buffers inside L2 (2
+    MiB), inside the MALL (32 MiB) and in HBM (512 MiB).  Group 8 is the sampling kernels'
+    128-byte x-pair line, group 4 a 64-byte row.  Median of 5 timed launches after one untimed."""
+    import torch
+
+    from ops3d_amd import _bench_lib
+
+    out = torch.empty(blocks * 256, dtype=torch.int32, device=device)
+    res = {}
+    for mib in sizes_mib:
+        src = torch.ones(mib << 18, dtype=torch.int32, device=device)   # mib MiB
+        for g in groups:
+            _bench_lib.gather(src, g, blocks, iters, out)
+            ts = []
+            for k in range(5):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                _bench_lib.gather(src, g, blocks, iters, out, seed=k + 2)
+                b.record()
+                torch.cuda.synchronize()
+                ts.append(a.elapsed_time(b))
+            res[(mib, g)] = blocks * 256 * iters * 16 / (statistics.median(ts) * 1e-3) / 1e12
+        del src
+    return res
+
+
 def measure(w, dtype, steps, warmup, device, with_kernels=True, fwd_only=False):
     b = Bench(w, dtype, device)
     res = {"workload": w.name, "dtype": dtype}
@@ -536,6 +564,8 @@ def main():
     ap.add_argument("--atomic-baseline", action="store_true",
                     help="only grad_value by the reference's fp32 atomic scatter against the library's "
                          "backward, at --config (stderr)")
+    ap.add_argument("--gather-ceiling", action="store_true",
+                    help="only the random-gather ceiling (TB/s for 64 to 512-byte blocks from L2, MALL, HBM)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB, 5 times (HBM counter calibration)")
     args = ap.parse_args()
@@ -565,6 +595,12 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         log(f"copied {args.copy_calibration} MiB 5 times")
+        return
+    if args.gather_ceiling:
+        o = measure_gather_ceiling(dev)
+        for mib in sorted({k[0] for k in o}):
+            log(f" random gather from a {mib:4d} MiB buffer | " +
+                " | ".join(f"{16 * g:4d}-byte blocks {o[(mib, g)]:6.2f} TB/s" for g in sorted({k[1] for k in o})))
         return
     if args.dcn or args.all:
         o = measure_dcnv4(args.steps, args.warmup, dev)

@@ -40,6 +40,17 @@ OPS3D_FDA_BENCH_API int ops3d_fda_bench_ref_scatter(const int64_t *spatial_shape
  */
 OPS3D_FDA_BENCH_API int ops3d_fda_bench_lds_atomic(float *out, int blocks, int iters, int pattern, void *stream);
 
+/*
+ * Random-gather ceiling probe: `blocks` blocks of 256 threads; every group of `group` lanes (4, 8,
+ * 32 or 64) fetches `iters` pseudo-random blocks of 16 * group contiguous bytes (one 16-byte load
+ * per lane) from src[0, bytes) (16-byte aligned); out[thread] receives a fold of what the thread
+ * loaded.  Bytes fetched = blocks * 256 * iters * 16.  The rate against the buffer size (inside
+ * L2, inside the MALL, in HBM) is the ceiling for the sampling kernels' random corner-row
+ * gathers (group 8: 128-byte x-pair lines; group 4: 64-byte rows).
+ */
+OPS3D_FDA_BENCH_API int ops3d_fda_bench_gather(const void *src, size_t bytes, int group, int blocks, int iters,
+                                               uint32_t *out, unsigned seed, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

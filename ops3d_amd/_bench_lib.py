@@ -26,6 +26,8 @@ def load() -> ctypes.CDLL:
         lib.ops3d_fda_bench_ref_scatter.argtypes = [vp] * 5 + [i] * 8 + [vp]
         lib.ops3d_fda_bench_lds_atomic.restype = i
         lib.ops3d_fda_bench_lds_atomic.argtypes = [vp, i, i, i, vp]
+        lib.ops3d_fda_bench_gather.restype = i
+        lib.ops3d_fda_bench_gather.argtypes = [vp, ctypes.c_size_t, i, i, i, vp, ctypes.c_uint, vp]
         _lib = lib
     return _lib
 
@@ -48,6 +50,15 @@ def ref_scatter(value, spatial_shapes, level_start_index, sampling_loc_attn, gra
             grad_output.data_ptr(), gv.data_ptr(), _DT[value.dtype], B, S, G, D, L, Q, int(K),
             torch.cuda.current_stream(value.device).cuda_stream))
     return gv
+
+
+def gather(src: torch.Tensor, group: int, blocks: int, iters: int, out: torch.Tensor, seed: int = 1) -> None:
+    """Launch the random-gather probe over the bytes of `src` (out: int32 device tensor of at
+    least blocks * 256 elements)."""
+    lib = load()
+    _check(lib.ops3d_fda_bench_gather(src.data_ptr(), src.numel() * src.element_size(), int(group), int(blocks),
+                                      int(iters), out.data_ptr(), int(seed),
+                                      torch.cuda.current_stream(src.device).cuda_stream))
 
 
 def lds_atomic(out: torch.Tensor, blocks: int, iters: int, pattern: int) -> None:

@@ -12,6 +12,11 @@
 //    lanes per (b, q, g) unit.
 // 2. The LDS float-atomic rate (ds_add_f32, no return), the bound of any scheme that pre-combines
 //    grad_value contributions with LDS atomics before writing them.
+// 3. The random-gather ceiling: the rate at which waves fetch randomly placed blocks of
+//    16 * G contiguous bytes (G lanes, one 16-byte load each) from a buffer of a given size, the
+//    access pattern of the sampling kernels' corner rows (G = 8: one 128-byte x-pair line; G = 4:
+//    a 64-byte row).  With the buffer inside L2, inside the MALL or in HBM it gives the ceiling
+//    each kind of miss allows.
 #include "fda_device.h"
 
 #include "../../include/ops3d_fda_bench.h"
@@ -95,6 +100,23 @@ __global__ __launch_bounds__(256) void lds_add_kernel(float *out, int iters, flo
   }
 }
 
+// Every group of G lanes fetches `iters` random blocks (a hash of its group index and the
+// iteration) and folds them into one word per thread, so nothing is optimised away.
+template <int G>
+__global__ __launch_bounds__(256) void gather_probe_kernel(const uint4 *src, uint32_t nblk, int iters, uint32_t *out,
+                                                           uint32_t seed) {
+  const int sub = (int)(threadIdx.x & 63) % G;
+  uint32_t h = (blockIdx.x * 256u + threadIdx.x) / G * 2654435761u + seed;
+  uint32_t acc = 0;
+  for (int i = 0; i < iters; ++i) {
+    h = h * 1664525u + 1013904223u;
+    const uint32_t b = (h >> 7) % nblk;
+    const uint4 v = src[(size_t)b * G + sub];
+    acc += v.x ^ v.y ^ v.z ^ v.w;
+  }
+  out[blockIdx.x * 256u + threadIdx.x] = acc;
+}
+
 thread_local char g_err[256] = "";
 
 int bench_fail(int code, const char *msg) {
@@ -149,6 +171,26 @@ int ops3d_fda_bench_ref_scatter(const int64_t *spatial_shapes, const int64_t *le
   if (dtype == 0) hipLaunchKernelGGL(ref_layout_scatter_kernel<float>, dim3(grid), dim3(kBenchBlock), lds, st, a);
   else if (dtype == 1) hipLaunchKernelGGL(ref_layout_scatter_kernel<_Float16>, dim3(grid), dim3(kBenchBlock), lds, st, a);
   else hipLaunchKernelGGL(ref_layout_scatter_kernel<__bf16>, dim3(grid), dim3(kBenchBlock), lds, st, a);
+  return hipGetLastError() == hipSuccess ? 0 : bench_fail(2, "launch failed");
+}
+
+int ops3d_fda_bench_gather(const void *src, size_t bytes, int group, int blocks, int iters, uint32_t *out,
+                           unsigned seed, void *stream) {
+  g_err[0] = 0;
+  if (!src || !out || blocks < 1 || iters < 1 || (reinterpret_cast<uintptr_t>(src) & 15u))
+    return bench_fail(1, "invalid arguments");
+  if (group != 4 && group != 8 && group != 32 && group != 64) return bench_fail(1, "group must be 4, 8, 32 or 64");
+  const size_t nblk = bytes / (16 * (size_t)group);
+  if (nblk < 1 || nblk > 0xffffffffu) return bench_fail(1, "buffer size out of range");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint4 *s = static_cast<const uint4 *>(src);
+  const uint32_t nb = (uint32_t)nblk;
+  switch (group) {
+    case 4: hipLaunchKernelGGL(gather_probe_kernel<4>, dim3(blocks), dim3(256), 0, st, s, nb, iters, out, seed); break;
+    case 8: hipLaunchKernelGGL(gather_probe_kernel<8>, dim3(blocks), dim3(256), 0, st, s, nb, iters, out, seed); break;
+    case 32: hipLaunchKernelGGL(gather_probe_kernel<32>, dim3(blocks), dim3(256), 0, st, s, nb, iters, out, seed); break;
+    default: hipLaunchKernelGGL(gather_probe_kernel<64>, dim3(blocks), dim3(256), 0, st, s, nb, iters, out, seed); break;
+  }
   return hipGetLastError() == hipSuccess ? 0 : bench_fail(2, "launch failed");
 }
 

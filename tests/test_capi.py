@@ -45,7 +45,7 @@ def test_bench_library_exports_every_declared_symbol():
         pytest.skip("libops3d_fda_bench.so not built")
     text = open(os.path.join(ROOT, "include", "ops3d_fda_bench.h")).read()
     names = sorted(set(re.findall(r"OPS3D_FDA_BENCH_API\s+[\w\s\*]*?\b(ops3d_\w+)\s*\(", text)))
-    assert len(names) == 3
+    assert len(names) == 4
     blib = _bench_lib.load()
     for name in names:
         assert hasattr(blib, name), name
@@ -195,4 +195,10 @@ def test_bench_library_argument_errors_before_device_work():
     assert call(dtype=7) == 1
     assert call() == 1 and b"NULL" in blib.ops3d_fda_bench_last_error()
     assert blib.ops3d_fda_bench_lds_atomic(None, 1, 1, 0, None) == 1
+    g = blib.ops3d_fda_bench_gather
+    assert g(None, 1 << 20, 8, 1, 1, None, 1, None) == 1                      # NULL buffers
+    # (the calls below pass stand-in pointers: each is refused before any launch)
+    assert g(16, 1 << 20, 5, 1, 1, 16, 1, None) == 1 and b"group" in blib.ops3d_fda_bench_last_error()
+    assert g(16, 8, 8, 1, 1, 16, 1, None) == 1 and b"size" in blib.ops3d_fda_bench_last_error()
+    assert g(16, 1 << 20, 8, 0, 1, 16, 1, None) == 1
     assert not hasattr(_extension.load_library(), "ops3d_fda_scatter_baseline")

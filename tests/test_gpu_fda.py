@@ -400,3 +400,17 @@ def test_error_unsupported_channels(gpu_device):
     inp = random_inputs([(4, 4, 4)], 1, 8, 2, 20, 4, torch.bfloat16)
     with pytest.raises(ValueError, match="unsupported channels"):
         _apply(inp, gpu_device)
+
+
+@pytest.mark.gpu
+def test_gather_ceiling_probe(gpu_device):
+    """The measurement library's random-gather probe runs and folds what it loads: a buffer of
+    ones gives every thread the fold of its loads (iters * (1 ^ 1 ^ 1 ^ 1) = 0)."""
+    from ops3d_amd import _bench_lib
+
+    src = torch.ones(1 << 18, dtype=torch.int32, device=gpu_device)
+    out = torch.full((8 * 256,), 7, dtype=torch.int32, device=gpu_device)
+    for g in (4, 8, 32, 64):
+        _bench_lib.gather(src, g, 8, 16, out)
+        torch.cuda.synchronize()
+        assert bool((out == 0).all())
