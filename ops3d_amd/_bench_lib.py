@@ -1,6 +1,6 @@
-"""ctypes binding of libops3d_fda_bench.so (include/ops3d_fda_bench.h): measurement baselines for
-the backward's value gradient, not part of the op.  Used by bench.py --atomic-baseline and its
-tests only."""
+"""ctypes binding of libops3d_fda_bench.so (include/ops3d_fda_bench.h): measurement baselines (the
+backward's value gradient by atomics, the LDS atomic rate, the random-gather ceiling), not part of
+the op.  Used by bench.py --atomic-baseline / --gather-ceiling and their tests only."""
 from __future__ import annotations
 
 import ctypes

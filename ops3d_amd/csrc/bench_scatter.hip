@@ -1,6 +1,6 @@
-// libops3d_fda_bench.so: measurement baselines for the backward's value gradient, gfx950.  Not
-// part of the op (libops3d_fda.so) and not used by it; bench.py --atomic-baseline and its GPU
-// test load it.
+// libops3d_fda_bench.so: measurement baselines, gfx950 (the backward's value gradient by atomics,
+// the LDS atomic rate, the random-gather ceiling).  Not part of the op (libops3d_fda.so) and not
+// used by it; bench.py --atomic-baseline / --gather-ceiling and their GPU tests load it.
 //
 // 1. The reference's grad_value scheme, at the reference's own lane layout.  The reference's
 //    backward (csrc/cuda/flash_deform_col2im_cuda.cuh:248-429, backward_kernel_warp_primitive,
