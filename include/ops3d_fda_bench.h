@@ -1,7 +1,8 @@
 /*
  * ops3d_fda_bench.h -- C ABI of libops3d_fda_bench.so: measurement baselines on gfx950 (the
- * backward's value gradient by atomics, the LDS atomic rate, the random-gather ceiling).  Not part of the op: nothing in libops3d_fda.so calls these, and
- * they replace no reference entry point.  Return codes: 0 ok, 1 bad argument, 2 HIP failure
+ * backward's value gradient by atomics, the LDS atomic rate, the random-gather ceiling).  Not
+ * part of the op: nothing in libops3d_fda.so calls these, and they replace no reference entry
+ * point.  Return codes: 0 ok, 1 bad argument, 2 HIP failure
  * (message: ops3d_fda_bench_last_error()).  Pointers are device memory; `stream` a hipStream_t.
  */
 #ifndef OPS3D_FDA_BENCH_H
