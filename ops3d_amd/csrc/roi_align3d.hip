@@ -834,7 +834,7 @@ __global__ __launch_bounds__(256) void roi_align3d_forward_cl_kernel(const T *fe
 #pragma clang fp contract(off)
   extern __shared__ __align__(16) unsigned char cl_lds[];
   T *res = reinterpret_cast<T *>(cl_lds);   // [C][bpb]
-  // block i runs on XCD i % 8: XCD x takes the x-th eighth of the (roi, pd, row) blocks, so a
+  // block i runs on XCD i % 8: XCD x takes the x-th eighth of the (roi, pd, part) blocks, so a
   // roi's blocks share one L2 (gridDim.x is a multiple of 8; nblk blocks are real)
   const unsigned blk = (blockIdx.x & 7u) * (gridDim.x / 8u) + (blockIdx.x >> 3);
   if (blk >= (unsigned)nblk) return;
