@@ -262,7 +262,7 @@ int bwd_layout(int B, int S, int G, int D, int e, int lpu, int L, int Q, int K, 
   ly.off_cursor = o; o += t4;
   ly.off_queue = o; o += 256;
   {
-    const uint64_t tvox = (uint64_t)(2 * tile_threads(lpu) / lpu);   // voxels of a nominal tile
+    const uint64_t tvox = (uint64_t)(2 * tile_threads(lpu, big_tiles(S, lpu)) / lpu);   // voxels of a nominal tile
     const uint64_t lb = (uint64_t)B * G * ((uint64_t)S + tvox - 1) / tvox;
     ly.split_slots = (S > 0 && lb < kSplitTiles) ? (uint32_t)kSplitSlots : 0u;
     ly.off_split = o; o += align256((size_t)ly.split_slots * tvox * D * 4);
@@ -278,10 +278,10 @@ int bwd_layout(int B, int S, int G, int D, int e, int lpu, int L, int Q, int K, 
 // Entries per LDS chunk of the tile kernel: as many as fit next to the bin arrays in the
 // block's share of the CU's 160 KB of LDS (1024 threads: one block per CU; 512: two; 256:
 // three), so that one block stages its next chunk while the others compute.
-int tile_chunk(int D, int e, int lpu) {
+int tile_chunk(int D, int e, int lpu, bool big) {
   const int rb = D * e;
-  const int nt = tile_threads(lpu);
-  const size_t bins = tile_kernel_lds_bytes(0, rb, lpu);
+  const int nt = tile_threads(lpu, big);
+  const size_t bins = tile_kernel_lds_bytes(0, rb, lpu, big);
   const size_t budget = (nt >= 1024 ? 150 : (nt >= 512 ? 76 : 50)) * (size_t)1024;
   if (budget <= bins) return 0;
   int ch = (int)((budget - bins) / (size_t)(rb + 20));
@@ -618,7 +618,11 @@ static int backward_impl(const void *value, const void *value_head_major, const 
   a.count_clear_wcap = tile_window(ly.tcap);   // the query kernel clears the counters (atomic mode)
   a.split_scratch = reinterpret_cast<float *>(ws + ly.off_split);
   a.split_slots = ly.split_slots;
-  tile_dims(tile_lanes(geo.lpu, geo.cpl * elem_size(dtype)), a.TX, a.TY, a.TZ);
+  {
+    const int tl = tile_lanes(geo.lpu, geo.cpl * elem_size(dtype));
+    a.big_tiles = big_tiles(spatial_size, tl) ? 1 : 0;
+    tile_dims(tl, a.TX, a.TY, a.TZ, a.big_tiles != 0);
+  }
   a.inv_lk = 1.0 / (double)(num_levels * num_point);
   hipError_t e;
   prof_mark(0, st);
@@ -662,9 +666,10 @@ static int backward_impl(const void *value, const void *value_head_major, const 
     g3.a.out = grad_value;
     g3.a.accumulate = out_f32_accumulate ? 1 : 0;
     g3.a.tile_affinity = num_heads % 8 == 0;
-    g3.a.chunk = tile_chunk(channels, elem_size(dtype), tile_lanes(geo.lpu, geo.cpl * elem_size(dtype)));
+    g3.a.chunk = tile_chunk(channels, elem_size(dtype), tile_lanes(geo.lpu, geo.cpl * elem_size(dtype)),
+                            a.big_tiles != 0);
     g3.lds = tile_kernel_lds_bytes(g3.a.chunk, channels * elem_size(dtype),
-                                   tile_lanes(geo.lpu, geo.cpl * elem_size(dtype)));
+                                   tile_lanes(geo.lpu, geo.cpl * elem_size(dtype)), a.big_tiles != 0);
     g3.grid = (unsigned)device_cus();   // times the resident blocks per CU (launch_one)
     if (g3.a.tile_affinity) g3.grid = (g3.grid + 7) & ~7u;
     if (g3.a.chunk < 64 || g3.lds > 160 * 1024)

@@ -72,6 +72,7 @@ struct Args {
   int chunk;                  // entries per LDS chunk of the tile kernel
   int tile_affinity;          // tiles of head g run on XCD g % 8 (G % 8 == 0)
   int accumulate;             // add into an fp32 grad_value instead of overwriting
+  int big_tiles;              // tile kernel with tile_threads(lpu, true) threads (big_tiles())
   int vhm;                    // value is head-major [B,G,S,D] (a transposed copy)
   int pair_levels;            // head-major copy in which large levels may be paired (copy_level);
                               // 0: every level at its level_start_index, heads S rows apart
@@ -715,10 +716,17 @@ __device__ __forceinline__ uint32_t sample_index(int b, int g, int q, int s, int
 // max(z0,0)), and additionally in the next tile along each axis on which its base corner is the
 // home tile's last voxel (its upper corner then lies in that tile): 1 to 8 entries per sample.
 // Threads of a tile-kernel block for `lpu` lanes per x-pair: 64 * lpu, at least 256 and at
-// most 1024, so tiles hold 128 voxels (512/lpu for lpu < 4, 64 for lpu = 32).
-__host__ __device__ constexpr int tile_threads(int lpu) {
-  return lpu <= 4 ? 256 : (lpu >= 16 ? 1024 : 64 * lpu);
+// most 1024, so tiles hold 128 voxels (512/lpu for lpu < 4, 64 for lpu = 32).  `big` (lpu 4,
+// large volumes): 512 threads and 256-voxel tiles, fewer entries per sample (a sample is
+// listed in a neighbour tile only when its base corner is on the tile's last plane).
+__host__ __device__ constexpr int tile_threads(int lpu, bool big = false) {
+  return big && lpu == 4 ? 512 : (lpu <= 4 ? 256 : (lpu >= 16 ? 1024 : 64 * lpu));
 }
+// Volumes of at least kBigTileVoxels voxels per batch item take the big tiles: c5 (598 016
+// voxels) tile kernel 2836 -> 2728 us and scatter 544 -> 472 us with them, c4 (73 728) tile
+// kernel 228 -> 249 us.
+constexpr int kBigTileVoxels = 1 << 18;
+__host__ __device__ constexpr bool big_tiles(int S, int lpu) { return lpu == 4 && S >= kBigTileVoxels; }
 constexpr int kTileKPT = 2;   // entries per thread and chunk (chunk <= KPT * threads)
 constexpr uint32_t kKeyInvalid = 0xffffffffu;
 
@@ -731,8 +739,8 @@ __host__ __device__ constexpr int tile_lanes(int lpu, int lane_bytes) { return (
 // Nominal tile dimensions for the tile kernel: its tile_threads(lpu) threads own x-pairs of
 // voxels, lpu lanes each, so a tile has 2 * tile_threads(lpu) / lpu voxels, as cubic as powers
 // of two allow (x even).
-__host__ __device__ constexpr void tile_dims(int lpu, int &tx, int &ty, int &tz) {
-  int v = 2 * tile_threads(lpu) / lpu, lg = 0;
+__host__ __device__ constexpr void tile_dims(int lpu, int &tx, int &ty, int &tz, bool big = false) {
+  int v = 2 * tile_threads(lpu, big) / lpu, lg = 0;
   while ((1 << lg) < v) ++lg;
   // split lg bits over (x, y, z): x gets the extra bit first, then y
   const int bz = lg / 3, by = (lg - bz) / 2, bx = lg - bz - by;
@@ -743,9 +751,9 @@ __host__ __device__ constexpr void tile_dims(int lpu, int &tx, int &ty, int &tz)
 
 // LDS bytes of fda_bwd_tile_kernel for `chunk` entries of row_bytes each, `lpu` tile lanes
 // per x-pair (host side).
-inline size_t tile_kernel_lds_bytes(int chunk, int row_bytes, int lpu) {
+inline size_t tile_kernel_lds_bytes(int chunk, int row_bytes, int lpu, bool big = false) {
   int tx, ty, tz;
-  tile_dims(lpu, tx, ty, tz);
+  tile_dims(lpu, tx, ty, tz, big);
   const size_t nb = (size_t)(tx + 1) * (ty + 1) * (tz + 1);
   return (size_t)chunk * (16 + (size_t)row_bytes + 4) + (2 * nb + 1) * 4;
 }

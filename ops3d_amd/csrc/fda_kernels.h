@@ -693,14 +693,14 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
 // Waves per SIMD the tile kernel runs at: its LDS chunk sizing puts three 256-thread blocks, two
 // 512-thread blocks or one 1024-thread block on a CU (3, 4, 4 waves per SIMD); compiling for no
 // more than that leaves the register allocator all the registers those waves can have.
-__host__ __device__ constexpr int tile_wpe(int lpu) {
-  return tile_threads(lpu) == 256 ? 3 : 4;
+__host__ __device__ constexpr int tile_wpe(int lpu, bool big) {
+  return tile_threads(lpu, big) == 256 ? 3 : 4;
 }
 
-template <typename T, int CPL, int LPU>
-__global__ __launch_bounds__(tile_threads(LPU)) __attribute__((amdgpu_waves_per_eu(tile_wpe(LPU))))
+template <typename T, int CPL, int LPU, bool BIG>
+__global__ __launch_bounds__(tile_threads(LPU, BIG)) __attribute__((amdgpu_waves_per_eu(tile_wpe(LPU, BIG))))
 void fda_bwd_tile_kernel(const Args a) {
-  constexpr int NT = tile_threads(LPU);
+  constexpr int NT = tile_threads(LPU, BIG);
   extern __shared__ __align__(16) unsigned char tsm[];
   constexpr int EB = CPL * (int)sizeof(T);      // bytes of a lane's channels
   constexpr int NW = EB / 4;
@@ -1109,9 +1109,9 @@ void fda_bwd_tile_kernel(const Args a) {
 // Split tiles (see the tile kernel): one block per tile of every group adds the F parts'
 // partial sums of each of its voxels and writes the rows (in T, or added to the caller's fp32
 // buffer).  Runs after the tile kernel, so plain loads see the parts; exits when F == 1.
-template <typename T, int CPL, int LPU>
-__global__ __launch_bounds__(tile_threads(LPU)) void fda_bwd_split_combine_kernel(const Args a) {
-  constexpr int NT = tile_threads(LPU);
+template <typename T, int CPL, int LPU, bool BIG>
+__global__ __launch_bounds__(tile_threads(LPU, BIG)) void fda_bwd_split_combine_kernel(const Args a) {
+  constexpr int NT = tile_threads(LPU, BIG);
   constexpr int kTileVox = 2 * (NT / LPU);
   const uint32_t F = a.tile_queue[8];
   if (F <= 1) return;
@@ -1217,19 +1217,27 @@ hipError_t launch_one(int which, const Args &a, unsigned grid, size_t lds, hipSt
   else if (which == 3) {
     // one block per tile of every group (`grid` = the bound on tiles times the groups)
     constexpr int TL = tile_lanes(LPU, CPL * (int)sizeof(T)), TC = CPL * LPU / TL;
-    hipLaunchKernelGGL((fda_bwd_split_combine_kernel<T, TC, TL>), dim3(grid), dim3(tile_threads(TL)), 0, st, a);
+    if (a.big_tiles)
+      hipLaunchKernelGGL((fda_bwd_split_combine_kernel<T, TC, TL, true>), dim3(grid), dim3(tile_threads(TL, true)), 0,
+                         st, a);
+    else
+      hipLaunchKernelGGL((fda_bwd_split_combine_kernel<T, TC, TL, false>), dim3(grid), dim3(tile_threads(TL)), 0, st,
+                         a);
   }
   else {
     // persistent: `grid` (the CU count, a multiple of 8 with XCD affinity) times the blocks that
     // fit on a CU at once
     // tile lanes per x-pair: half of LPU, twice the channels per lane
     constexpr int TL = tile_lanes(LPU, CPL * (int)sizeof(T)), TC = CPL * LPU / TL;
-    int occ = 1;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fda_bwd_tile_kernel<T, TC, TL>, tile_threads(TL), lds) !=
-            hipSuccess || occ < 1)
-      occ = 1;
-    hipLaunchKernelGGL((fda_bwd_tile_kernel<T, TC, TL>), dim3(grid * (unsigned)occ), dim3(tile_threads(TL)), lds, st,
-                       a);
+    const auto run = [&](auto kern, int nt) {
+      int occ = 1;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, nt, lds) != hipSuccess || occ < 1) occ = 1;
+      hipLaunchKernelGGL(kern, dim3(grid * (unsigned)occ), dim3(nt), lds, st, a);
+    };
+    if (a.big_tiles)
+      run(fda_bwd_tile_kernel<T, TC, TL, true>, tile_threads(TL, true));
+    else
+      run(fda_bwd_tile_kernel<T, TC, TL, false>, tile_threads(TL));
   }
   return hipGetLastError();
 }
