@@ -35,14 +35,16 @@ def level_tiles(shape, nominal):
     return t, nt, nt[0] * nt[1] * nt[2]
 
 
-def tile_threads(lpu):
+def tile_threads(lpu, big=False):
     """fda_device.h tile_threads."""
+    if big and lpu == 4:
+        return 512
     return 256 if lpu <= 4 else (1024 if lpu >= 16 else 64 * lpu)
 
 
-def tile_dims(lpu):
+def tile_dims(lpu, big=False):
     """fda_device.h tile_dims -> (tx, ty, tz)."""
-    v, lg = 2 * tile_threads(lpu) // lpu, 0
+    v, lg = 2 * tile_threads(lpu, big) // lpu, 0
     while (1 << lg) < v:
         lg += 1
     bz = lg // 3
@@ -182,7 +184,7 @@ CASES = [
     ([(2, 2, 2), (4, 3, 1)], 2, 6, 1, 8),
     ([(5, 6, 9)], 1, 20, 2, 4),
 ]
-TILES = [(2, 1, 1), (4, 2, 2), (8, 4, 4), (8, 8, 8)]
+TILES = [(2, 1, 1), (4, 2, 2), (8, 4, 4), (8, 8, 4), (8, 8, 8)]   # (8, 8, 4): the big tiles of LPU 4
 
 
 @pytest.mark.parametrize("tiles", TILES)
@@ -200,10 +202,11 @@ def test_tile_index_emulation_matches_oracle(shapes, B, Q, G, K, tiles):
     np.testing.assert_allclose(gv, ref, rtol=1e-9, atol=1e-11)
 
 
-@pytest.mark.parametrize("lpu", [1, 2, 4, 8, 16, 32])
-def test_tile_dims_fill_the_block(lpu):
-    tx, ty, tz = tile_dims(lpu)
-    threads = tile_threads(lpu)
+@pytest.mark.parametrize("lpu,big", [(1, False), (2, False), (4, False), (4, True), (8, False), (16, False),
+                                     (32, False)])
+def test_tile_dims_fill_the_block(lpu, big):
+    tx, ty, tz = tile_dims(lpu, big)
+    threads = tile_threads(lpu, big)
     assert threads % 64 == 0 and 256 <= threads <= 1024
     assert tx % 2 == 0
     assert (tx // 2) * ty * tz * lpu == threads   # one x-pair per LPU lanes
