@@ -29,7 +29,7 @@ namespace ops3d_fda {
 hipError_t launch_f32(int, int, int, const Args &, unsigned, size_t, hipStream_t);
 hipError_t launch_f16(int, int, int, const Args &, unsigned, size_t, hipStream_t);
 hipError_t launch_bf16(int, int, int, const Args &, unsigned, size_t, hipStream_t);
-hipError_t launch_tile_bucketing(const uint32_t *keys, const uint32_t *words, uint32_t n, uint32_t per_head,
+hipError_t launch_tile_bucketing(const uint32_t *keys, uint32_t n, uint32_t per_head,
                                  const int64_t *shapes, int L, int BG, int TX, int TY, int TZ, uint32_t *counts,
                                  uint32_t *start, uint32_t *cursor, uint32_t *mat, uint32_t tcap, uint32_t *entries, uint32_t *queue,
                                  bool counts_cleared, hipStream_t st, void (*mark)(int, hipStream_t));
@@ -236,7 +236,7 @@ bool grad_out_copied(int B, int Q, int G, int D, int e) {
 struct BwdLayout {
   uint64_t n, ntiles_bound;
   uint32_t tcap, split_slots;
-  size_t off_keys, off_words, off_stash, off_entries, off_counts, off_start, off_cursor, off_queue, off_split,
+  size_t off_keys, off_stash, off_entries, off_counts, off_start, off_cursor, off_queue, off_split,
       off_mat, off_vhm, off_ghm;
   size_t total;
 };
@@ -250,11 +250,12 @@ int bwd_layout(int B, int S, int G, int D, int e, int lpu, int L, int Q, int K, 
   if (ly.n >= 0x1fffffffull || ly.ntiles_bound >= 0xfffffff0ull)
     return fail(OPS3D_FDA_EINVAL, "backward too large for 32-bit sample/tile indices (N=%llu, tiles<=%llu)",
                 (unsigned long long)ly.n, (unsigned long long)ly.ntiles_bound);
+  if ((uint64_t)S >= (1ull << 26) - 1)   // tile ids within a head in 26 bits (tile_key)
+    return fail(OPS3D_FDA_EINVAL, "backward too large: %d voxels per batch item (at most 2^26 - 2)", S);
   size_t o = 0;
   const size_t n4 = align256(ly.n * 4);
   const size_t t4 = align256((ly.ntiles_bound + 1) * 4);
   ly.off_keys = o; o += n4;
-  ly.off_words = o; o += n4;
   ly.off_stash = o; o += align256(ly.n * 16);
   ly.off_entries = o; o += align256(ly.n * 8 * 4);
   ly.off_counts = o; o += t4;
@@ -589,7 +590,6 @@ static int backward_impl(const void *value, const void *value_head_major, const 
 
   char *ws = static_cast<char *>(workspace);
   uint32_t *keys = reinterpret_cast<uint32_t *>(ws + ly.off_keys);
-  uint32_t *words = reinterpret_cast<uint32_t *>(ws + ly.off_words);
   float4 *stash = reinterpret_cast<float4 *>(ws + ly.off_stash);
   uint32_t *entries = reinterpret_cast<uint32_t *>(ws + ly.off_entries);
   uint32_t *counts = reinterpret_cast<uint32_t *>(ws + ly.off_counts);
@@ -608,7 +608,6 @@ static int backward_impl(const void *value, const void *value_head_major, const 
   a.grad_out = grad_output;
   a.grad_loc_attn = grad_sampling_loc_attn;
   a.keys = keys;
-  a.vals = words;
   a.stash = stash;
   a.tile_counts = counts;
   a.tile_start = tstart;
@@ -652,7 +651,7 @@ static int backward_impl(const void *value, const void *value_head_major, const 
   prof_mark(2, st);
   // phase 2: entries grouped by tile (counters are cleared even without samples: the tile
   // kernel reads the tile ranges of every tile)
-  e = launch_tile_bucketing(keys, words, work ? (uint32_t)ly.n : 0u,
+  e = launch_tile_bucketing(keys, work ? (uint32_t)ly.n : 0u,
                             (uint32_t)num_query * (uint32_t)(num_levels * num_point), spatial_shapes, num_levels,
                             batch * num_heads, a.TX, a.TY, a.TZ, counts, tstart, cursor,
                             reinterpret_cast<uint32_t *>(ws + ly.off_mat), ly.tcap, entries,

@@ -55,8 +55,7 @@ struct Args {
   float *grad_value;          // [B,S,G,D] fp32 acc   (backward)
   void *grad_loc_attn;        // [B,Q,G,P] T          (backward)
   // backward, tile formulation of grad_value
-  uint32_t *keys;             // [N] home tile of each sample's base corner (kKeyInvalid if outside)
-  uint32_t *vals;             // [N] tile-local base corner word of each sample (tile_word)
+  uint32_t *keys;             // [N] bucketing key of each sample (tile_key; kKeyInvalid if outside)
   float4 *stash;              // [N] (x, y, z, attn) of each sample: level pixel coordinates
   uint32_t *tile_counts;      // [B*G*T_h] entries per tile
   uint32_t *tile_start;       // [B*G*T_h] first entry of each tile (head base + exclusive scan)
@@ -802,11 +801,12 @@ __device__ __forceinline__ void clear_tile_counts(const Args &a) {
   for (uint32_t i = threadIdx.x; i < total; i += blockDim.x) a.tile_counts[i] = 0u;
 }
 
-// Tile-local word of an entry: base corner relative to the tile origin, each coordinate in
-// [-1, t) stored +1 in 5 bits (x bits 0-4, y 5-9, z 10-14); in a sample's home word also the
-// "next tile" flags (x bit 15, y 16, z 17) and the level (bits 18-20).
-__device__ __forceinline__ uint32_t tile_word(int lx, int ly, int lz) {
-  return (uint32_t)(lx + 1) | ((uint32_t)(ly + 1) << 5) | ((uint32_t)(lz + 1) << 10);
+// Bucketing key of a sample: its home tile's id within its head (bits 6 and up), the "next tile"
+// flags (x bit 3, y bit 4, z bit 5: the sample is also listed in the next tile along that axis)
+// and its level (bits 0-2); kKeyInvalid for a sample outside the volume.  A head has fewer than
+// 2^26 - 1 tiles (the host limits a level to 2^28 elements of G*D >= 8 channels).
+__device__ __forceinline__ uint32_t tile_key(uint32_t tile, uint32_t flags, uint32_t level) {
+  return (tile << 6) | (flags << 3) | level;
 }
 
 }  // namespace ops3d_fda

@@ -315,7 +315,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kQueryWa
   __shared__ int64_t head_rows;      // rows between heads of the head-major copy
   if (threadIdx.x == 0) {
     if (kPairs) head_rows = copy_levels(a.shapes, a.lsi, L, a.S, CPL * 4 * (int)sizeof(T), lvcopy);
-    uint32_t t = (uint32_t)(b * a.G + g) * tiles_per_head(a.shapes, L, a.TX, a.TY, a.TZ);
+    uint32_t t = 0;   // tile ids within the head
     for (int l = 0; l < L; ++l) {
       lvt[l] = level_tiles(a.shapes, l, a.TX, a.TY, a.TZ);
       lvbase[l] = t;
@@ -456,8 +456,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kQueryWa
         const uint32_t ex = lx == lt.t[2] - 1 && (hx + 1) * lt.t[2] < lt.n[2];
         const uint32_t ey = ly == lt.t[1] - 1 && (hy + 1) * lt.t[1] < lt.n[1];
         const uint32_t ez = lz == lt.t[0] - 1 && (hz + 1) * lt.t[0] < lt.n[0];
-        a.keys[gs0 + e] = bx == kKeyInvalid ? kKeyInvalid : lvbase[l] + (uint32_t)((hz * lt.nt[1] + hy) * lt.nt[2] + hx);
-        a.vals[gs0 + e] = tile_word(lx, ly, lz) | (ex << 15) | (ey << 16) | (ez << 17) | ((uint32_t)l << 18);
+        a.keys[gs0 + e] = bx == kKeyInvalid ? kKeyInvalid
+                                            : tile_key(lvbase[l] + (uint32_t)((hz * lt.nt[1] + hy) * lt.nt[2] + hx),
+                                                       ex | (ey << 1) | (ez << 2), (uint32_t)l);
         // pixel coordinates = base corner + fraction (exact), from which the tile kernel takes both
         const float4 fr = stx[ss];
         a.stash[gs0 + e] = make_float4((float)x0 + fr.x, (float)y0 + fr.y, (float)z0 + fr.z, fr.w);
@@ -505,7 +506,7 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
   __shared__ LevelTiles lvt[5];
   __shared__ uint32_t lvbase[5];
   if (threadIdx.x == 0) {
-    uint32_t t = (uint32_t)(b * a.G + g) * tiles_per_head(a.shapes, L, a.TX, a.TY, a.TZ);
+    uint32_t t = 0;   // tile ids within the head
     for (int l = 0; l < L; ++l) {
       lvt[l] = level_tiles(a.shapes, l, a.TX, a.TY, a.TZ);
       lvbase[l] = t;
@@ -646,8 +647,9 @@ __global__ __launch_bounds__(kBlock) void fda_bwd_query_kernel(const Args a) {
         const uint32_t ex = lx == lt.t[2] - 1 && (hx + 1) * lt.t[2] < lt.n[2];
         const uint32_t ey = ly == lt.t[1] - 1 && (hy + 1) * lt.t[1] < lt.n[1];
         const uint32_t ez = lz == lt.t[0] - 1 && (hz + 1) * lt.t[0] < lt.n[0];
-        a.keys[gs0 + e] = bx == kKeyInvalid ? kKeyInvalid : lvbase[l] + (uint32_t)((hz * lt.nt[1] + hy) * lt.nt[2] + hx);
-        a.vals[gs0 + e] = tile_word(lx, ly, lz) | (ex << 15) | (ey << 16) | (ez << 17) | ((uint32_t)l << 18);
+        a.keys[gs0 + e] = bx == kKeyInvalid ? kKeyInvalid
+                                            : tile_key(lvbase[l] + (uint32_t)((hz * lt.nt[1] + hy) * lt.nt[2] + hx),
+                                                       ex | (ey << 1) | (ez << 2), (uint32_t)l);
         // pixel coordinates = base corner + fraction (exact), from which the tile kernel takes both
         const float4 fr = stx[ss];
         a.stash[gs0 + e] = make_float4((float)x0 + fr.x, (float)y0 + fr.y, (float)z0 + fr.z, fr.w);

@@ -1,8 +1,8 @@
 // Phase 2 of the backward: group the samples' entries by spatial tile, gfx950.
 //
-// Every sample inside the volume has a home tile (key) and a tile-local word (fda_device.h,
-// tile_word); it is listed in its home tile and in the next tile along each axis whose flag is
-// set, 1 to 8 entries.  A block handles a contiguous range of one head's samples (about 64
+// Every sample inside the volume has a key (fda_device.h, tile_key: its home tile within its
+// head, "next tile" flags, level); it is listed in its home tile and in the next tile along each
+// axis whose flag is set, 1 to 8 entries.  A block handles a contiguous range of one head's samples (about 64
 // blocks per head) and keeps an LDS histogram over all of the head's tiles.
 //
 // Matrix mode (the head has at most wcap = min(tcap, kWin) tiles; tcap is what the workspace
@@ -36,8 +36,7 @@ constexpr int kBlocksPerHead = 64;
 constexpr uint32_t kFusedHeadSamples = 4096;          // heads this small take one fused block
 
 struct BucketArgs {
-  const uint32_t *keys;        // [N] home tile id or kKeyInvalid
-  const uint32_t *words;       // [N] home tile-local word (+ next-tile flags, level)
+  const uint32_t *keys;        // [N] tile_key of each sample or kKeyInvalid
   uint32_t n;                  // samples
   uint32_t per_head;           // samples per (b, g) = Q * L * K
   uint32_t chunk;              // samples per block (a block never spans two heads)
@@ -71,21 +70,19 @@ __device__ __forceinline__ void level_grids(const BucketArgs &a, LevelGrid *lg) 
   }
 }
 
-// Calls f(tile id, tile-local word) for each entry of sample (key, word): the home tile, then
-// each of the 7 neighbour combinations (x, y, z bits of c) whose flags are all set.  Straight-line
-// predicated calls: with 64 lanes every combination is taken by some lane, so a per-lane loop
-// would run all 8 rounds anyway, with loop control on top.
+// Calls f(tile id) for each entry of a sample of the head whose first tile id is w0, from its
+// key (tile_key): the home tile, then each of the 7 neighbour combinations (x, y, z bits of c)
+// whose flags are all set.  Straight-line predicated calls: with 64 lanes every combination is
+// taken by some lane, so a per-lane loop would run all 8 rounds anyway, with loop control on top.
 template <typename F>
-__device__ __forceinline__ void for_each_entry(uint32_t key, uint32_t word, const LevelGrid *lg, F &&f) {
-  const uint32_t fl = (word >> 15) & 7u;   // bit 0: next x tile, bit 1: y, bit 2: z
-  const LevelGrid g = lg[word >> 18];
-  const uint32_t base = word & 0x7fffu;
-  f(key, base);
+__device__ __forceinline__ void for_each_entry(uint32_t key, uint32_t w0, const LevelGrid *lg, F &&f) {
+  const uint32_t fl = (key >> 3) & 7u;   // bit 0: next x tile, bit 1: y, bit 2: z
+  const LevelGrid g = lg[key & 7u];
+  const uint32_t home = w0 + (key >> 6);
+  f(home);
   static_for<7>([&](auto cc) {
     constexpr uint32_t c = decltype(cc)::value + 1;
-    // in the next tile along an axis the base corner is at local -1 (stored as 0)
-    constexpr uint32_t keep = ~(((c & 1u) ? 0x1fu : 0u) | ((c & 2u) ? 0x1fu << 5 : 0u) | ((c & 4u) ? 0x1fu << 10 : 0u));
-    if ((fl & c) == c) f(key + (c & 1u) + ((c & 2u) ? g.sy : 0u) + ((c & 4u) ? g.sz : 0u), base & keep);
+    if ((fl & c) == c) f(home + (c & 1u) + ((c & 2u) ? g.sy : 0u) + ((c & 4u) ? g.sz : 0u));
   });
 }
 
@@ -135,17 +132,16 @@ __global__ __launch_bounds__(kBucketThreads) void tile_count_kernel(const Bucket
   // all_in (every tile of the head in the window) drops the global-atomic path from the code
   const auto count_all = [&](auto all_in) {
     for (uint32_t sb = s0 + threadIdx.x; sb < s1; sb += kCountBatch * kBucketThreads) {
-      uint32_t key[kCountBatch], word[kCountBatch];
+      uint32_t key[kCountBatch];
 #pragma unroll
       for (int i = 0; i < kCountBatch; ++i) {
         const uint32_t s = sb + (uint32_t)i * kBucketThreads;
         key[i] = s < s1 ? a.keys[s] : kKeyInvalid;
-        word[i] = s < s1 ? a.words[s] : 0u;
       }
 #pragma unroll
       for (int i = 0; i < kCountBatch; ++i) {
         if (key[i] == kKeyInvalid) continue;
-        for_each_entry(key[i], word[i], lg, [&](uint32_t id, uint32_t) {
+        for_each_entry(key[i], w0, lg, [&](uint32_t id) {
           if (decltype(all_in)::value || id - w0 < nw) atomicAdd(&win[id - w0], 1u);
           else atomicAdd(&a.counts[id], 1u);
         });
@@ -251,7 +247,7 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
     for (uint32_t s = s0 + tid; s < s1; s += kBucketThreads) {
       const uint32_t key = a.keys[s];
       if (key == kKeyInvalid) continue;
-      for_each_entry(key, a.words[s], lg, [&](uint32_t id, uint32_t) {
+      for_each_entry(key, w0, lg, [&](uint32_t id) {
         if (mat) atomicAdd(&cur[id - w0], 1u);
         else atomicAdd(&a.counts[id], 1u);   // zeroed by the query kernel
       });
@@ -313,7 +309,7 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
     for (uint32_t s = s0 + tid; s < s1; s += kBucketThreads) {
       const uint32_t key = a.keys[s];
       if (key == kKeyInvalid) continue;
-      for_each_entry(key, a.words[s], lg, [&](uint32_t id, uint32_t) {
+      for_each_entry(key, w0, lg, [&](uint32_t id) {
         if (id - w0 < nw) atomicAdd(&win[id - w0], 1u);
       });
     }
@@ -325,12 +321,11 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
   constexpr int SPT = kRound / kBucketThreads;
   const bool all_in = nw == T_h;   // no tile outside the window: no global-atomic path
   for (uint32_t r0 = s0; r0 < s1; r0 += kRound) {
-    uint32_t key[SPT], word[SPT];
+    uint32_t key[SPT];
 #pragma unroll
     for (int k = 0; k < SPT; ++k) {
       const uint32_t s = r0 + (uint32_t)(k * kBucketThreads + tid);
       key[k] = s < s1 ? a.keys[s] : kKeyInvalid;
-      word[k] = s < s1 ? a.words[s] : 0u;
     }
     // (a) the round's entries per tile; tiles outside the window take a position at once
     const auto count_round = [&](auto all_in) {
@@ -338,7 +333,7 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
       for (int k = 0; k < SPT; ++k) {
         if (key[k] == kKeyInvalid) continue;
         const uint32_t s = r0 + (uint32_t)(k * kBucketThreads + tid);
-        for_each_entry(key[k], word[k], lg, [&](uint32_t id, uint32_t) {
+        for_each_entry(key[k], w0, lg, [&](uint32_t id) {
           if (decltype(all_in)::value || id - w0 < nw) atomicAdd(&cur[id - w0], 1u);
           else a.entries[atomicAdd(&a.cursor[id], 1u)] = s;
         });
@@ -361,7 +356,7 @@ __global__ __launch_bounds__(kBucketThreads) void tile_scatter_kernel(const Buck
       for (int k = 0; k < SPT; ++k) {
         if (key[k] == kKeyInvalid) continue;
         const uint32_t so = (uint32_t)(k * kBucketThreads + tid);
-        for_each_entry(key[k], word[k], lg, [&](uint32_t id, uint32_t) {
+        for_each_entry(key[k], w0, lg, [&](uint32_t id) {
           const uint32_t t = id - w0;
           if (decltype(all_in)::value || t < nw) {
             const uint32_t slot = atomicAdd(&cur[t], 1u);
@@ -467,12 +462,12 @@ uint32_t tile_window(uint32_t tcap) { return tcap < (uint32_t)kWin ? (tcap > 0 ?
 // to tcap tiles.
 size_t tile_matrix_words(uint32_t BG, uint32_t tcap) { return (size_t)BG * kBlocksPerHead * tcap; }
 
-hipError_t launch_tile_bucketing(const uint32_t *keys, const uint32_t *words, uint32_t n, uint32_t per_head,
+hipError_t launch_tile_bucketing(const uint32_t *keys, uint32_t n, uint32_t per_head,
                                  const int64_t *shapes, int L, int BG, int TX, int TY, int TZ, uint32_t *counts,
                                  uint32_t *start, uint32_t *cursor, uint32_t *mat, uint32_t tcap, uint32_t *entries, uint32_t *queue,
                                  bool counts_cleared, hipStream_t st, void (*mark)(int, hipStream_t)) {
   BucketArgs a{};
-  a.keys = keys; a.words = words; a.n = n; a.per_head = per_head; a.shapes = shapes;
+  a.keys = keys; a.n = n; a.per_head = per_head; a.shapes = shapes;
   a.L = L; a.BG = BG; a.TX = TX; a.TY = TY; a.TZ = TZ;
   a.counts = counts; a.cursor = cursor; a.start = start; a.mat = mat; a.tcap = tcap; a.entries = entries; a.queue = queue;
   // LDS sized to what the matrix can hold (tiles past the window take the global-atomic path),

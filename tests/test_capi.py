@@ -99,7 +99,7 @@ def test_workspace_bytes(lib):
     # B*G*S/128 = 4608 tiles)
     def want(B, S, G, D, L, Q, K, split_slots, value_copy=True):
         n = B * Q * G * L * K
-        return (2 * al(4 * n) + al(16 * n) + al(32 * n) + 3 * al(4 * (B * G * S + 1)) + 256
+        return (al(4 * n) + al(16 * n) + al(32 * n) + 3 * al(4 * (B * G * S + 1)) + 256
                 + al(split_slots * 128 * D * 4)
                 + al(4 * B * G * 64 * (S // 16 + 64)) + (al(B * G * (2 * S + 10) * D * 2) if value_copy else 0) + (al(B * Q * G * D * 2) if B * Q * G * D * 2 > 64 << 20 else 0))
     assert lib.ops3d_fda_backward_workspace_bytes(2, B, S, G, D, L, Q, K) == want(B, S, G, D, L, Q, K, 0)
